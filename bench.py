@@ -1,0 +1,171 @@
+"""Benchmark: NN evals/s of the HIP backend on b18c384nbt fp16, 19x19, batch 256
+with inputs resident in HBM, called through the C
+ABI (kgh_forward_device); the matrix-core roofline of the 3x3 conv kernel
+measured with HIP events on the handle's stream over the timed steps; and the
+same-run CPU baseline (the oracle: a restatement of KataGo's Eigen backend).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import threading
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 matrix-core peak (datasheet)
+CFG_INDEX = 2              # b18c384nbt fp16 19x19 batch 256
+
+
+def conv_flops(layers, hw):
+    """Direct-convolution FLOPs per eval (2*k*k*Cin*Cout*HW per conv) split
+    into 3x3, 1x1 and the rest (other convs + matmuls, 2*in*out)."""
+    f3 = f1 = other = 0.0
+    for rec in layers:
+        if rec["op"] == 1:
+            ky, kx, ci, co = (int(v) for v in rec["i"][:4])
+            f = 2.0 * ky * kx * ci * co * hw
+            if ky == 3 and kx == 3:
+                f3 += f
+            elif ky == 1 and kx == 1:
+                f1 += f
+            else:
+                other += f
+        elif rec["op"] == 4:
+            other += 2.0 * int(rec["i"][0]) * int(rec["i"][1])
+    return f3, f1, other
+
+
+def cpu_baseline(path, seconds_target=15.0):
+    """The oracle (fp32 Eigen-algorithm restatement) on T host threads, each
+    running forwards of batch 8, as the reference's Eigen deployment runs one
+    single-threaded forward per server thread (eigenbackend.cpp:8-9)."""
+    from katago_amd import modelgen
+    from oracle import oracle
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(cores, 16))
+    om = oracle.OracleModel(path)
+    sp, gl = modelgen.synthetic_inputs(2000 + CFG_INDEX, 8)
+    t0 = time.perf_counter()
+    om.forward(sp[:1], gl[:1])
+    per_row = time.perf_counter() - t0
+    iters = int(max(1, min(4, seconds_target / max(per_row * 8, 1e-3))))
+    done = [0]
+    lock = threading.Lock()
+
+    def work():
+        for _ in range(iters):
+            om.forward(sp, gl)
+            with lock:
+                done[0] += 8
+
+    ths = [threading.Thread(target=work) for _ in range(threads)]
+    t0 = time.perf_counter()
+    for t in ths:
+        t.start()
+    for t in ths:
+        t.join()
+    wall = time.perf_counter() - t0
+    return {"value": round(done[0] / wall, 3), "unit": "evals/s", "cores": threads, "kind": "port",
+            "sample": f"b18c384nbt fp32, Eigen-algorithm restatement (oracle/eigen_oracle.cpp), {threads} threads x "
+                      f"{iters} forwards x batch 8 = {done[0]} evals in {wall:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--model-dir", default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU. Rows are independent and weights replicated, so N GPUs run N independent "
+              "handles with no communication; this build does not launch multi-GPU runs.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    from katago_amd import modelgen, nn
+
+    cfg = modelgen.configs()[CFG_INDEX]
+    batch, hw = cfg.batch, 19 * 19
+    model_dir = args.model_dir or os.path.join(tempfile.gettempdir(), "katago_amd_models")
+    path = modelgen.ensure_model(model_dir, cfg)
+    print(f"bench: model {path}", file=sys.stderr, flush=True)
+
+    lm = nn.LoadedModel(path)
+    dm = nn.DeviceModel(lm, use_fp16=cfg.fp16)
+    h = nn.DeviceHandle(dm, batch)
+    f3, f1, fother = conv_flops(dm.layers, hw)
+    flops_per_eval = f3 + f1 + fother
+
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, batch)
+    d_sp = nn.DeviceBuffer.from_array(sp)
+    d_gl = nn.DeviceBuffer.from_array(gl)
+    d_sym = nn.DeviceBuffer.from_array(np.zeros(batch, np.int32))
+    d_opt = nn.DeviceBuffer.from_array(np.zeros(batch, np.float32))
+    d_out = nn.DeviceBuffer(batch * h.row_floats * 4)
+    call = lambda: h.forward_device(batch, d_sp.ptr, d_gl.ptr, d_sym.ptr, d_opt.ptr, d_out.ptr)
+
+    for _ in range(args.warmup):
+        call()
+    h.synchronize()
+    print(f"bench: warmup {args.warmup} done", file=sys.stderr, flush=True)
+
+    h.set_profiling(True)
+    h.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        call()
+    h.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms3, n3, fl3 = h.profile(0)
+    ms1, n1, fl1 = h.profile(1)
+    out = d_out.to_array(np.float32, (batch, h.row_floats))
+    assert np.isfinite(out).all(), "non-finite outputs"
+
+    evals = batch * args.steps
+    value = evals / elapsed
+    avg3_ms = ms3 / max(n3, 1)
+    achieved3 = (fl3 / max(n3, 1)) / (avg3_ms * 1e-3) / 1e12 if n3 else 0.0
+    print(f"bench: {args.steps} steps in {elapsed:.3f} s; 3x3 conv {n3} launches {ms3:.2f} ms total, "
+          f"1x1 conv {n1} launches {ms1:.2f} ms total", file=sys.stderr, flush=True)
+
+    result = {
+        "metric": "NN evals/sec, b18c384nbt fp16 19x19 batch 256; % of fp16 MFMA peak",
+        "value": round(value, 2),
+        "unit": "evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000.0 * elapsed / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded random-weight b18c384nbt, seeded synthetic positions)",
+        "config": {"workload": "C2: b18c384nbt fp16 19x19, batch 256, symmetry 0, inputs resident in HBM",
+                   "global_batch": batch, "board": "19x19", "parallelism": "none (1 GPU)"},
+        "mfma_frac_end_to_end": round(value * flops_per_eval / (PEAK_FP16_TFLOPS * 1e12), 4),
+        "gflop_per_eval": round(flops_per_eval / 1e9, 3),
+        "roofline": {"bound": "mfma", "kernel": "convMfmaKernel (3x3, fp16)", "achieved": round(achieved3, 2),
+                     "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved3 / PEAK_FP16_TFLOPS, 4),
+                     "traffic": None, "avg_launch_ms": round(avg3_ms, 5), "launches": n3},
+    }
+    if not args.no_cpu:
+        print("bench: timing CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(path)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

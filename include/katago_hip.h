@@ -1,0 +1,166 @@
+/*
+ * katago_hip.h - C ABI of libkatago_hip.so, the MI355X (gfx950) device library
+ * behind the HIP backend of KataGo's neural-net interface.
+ *
+ * The C++ host side (katago_amd/host/neuralnet/hipbackend.cpp, which
+ * implements every NeuralNet::* function of
+ * /root/reference/cpp/neuralnet/nninterface.h:32-182) calls only the functions
+ * declared here. The ABI deals in plain pointers, sizes and POD structs: no C++
+ * types, no HIP or torch types.
+ *
+ * Conventions:
+ *  - Every function returns KGH_OK (0) or a nonzero KGH_ERR_* code. The
+ *    message for the most recent failure on the calling thread is returned by
+ *    kgh_last_error(). The host converts failures to StringError, the
+ *    reference's error convention (cudaerrorcheck.h:10-46, nneval.cpp:362-365).
+ *  - Spatial tensors are NHWC float32 rows of nn_y*nn_x*C values.
+ *  - A kgh_handle is not thread-safe; create one per server thread
+ *    (nninterface.h:19-21,69-75). A kgh_model may be shared by handles on
+ *    its device.
+ */
+#ifndef KATAGO_HIP_H
+#define KATAGO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KGH_OK 0
+#define KGH_ERR_INVALID_ARGUMENT 1
+#define KGH_ERR_HIP 2
+#define KGH_ERR_UNSUPPORTED 3
+#define KGH_ERR_OUT_OF_MEMORY 4
+#define KGH_ERR_INTERNAL 5
+
+/* ------------------------------------------------------------------------ */
+/* Layer program: a pre-order flattening of KataGo's ModelDesc tree
+ * (desc.h:15-537). Each record names one layer or opens one block; a block's
+ * layers follow it in the same order the model file lists them
+ * (desc.cpp:507-786,1104-1343,1548-1661,1913-2220). Weights live in one
+ * float array; w[k] is an offset into it (or -1) and wn[k] the element count.
+ */
+enum kgh_op {
+  KGH_OP_CONV = 1,            /* i: convY, convX, inC, outC, dilY, dilX; w0: weights (oc,ic,y,x) */
+  KGH_OP_BN = 2,              /* i: C; w0: mergedScale[C], w1: mergedBias[C] */
+  KGH_OP_ACT = 3,             /* i: activation (ACTIVATION_* codes of activations.h) */
+  KGH_OP_MATMUL = 4,          /* i: inC, outC; w0: weights (ic,oc), oc fastest */
+  KGH_OP_MATBIAS = 5,         /* i: C; w0: bias[C] */
+  KGH_OP_RMSNORM = 6,         /* trunk-tip RMSNorm. i: C, spatial; f0: epsilon; w0: gamma, w1: beta */
+  KGH_OP_TRMSNORM = 7,        /* transformer RMSNorm. i: C; f0: epsilon; w0: weight */
+  KGH_OP_BLOCK_ORDINARY = 10, /* then BN ACT CONV BN ACT CONV */
+  KGH_OP_BLOCK_GPOOL = 11,    /* then BN ACT CONV(regular) CONV(gpool) BN ACT MATMUL BN ACT CONV */
+  KGH_OP_BLOCK_NBT = 12,      /* i: numBlocks; then BN ACT CONV, numBlocks blocks, BN ACT CONV */
+  KGH_OP_BLOCK_ATTENTION = 13,/* i: numHeads, numKVHeads, qHeadDim, vHeadDim, useRope, learnableRope;
+                                 f0: ropeTheta; w0: ropeFreqs (kv,pair,2) or -1;
+                                 then TRMSNORM MATMUL(q) MATMUL(k) MATMUL(v) MATMUL(out) */
+  KGH_OP_BLOCK_FFN = 14,      /* i: C, ffnC, useSwiGLU; then TRMSNORM MATMUL(l1) [MATMUL(gate)] MATMUL(l2) */
+  KGH_OP_TRUNK = 20,          /* i: numBlocks, trunkC, trunkNormKind; then CONV MATMUL, blocks, (BN|RMSNORM) ACT */
+  KGH_OP_POLICY_HEAD = 21,    /* i: policyOutChannels, modelVersion; then CONV(p1) CONV(g1) BN ACT MATMUL
+                                 BN ACT CONV(p2) MATMUL(pass) [MATBIAS ACT MATMUL(pass2) if version>=15] */
+  KGH_OP_VALUE_HEAD = 22      /* then CONV(v1) BN ACT MATMUL(v2) MATBIAS ACT MATMUL(v3) MATBIAS MATMUL(sv3)
+                                 MATBIAS CONV(ownership) */
+};
+
+typedef struct kgh_layer {
+  int32_t op;
+  int32_t i[7];
+  float f[2];
+  int64_t w[2];
+  int64_t wn[2];
+} kgh_layer;
+
+typedef struct kgh_model_desc {
+  int32_t model_version;
+  int32_t num_input_channels;
+  int32_t num_input_global_channels;
+  int32_t num_input_meta_channels;
+  int32_t num_policy_channels;
+  int32_t num_value_channels;
+  int32_t num_score_value_channels;
+  int32_t num_ownership_channels;
+  int32_t num_layers;
+  const kgh_layer* layers;
+  const float* weights;
+  int64_t num_weights;
+} kgh_model_desc;
+
+/* Packed per-row output written by kgh_forward*: for each row, in order,
+ * policy[nn_y*nn_x] (optimism-mixed, inverse-symmetry applied), pass[1],
+ * value[3], score[num_score_value_channels], ownership[nn_y*nn_x]
+ * (inverse-symmetry applied). All raw (pre-softmax/tanh) network outputs,
+ * as NeuralNet::getOutput writes them (eigenbackend.cpp:2527-2615). */
+int32_t kgh_output_row_floats(int32_t nn_x, int32_t nn_y, int32_t num_score_value_channels);
+
+/* ------------------------------------------------------------------------ */
+const char* kgh_last_error(void);
+int kgh_device_count(int32_t* count);
+/* Writes a NUL-terminated description (name, CU count, memory) of device. */
+int kgh_device_info(int32_t device, char* buf, int32_t buflen);
+
+typedef struct kgh_model kgh_model;
+typedef struct kgh_handle kgh_handle;
+
+/* Uploads a model to one device. use_fp16 selects fp16 storage with fp32
+ * accumulation; otherwise everything is fp32. The layer program and weights
+ * are copied; the caller may free them after return. */
+int kgh_model_create(int32_t device, const kgh_model_desc* desc, int32_t use_fp16, kgh_model** out);
+int kgh_model_free(kgh_model* model);
+
+/* One execution context (stream, activation buffers, staging) for batches of
+ * up to max_batch rows of nn_x by nn_y. */
+int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t nn_y,
+                      int32_t require_exact_nn_len, kgh_handle** out);
+int kgh_handle_free(kgh_handle* handle);
+
+/* Host-memory forward: rows are the unsymmetrized NHWC spatial inputs
+ * (n * nn_y*nn_x*num_input_channels floats) and global inputs
+ * (n * num_input_global_channels); symmetry[n] in 0..7 and
+ * policy_optimism[n] per row. out receives n * kgh_output_row_floats(...)
+ * floats. Synchronous. Mirrors NeuralNet::getOutput (nninterface.h:114-122). */
+int kgh_forward(kgh_handle* handle, int32_t n, const float* spatial, const float* global_in,
+                const int32_t* symmetry, const float* policy_optimism, float* out);
+
+/* Device-memory forward on the handle's stream: every pointer is a device
+ * pointer with the same layout as kgh_forward. Asynchronous; call
+ * kgh_handle_synchronize before reading out. */
+int kgh_forward_device(kgh_handle* handle, int32_t n, const float* d_spatial, const float* d_global,
+                       const int32_t* d_symmetry, const float* d_policy_optimism, float* d_out);
+int kgh_handle_synchronize(kgh_handle* handle);
+
+/* Device allocation helpers so that callers without a HIP runtime binding can
+ * stage device-resident inputs (used by the benchmark). */
+int kgh_device_alloc(int32_t device, size_t bytes, void** ptr);
+int kgh_device_free(void* ptr);
+int kgh_memcpy_htod(void* dst, const void* src, size_t bytes);
+int kgh_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+
+/* Layer-level evaluation used by NeuralNet::testEvaluate* (nninterface.h:134-180):
+ * the program is a single CONV, a BN+ACT pair, or one residual block
+ * (ORDINARY / GPOOL / NBT). Input, mask and output are NHWC / NHW float32
+ * host arrays; the result is conv(x), act(bn(x))*mask, or x + block(x). */
+int kgh_evaluate_layers(int32_t device, const kgh_layer* layers, int32_t num_layers, const float* weights,
+                        int64_t num_weights, int32_t use_fp16, int32_t batch, int32_t nn_x, int32_t nn_y,
+                        const float* input, const float* mask, float* output);
+
+/* Per-launch timing of the convolution kernels, measured with HIP events on
+ * the handle's stream. kgh_handle_set_profiling(h, 1) clears the records and
+ * starts recording every conv launch of the following forwards;
+ * kgh_handle_profile sums the records of one kind (0 = 3x3 convs, 1 = 1x1
+ * convs, 2 = all convs): total milliseconds, number of launches and the
+ * launches' algorithmic FLOPs (2*M*Cin*Cout*ky*kx each). */
+int kgh_handle_set_profiling(kgh_handle* handle, int32_t enabled);
+int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32_t* launches, double* flops);
+
+/* Self-test of the matrix-core operand/result layout the conv kernels assume:
+ * multiplies fixed 32x32x16 fp16 (and 32x32x2 fp32) tiles on device and
+ * compares with a host product. Returns KGH_OK when every element matches. */
+int kgh_selftest_mfma(int32_t device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,75 @@
+/*
+ * katago_nn.h - C ABI over the NeuralNet interface of libkatago_host.so, for
+ * callers that cannot use C++ (the Python package's ctypes binding and its
+ * tests). Each function maps onto one NeuralNet::* call of
+ * /root/reference/cpp/neuralnet/nninterface.h:32-182 as implemented by
+ * katago_amd/host/neuralnet/hipbackend.cpp; a C++ caller inside KataGo uses
+ * NeuralNet::* directly instead.
+ *
+ * Errors: functions returning int return 0 on success and -1 on failure;
+ * functions returning pointers return NULL on failure. In both cases the
+ * StringError message is copied into err (NUL-terminated, errlen bytes).
+ */
+#ifndef KATAGO_NN_H
+#define KATAGO_NN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* NeuralNet::loadModelFile (nninterface.h:43). */
+void* kgn_load_model(const char* path, const char* expected_sha256, char* err, int32_t errlen);
+/* NeuralNet::freeLoadedModel (nninterface.h:44). */
+void kgn_free_model(void* loaded_model);
+/* Fields of NeuralNet::getModelDesc (nninterface.h:46): info[0..8] =
+ * modelVersion, numInputChannels, numInputGlobalChannels, numPolicyChannels,
+ * numValueChannels, numScoreValueChannels, numOwnershipChannels,
+ * trunkNumChannels, numInputMetaChannels. */
+int32_t kgn_model_info(void* loaded_model, int32_t* info, float* output_scale_multiplier, char* name, int32_t namelen);
+
+/* The layer program (kgh_layer records) and weights the backend passes to
+ * kgh_model_create for this model, after the load-time transforms. Call with
+ * NULL outputs to get the sizes, then again with buffers of those sizes. */
+int32_t kgn_model_flatten(void* loaded_model, int32_t* num_layers, int64_t* num_weights, void* layers_out,
+                          float* weights_out);
+
+/* NeuralNet::createComputeContext (nninterface.h:50-63); use_fp16: 0 false,
+ * 1 true, 2 auto. */
+void* kgn_create_context(void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t use_fp16, char* err, int32_t errlen);
+/* NeuralNet::freeComputeContext (nninterface.h:64). */
+void kgn_free_context(void* context);
+/* NeuralNet::createComputeHandle (nninterface.h:74-83). */
+void* kgn_create_handle(void* context, void* loaded_model, int32_t max_batch, int32_t require_exact_nn_len,
+                        int32_t inputs_use_nhwc, int32_t gpu_idx, char* err, int32_t errlen);
+/* NeuralNet::freeComputeHandle (nninterface.h:84). */
+void kgn_free_handle(void* handle);
+/* NeuralNet::isUsingFP16 (nninterface.h:86). */
+int32_t kgn_is_using_fp16(void* handle);
+
+/* NeuralNet::getOutput (nninterface.h:114-120) for n rows of the nn_x by nn_y
+ * board size the handle's context was created with: spatial and global
+ * are the rows' rowSpatialBuf/rowGlobalBuf back to back, symmetry and
+ * policy_optimism per row. Outputs (raw logits, as getOutput writes them):
+ * policy n*(nn_x*nn_y+1) (pass last), value n*3, score n*6 (whiteScoreMean,
+ * whiteScoreMeanSq, whiteLead, varTimeLeft, shorttermWinlossError,
+ * shorttermScoreError), ownership n*nn_x*nn_y. */
+int32_t kgn_get_output(void* handle, void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t n, const float* spatial, const float* global_in,
+                       const int32_t* symmetry, const float* policy_optimism, float* policy, float* value, float* score,
+                       float* ownership, char* err, int32_t errlen);
+
+/* NeuralNet::testEvaluate{Conv,BatchNorm,ResidualBlock,GlobalPoolingResidualBlock}
+ * (nninterface.h:134-180). kind: 0 conv, 1 batch norm, 2 residual block,
+ * 3 global pooling residual block; desc_text is the descriptor in the model
+ * text format (model version 15 grammar). Returns 1 if evaluated, 0 if the
+ * backend does not support the combination, -1 on error. */
+int32_t kgn_test_evaluate(int32_t kind, const char* desc_text, int32_t batch, int32_t nn_x, int32_t nn_y, int32_t use_fp16,
+                          int32_t use_nhwc, const float* input, const float* mask, float* output, int64_t output_len,
+                          char* err, int32_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

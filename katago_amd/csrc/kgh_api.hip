@@ -1,0 +1,1164 @@
+// C ABI of libkatago_hip.so (include/katago_hip.h): model upload from a layer
+// program, per-handle execution state, and the forward pass.
+//
+// Forward pass structure (reference: Model::apply, eigenbackend.cpp:2150-2205):
+//   pack inputs (symmetry, mask, mask sums) -> stem conv (+ global matmul bias)
+//   -> block stack -> trunk tip -> policy/value heads -> unpack outputs.
+// KataGo's blocks are pre-activation (BN+act precede each conv,
+// eigenbackend.cpp:1055-1066), so every convolution that updates a residual
+// stream also writes, in its epilogue, the next consumer's folded-BN +
+// activation + mask of the updated stream. Each stream level therefore keeps
+// two tensors: the raw residual stream R and its activated copy A.
+#include "kgh_kernels.h"
+
+#include <algorithm>
+#include <climits>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/katago_hip.h"
+
+namespace {
+
+thread_local std::string g_lastError;
+
+int fail(int code, const std::string& msg) {
+  g_lastError = msg;
+  return code;
+}
+
+template<typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    return KGH_OK;
+  }
+  catch(const KghError& e) {
+    return fail(e.code, e.what());
+  }
+  catch(const std::bad_alloc&) {
+    return fail(KGH_ERR_OUT_OF_MEMORY, "host out of memory");
+  }
+  catch(const std::exception& e) {
+    return fail(KGH_ERR_INTERNAL, e.what());
+  }
+}
+
+[[noreturn]] void invalid(const std::string& m) { throw KghError(KGH_ERR_INVALID_ARGUMENT, m); }
+[[noreturn]] void unsupported(const std::string& m) { throw KghError(KGH_ERR_UNSUPPORTED, m); }
+
+size_t roundUp(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+// Device allocations owned by a model or handle, freed together.
+struct DeviceArena {
+  std::vector<void*> ptrs;
+  void* alloc(size_t bytes) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, std::max<size_t>(bytes, 256));
+    if(e != hipSuccess) throw KghError(KGH_ERR_OUT_OF_MEMORY, std::string("hipMalloc failed: ") + hipGetErrorString(e));
+    ptrs.push_back(p);
+    return p;
+  }
+  template<typename X> X* allocN(size_t n) { return (X*)alloc(n * sizeof(X)); }
+  ~DeviceArena() {
+    for(void* p : ptrs) (void)hipFree(p);
+  }
+};
+
+struct ConvW {
+  int ky = 0, kx = 0, cin = 0, cinPad = 0, cout = 0;
+  void* wPrep = nullptr;          // [tap][cout][cinPad] of the activation type, when matrix cores apply
+  const float* wDirect = nullptr; // (oc, ic, y, x) fp32 on device
+};
+
+struct BNAct {
+  int C = 0;
+  const float* scale = nullptr;
+  const float* bias = nullptr;
+  int act = KGH_ACT_IDENTITY;
+};
+
+struct MatW {
+  int cin = 0, cout = 0;
+  const float* w = nullptr;  // [cin][cout]
+};
+
+struct BiasW {
+  int C = 0;
+  const float* b = nullptr;
+};
+
+enum BlockKind { BK_ORDINARY = 0, BK_GPOOL = 2, BK_NBT = 3 };
+
+struct Block {
+  int kind = BK_ORDINARY;
+  BNAct preBN;
+  ConvW conv1;   // ordinary: regular conv; gpool: regular+gpool combined; nbt: preConv
+  BNAct midBN;   // ordinary/gpool: midBN; nbt: postBN
+  ConvW conv2;   // ordinary/gpool: finalConv; nbt: postConv
+  int regC = 0, gpC = 0;
+  BNAct gpoolBN;
+  MatW gpoolMul;
+  std::vector<Block> inner;
+};
+
+struct HeadConv {
+  ConvW conv;
+  int rawEnd = 0;      // channels [0, rawEnd) are raw p1
+  int actBegin = 0;    // channels [actBegin, cout) are activated into the g1|v1 buffer
+  int actDstOffset = 0;
+  BNAct act;           // scale/bias for channels >= actBegin
+};
+
+struct Net {
+  bool fp16 = false;
+  int modelVersion = 0;
+  int inputC = 0, inputCPad = 0, globalC = 0;
+  int policyC = 0, scoreC = 0;
+  ConvW initialConv;
+  MatW initialMatMul;
+  int trunkC = 0;
+  int tipKind = 0;
+  BNAct tipBN;
+  std::vector<Block> blocks;
+  // heads
+  int p1C = 0, g1C = 0, v1C = 0;
+  std::vector<HeadConv> headConvs;
+  MatW gpoolToBiasMul;
+  BNAct p1BN;
+  const float* p2W = nullptr;
+  MatW passMul;
+  BiasW passBias;
+  int passAct = KGH_ACT_IDENTITY;
+  MatW passMul2;
+  MatW v2Mul;
+  BiasW v2Bias;
+  int v2Act = KGH_ACT_IDENTITY;
+  MatW v3Mul;
+  BiasW v3Bias;
+  MatW sv3Mul;
+  BiasW sv3Bias;
+  const float* ownW = nullptr;
+  // buffer sizing
+  std::vector<int> depthC;
+  int tmpC = 0;
+};
+
+// ---------------------------------------------------------------------------
+// Building the device network from a layer program.
+
+struct Builder {
+  const kgh_layer* L;
+  int n;
+  int pos = 0;
+  const float* hostW;
+  int64_t numW;
+  const float* devW;  // device copy of the whole weight array
+  DeviceArena& arena;
+  bool fp16;
+  hipStream_t stream;
+
+  const kgh_layer& take(int op, const char* what) {
+    if(pos >= n) invalid(std::string("layer program ended early, expected ") + what);
+    const kgh_layer& l = L[pos];
+    if(l.op != op) invalid(std::string("layer program: expected ") + what + " at record " + std::to_string(pos) + ", found op " + std::to_string(l.op));
+    pos++;
+    return l;
+  }
+  int peek() const { return pos < n ? L[pos].op : -1; }
+
+  const float* dev(const kgh_layer& l, int k, int64_t expectCount, const char* what) {
+    if(l.w[k] < 0 || l.w[k] + l.wn[k] > numW) invalid(std::string(what) + ": weight range out of bounds");
+    if(l.wn[k] != expectCount) invalid(std::string(what) + ": weight count " + std::to_string(l.wn[k]) + " != expected " + std::to_string(expectCount));
+    return devW + l.w[k];
+  }
+  const float* host(const kgh_layer& l, int k) const { return hostW + l.w[k]; }
+
+  const float* upload(const std::vector<float>& v) {
+    float* d = arena.allocN<float>(v.size());
+    KGH_HIP_CHECK(hipMemcpyAsync(d, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice, stream));
+    KGH_HIP_CHECK(hipStreamSynchronize(stream));
+    return d;
+  }
+
+  int bk() const { return fp16 ? 32 : 16; }
+
+  // Prepares conv weights from a device fp32 (oc,ic,y,x) array.
+  ConvW makeConv(const float* dW, int ky, int kx, int cin, int cout, bool allowPadCin) {
+    ConvW c;
+    c.ky = ky;
+    c.kx = kx;
+    c.cin = cin;
+    c.cout = cout;
+    c.cinPad = (allowPadCin && cin % bk() != 0) ? (int)roundUp(cin, bk()) : cin;
+    c.wDirect = dW;
+    bool shapeOk = (ky == kx) && (ky == 1 || ky == 3);
+    bool mfmaOk = fp16 ? kgh::convMfmaSupported<half_t>(c.cinPad, cout) : kgh::convMfmaSupported<float>(c.cinPad, cout);
+    if(shapeOk && mfmaOk) {
+      size_t count = (size_t)ky * kx * cout * c.cinPad;
+      if(fp16) {
+        half_t* p = arena.allocN<half_t>(count);
+        kgh::prepareConvWeights<half_t>(dW, p, cout, cin, c.cinPad, ky, kx, stream);
+        c.wPrep = p;
+      }
+      else {
+        float* p = arena.allocN<float>(count);
+        kgh::prepareConvWeights<float>(dW, p, cout, cin, c.cinPad, ky, kx, stream);
+        c.wPrep = p;
+      }
+    }
+    return c;
+  }
+
+  struct ConvRec {
+    const kgh_layer* l;
+    int ky, kx, cin, cout;
+  };
+  ConvRec convRec(const char* what) {
+    const kgh_layer& l = take(KGH_OP_CONV, what);
+    ConvRec r{&l, l.i[0], l.i[1], l.i[2], l.i[3]};
+    if(r.ky <= 0 || r.kx <= 0 || r.ky % 2 != 1 || r.kx % 2 != 1 || r.cin <= 0 || r.cout <= 0) invalid(std::string(what) + ": bad conv shape");
+    if(l.i[4] != 1 || l.i[5] != 1) unsupported(std::string(what) + ": dilated convolutions are not supported");
+    dev(l, 0, (int64_t)r.ky * r.kx * r.cin * r.cout, what);
+    return r;
+  }
+  ConvW conv(const char* what, bool allowPadCin = false) {
+    ConvRec r = convRec(what);
+    return makeConv(dev(*r.l, 0, (int64_t)r.ky * r.kx * r.cin * r.cout, what), r.ky, r.kx, r.cin, r.cout, allowPadCin);
+  }
+
+  BNAct bnAct(const char* what) {
+    const kgh_layer& b = take(KGH_OP_BN, what);
+    BNAct r;
+    r.C = b.i[0];
+    r.scale = dev(b, 0, r.C, what);
+    r.bias = dev(b, 1, r.C, what);
+    const kgh_layer& a = take(KGH_OP_ACT, what);
+    r.act = a.i[0];
+    if(r.act != KGH_ACT_IDENTITY && r.act != KGH_ACT_RELU && r.act != KGH_ACT_MISH && r.act != KGH_ACT_SILU && r.act != KGH_ACT_MISH_SCALE8)
+      invalid(std::string(what) + ": unknown activation " + std::to_string(r.act));
+    return r;
+  }
+  int act(const char* what) { return take(KGH_OP_ACT, what).i[0]; }
+
+  MatW matmul(const char* what) {
+    const kgh_layer& l = take(KGH_OP_MATMUL, what);
+    MatW m;
+    m.cin = l.i[0];
+    m.cout = l.i[1];
+    m.w = dev(l, 0, (int64_t)m.cin * m.cout, what);
+    return m;
+  }
+  BiasW matbias(const char* what) {
+    const kgh_layer& l = take(KGH_OP_MATBIAS, what);
+    BiasW b;
+    b.C = l.i[0];
+    b.b = dev(l, 0, b.C, what);
+    return b;
+  }
+
+  Block block(Net& net, int depth, int streamC) {
+    Block blk;
+    int op = peek();
+    if(op == KGH_OP_BLOCK_ORDINARY) {
+      take(op, "ordinary block");
+      blk.kind = BK_ORDINARY;
+      blk.preBN = bnAct("ordinary preBN");
+      blk.conv1 = conv("ordinary regularConv");
+      blk.midBN = bnAct("ordinary midBN");
+      blk.conv2 = conv("ordinary finalConv");
+      if(blk.preBN.C != streamC || blk.conv1.cin != streamC || blk.conv2.cout != streamC || blk.midBN.C != blk.conv1.cout ||
+         blk.conv2.cin != blk.conv1.cout)
+        invalid("ordinary block: channel mismatch");
+      net.tmpC = std::max(net.tmpC, blk.conv1.cout);
+    }
+    else if(op == KGH_OP_BLOCK_GPOOL) {
+      take(op, "gpool block");
+      blk.kind = BK_GPOOL;
+      blk.preBN = bnAct("gpool preBN");
+      ConvRec reg = convRec("gpool regularConv");
+      ConvRec gp = convRec("gpool gpoolConv");
+      if(reg.ky != gp.ky || reg.kx != gp.kx || reg.cin != gp.cin) unsupported("gpool block: regular and gpool convs differ in shape");
+      // One convolution producing [regular | gpool] output channels.
+      std::vector<float> cat((size_t)(reg.cout + gp.cout) * reg.cin * reg.ky * reg.kx);
+      size_t regCount = (size_t)reg.cout * reg.cin * reg.ky * reg.kx;
+      memcpy(cat.data(), host(*reg.l, 0), regCount * sizeof(float));
+      memcpy(cat.data() + regCount, host(*gp.l, 0), (size_t)gp.cout * gp.cin * gp.ky * gp.kx * sizeof(float));
+      blk.conv1 = makeConv(upload(cat), reg.ky, reg.kx, reg.cin, reg.cout + gp.cout, false);
+      blk.regC = reg.cout;
+      blk.gpC = gp.cout;
+      blk.gpoolBN = bnAct("gpool gpoolBN");
+      blk.gpoolMul = matmul("gpool gpoolToBiasMul");
+      blk.midBN = bnAct("gpool midBN");
+      blk.conv2 = conv("gpool finalConv");
+      if(blk.preBN.C != streamC || reg.cin != streamC || blk.conv2.cout != streamC || blk.gpoolBN.C != blk.gpC ||
+         blk.gpoolMul.cin != 3 * blk.gpC || blk.gpoolMul.cout != blk.regC || blk.midBN.C != blk.regC || blk.conv2.cin != blk.regC)
+        invalid("gpool block: channel mismatch");
+      net.tmpC = std::max(net.tmpC, std::max(blk.regC, blk.gpC));
+    }
+    else if(op == KGH_OP_BLOCK_NBT) {
+      const kgh_layer& h = take(op, "nested bottleneck block");
+      blk.kind = BK_NBT;
+      int numInner = h.i[0];
+      if(numInner < 1) invalid("nested bottleneck block: numBlocks must be positive");
+      blk.preBN = bnAct("nbt preBN");
+      blk.conv1 = conv("nbt preConv");
+      int midC = blk.conv1.cout;
+      if((int)net.depthC.size() <= depth + 1) net.depthC.resize(depth + 2, 0);
+      net.depthC[depth + 1] = std::max(net.depthC[depth + 1], midC);
+      for(int i = 0; i < numInner; i++) blk.inner.push_back(block(net, depth + 1, midC));
+      blk.midBN = bnAct("nbt postBN");
+      blk.conv2 = conv("nbt postConv");
+      if(blk.preBN.C != streamC || blk.conv1.cin != streamC || blk.conv2.cout != streamC || blk.midBN.C != midC || blk.conv2.cin != midC)
+        invalid("nested bottleneck block: channel mismatch");
+    }
+    else if(op == KGH_OP_BLOCK_ATTENTION || op == KGH_OP_BLOCK_FFN) {
+      unsupported("transformer blocks are not supported by this build of the device library");
+    }
+    else {
+      invalid("layer program: expected a block at record " + std::to_string(pos));
+    }
+    return blk;
+  }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+
+struct kgh_model {
+  int device = 0;
+  Net net;
+  DeviceArena arena;
+};
+
+namespace {
+
+struct ProfRec {
+  int kind;  // 0 = 3x3 conv, 1 = 1x1 conv, 2 = other conv
+  double flops;
+  hipEvent_t start, stop;
+};
+
+}  // namespace
+
+struct kgh_handle {
+  kgh_model* model = nullptr;
+  int maxBatch = 0, H = 0, W = 0;
+  bool exact = false;
+  hipStream_t stream = nullptr;
+  DeviceArena arena;
+  int rowFloats = 0;
+
+  // activation buffers (element type = model dtype)
+  void* x0 = nullptr;
+  float* mask = nullptr;
+  float* maskSum = nullptr;
+  float* gbias = nullptr;
+  std::vector<void*> R, A;
+  void* tmp1 = nullptr;
+  void* tmp2 = nullptr;
+  void* tmp3 = nullptr;
+  float* nbias = nullptr;
+  void* p1 = nullptr;
+  void* gv = nullptr;
+  float* g1Bias = nullptr;
+  float* pass = nullptr;
+  float* value = nullptr;
+  float* score = nullptr;
+  float* policyRaw = nullptr;
+  float* ownRaw = nullptr;
+
+  // staging for host-memory forwards
+  float* dSpatial = nullptr;
+  float* dGlobal = nullptr;
+  int* dSym = nullptr;
+  float* dOpt = nullptr;
+  float* dOut = nullptr;
+  float* hSpatial = nullptr;
+  float* hGlobal = nullptr;
+  int* hSym = nullptr;
+  float* hOpt = nullptr;
+  float* hOut = nullptr;
+
+  bool profiling = false;
+  std::vector<ProfRec> prof;
+  size_t profUsed = 0;
+
+  ~kgh_handle() {
+    for(auto& p : prof) {
+      (void)hipEventDestroy(p.start);
+      (void)hipEventDestroy(p.stop);
+    }
+    if(hSpatial) (void)hipHostFree(hSpatial);
+    if(hGlobal) (void)hipHostFree(hGlobal);
+    if(hSym) (void)hipHostFree(hSym);
+    if(hOpt) (void)hipHostFree(hOpt);
+    if(hOut) (void)hipHostFree(hOut);
+    if(stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Forward execution.
+
+template<typename T>
+struct Runner {
+  const Net& net;
+  kgh_handle* h;  // may be null for layer tests (no profiling)
+  hipStream_t s;
+  BoardGeom g;
+  int M;
+  const float* mask;
+  const float* maskSum;
+  std::vector<T*> R, A;
+  int ldR0;
+  T* tmp1;
+  T* tmp2;
+  T* tmp3;
+  float* nbias;
+
+  ConvEpilogue<T> epi() const {
+    ConvEpilogue<T> e;
+    memset(&e, 0, sizeof(e));
+    e.rawEnd = 0;
+    e.actBegin = INT_MAX;
+    e.mask = mask;
+    e.actKind = KGH_ACT_IDENTITY;
+    return e;
+  }
+  static void setAct(ConvEpilogue<T>& e, const BNAct* bn, T* out, int ld) {
+    if(bn == nullptr) {
+      e.outAct = nullptr;
+      e.actBegin = INT_MAX;
+      return;
+    }
+    e.outAct = out;
+    e.ldAct = ld;
+    e.actBegin = 0;
+    e.actScale = bn->scale;
+    e.actBias = bn->bias;
+    e.actKind = bn->act;
+  }
+
+  void conv(const ConvW& c, const T* x, int ldx, const ConvEpilogue<T>& e) {
+    ProfRec* rec = nullptr;
+    if(h != nullptr && h->profiling) {
+      if(h->profUsed == h->prof.size()) {
+        ProfRec r;
+        KGH_HIP_CHECK(hipEventCreate(&r.start));
+        KGH_HIP_CHECK(hipEventCreate(&r.stop));
+        h->prof.push_back(r);
+      }
+      rec = &h->prof[h->profUsed++];
+      rec->kind = (c.ky == 3 && c.kx == 3) ? 0 : (c.ky == 1 && c.kx == 1) ? 1 : 2;
+      rec->flops = 2.0 * M * (double)c.cin * c.cout * c.ky * c.kx;
+      KGH_HIP_CHECK(hipEventRecord(rec->start, s));
+    }
+    kgh::launchConv<T>(x, ldx, c.cin, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, c.wDirect, g, e, s, nullptr);
+    if(rec != nullptr) KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
+  }
+
+  void bnAct(const T* x, int ldx, T* y, int ldy, const BNAct& bn, const float* ncBias, int ldNC) {
+    kgh::launchBnAct<T>(x, ldx, y, ldy, bn.C, bn.scale, bn.bias, bn.act, mask, ncBias, ldNC, g.H * g.W, M, s);
+  }
+
+  static bool isConvKind(const Block& b) { return b.kind == BK_ORDINARY || b.kind == BK_GPOOL || b.kind == BK_NBT; }
+
+  // On entry, if blocks[0] is a conv-kind block, A[depth] holds
+  // act(blocks[0].preBN(R[depth])) * mask. On exit, if tail != null, A[depth]
+  // holds act(tail(R[depth])) * mask.
+  void runStack(const std::vector<Block>& blocks, int depth, const BNAct* tail) {
+    for(size_t i = 0; i < blocks.size(); i++) {
+      const BNAct* next = (i + 1 < blocks.size()) ? (isConvKind(blocks[i + 1]) ? &blocks[i + 1].preBN : nullptr) : tail;
+      runBlock(blocks[i], depth, next);
+    }
+  }
+
+  void runBlock(const Block& b, int depth, const BNAct* next) {
+    T* Rd = R[depth];
+    T* Ad = A[depth];
+    const int C = b.preBN.C;
+    if(b.kind == BK_ORDINARY) {
+      // mid = act(midBN(conv1(A))) * mask
+      ConvEpilogue<T> e1 = epi();
+      setAct(e1, &b.midBN, tmp1, b.conv1.cout);
+      conv(b.conv1, Ad, C, e1);
+      // R += conv2(mid); A = act(next(R)) * mask
+      ConvEpilogue<T> e2 = epi();
+      e2.residual = Rd;
+      e2.ldRes = C;
+      e2.outRaw = Rd;
+      e2.ldRaw = C;
+      e2.rawEnd = C;
+      setAct(e2, next, Ad, C);
+      conv(b.conv2, tmp1, b.conv1.cout, e2);
+    }
+    else if(b.kind == BK_GPOOL) {
+      // [regular raw | gpool activated] from one conv
+      ConvEpilogue<T> e1 = epi();
+      e1.outRaw = tmp1;
+      e1.ldRaw = b.regC;
+      e1.rawEnd = b.regC;
+      e1.outAct = tmp2;
+      e1.ldAct = b.gpC;
+      e1.actBegin = b.regC;
+      e1.actScale = b.gpoolBN.scale;
+      e1.actBias = b.gpoolBN.bias;
+      e1.actKind = b.gpoolBN.act;
+      conv(b.conv1, Ad, C, e1);
+      // masked pooling of the gpool channels, then the bias matvec
+      kgh::launchPool<T>(tmp2, b.gpC, b.gpC, mask, maskSum, g.batch, g.H * g.W, false, nullptr, 0, b.gpoolMul.w, b.regC, nbias,
+                         b.regC, s);
+      // x = act(midBN(regular + bias)) * mask
+      bnAct(tmp1, b.regC, tmp3, b.regC, b.midBN, nbias, b.regC);
+      ConvEpilogue<T> e2 = epi();
+      e2.residual = Rd;
+      e2.ldRes = C;
+      e2.outRaw = Rd;
+      e2.ldRaw = C;
+      e2.rawEnd = C;
+      setAct(e2, next, Ad, C);
+      conv(b.conv2, tmp3, b.regC, e2);
+    }
+    else if(b.kind == BK_NBT) {
+      const int midC = b.conv1.cout;
+      T* Rm = R[depth + 1];
+      T* Am = A[depth + 1];
+      ConvEpilogue<T> e1 = epi();
+      e1.outRaw = Rm;
+      e1.ldRaw = midC;
+      e1.rawEnd = midC;
+      const BNAct* firstInner = isConvKind(b.inner[0]) ? &b.inner[0].preBN : nullptr;
+      setAct(e1, firstInner, Am, midC);
+      conv(b.conv1, Ad, C, e1);
+      runStack(b.inner, depth + 1, &b.midBN);
+      ConvEpilogue<T> e2 = epi();
+      e2.residual = Rd;
+      e2.ldRes = C;
+      e2.outRaw = Rd;
+      e2.ldRaw = C;
+      e2.rawEnd = C;
+      setAct(e2, next, Ad, C);
+      conv(b.conv2, Am, midC, e2);
+    }
+    else {
+      throw KghError(KGH_ERR_INTERNAL, "unknown block kind");
+    }
+  }
+};
+
+template<typename T>
+Runner<T> makeRunner(const Net& net, kgh_handle* h, int batch) {
+  Runner<T> r{net, h, h->stream, BoardGeom{batch, h->H, h->W}, batch * h->H * h->W, h->mask, h->maskSum, {}, {}, 0,
+              (T*)h->tmp1, (T*)h->tmp2, (T*)h->tmp3, h->nbias};
+  for(size_t d = 0; d < h->R.size(); d++) {
+    r.R.push_back((T*)h->R[d]);
+    r.A.push_back((T*)h->A[d]);
+  }
+  return r;
+}
+
+template<typename T>
+void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlobal, const int* dSym, const float* dOpt, float* dOut) {
+  const Net& net = h->model->net;
+  Runner<T> r = makeRunner<T>(net, h, n);
+  hipStream_t s = h->stream;
+  const int HW = h->H * h->W;
+
+  kgh::launchPackInputs<T>(dSpatial, dSym, n, h->H, h->W, net.inputC, (T*)h->x0, net.inputCPad, h->mask, h->maskSum, s);
+  kgh::launchRowMatmul(dGlobal, net.globalC, net.globalC, net.initialMatMul.w, net.trunkC, nullptr, KGH_ACT_IDENTITY, h->gbias,
+                       net.trunkC, n, s);
+
+  // Stem: R0 = conv(x) + globalBias[n]; A0 = first block's preBN activation.
+  {
+    ConvEpilogue<T> e = r.epi();
+    e.ncBias = h->gbias;
+    e.ldNC = net.trunkC;
+    e.outRaw = r.R[0];
+    e.ldRaw = net.trunkC;
+    e.rawEnd = net.trunkC;
+    const BNAct* first = Runner<T>::isConvKind(net.blocks[0]) ? &net.blocks[0].preBN : nullptr;
+    Runner<T>::setAct(e, first, r.A[0], net.trunkC);
+    r.conv(net.initialConv, (const T*)h->x0, net.inputCPad, e);
+  }
+  r.runStack(net.blocks, 0, &net.tipBN);
+
+  // Heads: 1x1 convs p1 | g1 | v1 from the activated trunk tip.
+  T* p1 = (T*)h->p1;
+  T* gv = (T*)h->gv;
+  const int gvC = net.g1C + net.v1C;
+  for(const HeadConv& hc : net.headConvs) {
+    ConvEpilogue<T> e = r.epi();
+    e.outRaw = p1;
+    e.ldRaw = net.p1C;
+    e.rawEnd = hc.rawEnd;
+    e.outAct = gv + hc.actDstOffset;
+    e.ldAct = gvC;
+    e.actBegin = hc.actBegin;
+    e.actScale = hc.act.scale;
+    e.actBias = hc.act.bias;
+    e.actKind = hc.act.act;
+    r.conv(hc.conv, r.A[0], net.trunkC, e);
+  }
+  HeadRowArgs<T> ha;
+  ha.g1 = gv;
+  ha.ldG1 = gvC;
+  ha.v1 = gv + net.g1C;
+  ha.ldV1 = gvC;
+  ha.g1C = net.g1C;
+  ha.v1C = net.v1C;
+  ha.p1C = net.p1C;
+  ha.policyC = net.policyC;
+  ha.passHidden = net.passMul2.w != nullptr ? net.passMul.cout : 0;
+  ha.v2C = net.v2Mul.cout;
+  ha.scoreC = net.scoreC;
+  ha.hiddenMax = std::max(ha.passHidden, ha.v2C);
+  ha.HW = HW;
+  ha.mask = h->mask;
+  ha.maskSum = h->maskSum;
+  ha.gpoolToBiasMul = net.gpoolToBiasMul.w;
+  ha.passMul = net.passMul.w;
+  ha.passBias = net.passBias.b;
+  ha.passAct = net.passAct;
+  ha.passMul2 = net.passMul2.w;
+  ha.v2Mul = net.v2Mul.w;
+  ha.v2Bias = net.v2Bias.b;
+  ha.v2Act = net.v2Act;
+  ha.v3Mul = net.v3Mul.w;
+  ha.v3Bias = net.v3Bias.b;
+  ha.sv3Mul = net.sv3Mul.w;
+  ha.sv3Bias = net.sv3Bias.b;
+  ha.g1Bias = h->g1Bias;
+  ha.pass = h->pass;
+  ha.value = h->value;
+  ha.score = h->score;
+  kgh::launchHeadRow<T>(ha, n, s);
+
+  HeadSpatialArgs<T> hs;
+  hs.p1 = p1;
+  hs.ldP1 = net.p1C;
+  hs.v1 = gv + net.g1C;
+  hs.ldV1 = gvC;
+  hs.p1C = net.p1C;
+  hs.v1C = net.v1C;
+  hs.policyC = net.policyC;
+  hs.M = n * HW;
+  hs.HW = HW;
+  hs.g1Bias = h->g1Bias;
+  hs.p1Scale = net.p1BN.scale;
+  hs.p1Bias = net.p1BN.bias;
+  hs.p1Act = net.p1BN.act;
+  hs.p2W = net.p2W;
+  hs.ownW = net.ownW;
+  hs.mask = h->mask;
+  hs.policy = h->policyRaw;
+  hs.ownership = h->ownRaw;
+  kgh::launchHeadSpatial<T>(hs, s);
+
+  UnpackArgs ua;
+  ua.policy = h->policyRaw;
+  ua.pass = h->pass;
+  ua.value = h->value;
+  ua.score = h->score;
+  ua.ownership = h->ownRaw;
+  ua.sym = dSym;
+  ua.optimism = dOpt;
+  ua.policyC = net.policyC;
+  ua.scoreC = net.scoreC;
+  ua.mixOptimism = (net.policyC == 2 || (net.policyC == 4 && net.modelVersion >= 16)) ? 1 : 0;
+  ua.batch = n;
+  ua.H = h->H;
+  ua.W = h->W;
+  ua.rowFloats = h->rowFloats;
+  ua.out = dOut;
+  kgh::launchUnpackOutputs(ua, s);
+}
+
+void buildNet(kgh_model* m, const kgh_model_desc* d, hipStream_t stream) {
+  Net& net = m->net;
+  const float* devW = m->arena.allocN<float>((size_t)std::max<int64_t>(d->num_weights, 1));
+  if(d->num_weights > 0)
+    KGH_HIP_CHECK(hipMemcpy((void*)devW, d->weights, (size_t)d->num_weights * sizeof(float), hipMemcpyHostToDevice));
+  Builder b{d->layers, d->num_layers, 0, d->weights, d->num_weights, devW, m->arena, net.fp16, stream};
+
+  net.modelVersion = d->model_version;
+  net.inputC = d->num_input_channels;
+  net.globalC = d->num_input_global_channels;
+  net.policyC = d->num_policy_channels;
+  net.scoreC = d->num_score_value_channels;
+  if(d->num_input_meta_channels > 0) unsupported("models with an SGF metadata encoder are not supported");
+  if(net.policyC < 1 || net.policyC > 4) invalid("num_policy_channels must be 1..4");
+  if(d->num_value_channels != 3) invalid("num_value_channels must be 3");
+  if(net.scoreC < 1 || net.scoreC > 6) invalid("num_score_value_channels must be 1..6");
+  if(d->num_ownership_channels != 1) invalid("num_ownership_channels must be 1");
+
+  const kgh_layer& t = b.take(KGH_OP_TRUNK, "trunk");
+  int numBlocks = t.i[0];
+  net.trunkC = t.i[1];
+  net.tipKind = t.i[2];
+  if(net.tipKind != 0) unsupported("RMSNorm trunk tips are not supported by this build of the device library");
+  net.initialConv = b.conv("initialConv", true);
+  net.inputCPad = net.initialConv.cinPad;
+  if(net.initialConv.cin != net.inputC || net.initialConv.cout != net.trunkC) invalid("initialConv channel mismatch");
+  net.initialMatMul = b.matmul("initialMatMul");
+  if(net.initialMatMul.cin != net.globalC || net.initialMatMul.cout != net.trunkC) invalid("initialMatMul channel mismatch");
+  net.depthC.assign(1, net.trunkC);
+  for(int i = 0; i < numBlocks; i++) net.blocks.push_back(b.block(net, 0, net.trunkC));
+  net.tipBN = b.bnAct("trunk tip");
+  if(net.tipBN.C != net.trunkC) invalid("trunk tip channel mismatch");
+
+  // Policy head
+  const kgh_layer& ph = b.take(KGH_OP_POLICY_HEAD, "policy head");
+  if(ph.i[0] != net.policyC) invalid("policy head channel count mismatch");
+  Builder::ConvRec p1 = b.convRec("p1Conv");
+  Builder::ConvRec g1 = b.convRec("g1Conv");
+  BNAct g1BN = b.bnAct("g1BN");
+  net.gpoolToBiasMul = b.matmul("gpoolToBiasMul");
+  net.p1BN = b.bnAct("p1BN");
+  Builder::ConvRec p2 = b.convRec("p2Conv");
+  net.passMul = b.matmul("gpoolToPassMul");
+  if(b.peek() == KGH_OP_MATBIAS) {
+    net.passBias = b.matbias("gpoolToPassBias");
+    net.passAct = b.act("passActivation");
+    net.passMul2 = b.matmul("gpoolToPassMul2");
+  }
+  // Value head
+  b.take(KGH_OP_VALUE_HEAD, "value head");
+  Builder::ConvRec v1 = b.convRec("v1Conv");
+  BNAct v1BN = b.bnAct("v1BN");
+  net.v2Mul = b.matmul("v2Mul");
+  net.v2Bias = b.matbias("v2Bias");
+  net.v2Act = b.act("v2Activation");
+  net.v3Mul = b.matmul("v3Mul");
+  net.v3Bias = b.matbias("v3Bias");
+  net.sv3Mul = b.matmul("sv3Mul");
+  net.sv3Bias = b.matbias("sv3Bias");
+  Builder::ConvRec own = b.convRec("vOwnershipConv");
+  if(b.pos != b.n) invalid("layer program has trailing records");
+
+  net.p1C = p1.cout;
+  net.g1C = g1.cout;
+  net.v1C = v1.cout;
+  if(p1.cin != net.trunkC || g1.cin != net.trunkC || v1.cin != net.trunkC) invalid("head conv input channels mismatch");
+  if(p1.ky != g1.ky || p1.kx != g1.kx || p1.ky != v1.ky || p1.kx != v1.kx) unsupported("heads with differing p1/g1/v1 conv sizes");
+  if(p2.ky != 1 || p2.kx != 1 || own.ky != 1 || own.kx != 1) unsupported("heads with non-1x1 p2 or ownership convs");
+  if(p2.cin != net.p1C || p2.cout != net.policyC || own.cin != net.v1C || own.cout != 1) invalid("head conv channel mismatch");
+  if(g1BN.C != net.g1C || v1BN.C != net.v1C || net.p1BN.C != net.p1C) invalid("head BN channel mismatch");
+  if(net.gpoolToBiasMul.cin != 3 * net.g1C || net.gpoolToBiasMul.cout != net.p1C) invalid("gpoolToBiasMul shape mismatch");
+  if(net.v2Mul.cin != 3 * net.v1C || net.v3Mul.cin != net.v2Mul.cout || net.v3Mul.cout != 3 || net.sv3Mul.cout != net.scoreC)
+    invalid("value head shape mismatch");
+  net.p2W = b.dev(*p2.l, 0, (int64_t)p2.cin * p2.cout, "p2Conv");
+  net.ownW = b.dev(*own.l, 0, own.cin, "vOwnershipConv");
+
+  // Combined head conv(s): [p1 | g1 | v1] when g1 and v1 share an activation.
+  size_t per = (size_t)net.trunkC * p1.ky * p1.kx;
+  auto convPart = [&](const Builder::ConvRec& c) { return b.host(*c.l, 0); };
+  std::vector<float> headScale, headBias;
+  if(g1BN.act == v1BN.act) {
+    std::vector<float> cat(per * (net.p1C + net.g1C + net.v1C));
+    memcpy(cat.data(), convPart(p1), per * net.p1C * sizeof(float));
+    memcpy(cat.data() + per * net.p1C, convPart(g1), per * net.g1C * sizeof(float));
+    memcpy(cat.data() + per * (net.p1C + net.g1C), convPart(v1), per * net.v1C * sizeof(float));
+    std::vector<float> sc(net.g1C + net.v1C), bi(net.g1C + net.v1C);
+    KGH_HIP_CHECK(hipMemcpy(sc.data(), g1BN.scale, net.g1C * sizeof(float), hipMemcpyDeviceToHost));
+    KGH_HIP_CHECK(hipMemcpy(sc.data() + net.g1C, v1BN.scale, net.v1C * sizeof(float), hipMemcpyDeviceToHost));
+    KGH_HIP_CHECK(hipMemcpy(bi.data(), g1BN.bias, net.g1C * sizeof(float), hipMemcpyDeviceToHost));
+    KGH_HIP_CHECK(hipMemcpy(bi.data() + net.g1C, v1BN.bias, net.v1C * sizeof(float), hipMemcpyDeviceToHost));
+    HeadConv hc;
+    hc.conv = b.makeConv(b.upload(cat), p1.ky, p1.kx, net.trunkC, net.p1C + net.g1C + net.v1C, false);
+    hc.rawEnd = net.p1C;
+    hc.actBegin = net.p1C;
+    hc.actDstOffset = 0;
+    hc.act.C = net.g1C + net.v1C;
+    hc.act.scale = b.upload(sc);
+    hc.act.bias = b.upload(bi);
+    hc.act.act = g1BN.act;
+    net.headConvs.push_back(hc);
+  }
+  else {
+    std::vector<float> cat(per * (net.p1C + net.g1C));
+    memcpy(cat.data(), convPart(p1), per * net.p1C * sizeof(float));
+    memcpy(cat.data() + per * net.p1C, convPart(g1), per * net.g1C * sizeof(float));
+    HeadConv a;
+    a.conv = b.makeConv(b.upload(cat), p1.ky, p1.kx, net.trunkC, net.p1C + net.g1C, false);
+    a.rawEnd = net.p1C;
+    a.actBegin = net.p1C;
+    a.actDstOffset = 0;
+    a.act = g1BN;
+    net.headConvs.push_back(a);
+    HeadConv v;
+    v.conv = b.makeConv(b.dev(*v1.l, 0, (int64_t)per * net.v1C, "v1Conv"), v1.ky, v1.kx, net.trunkC, net.v1C, false);
+    v.rawEnd = 0;
+    v.actBegin = 0;
+    v.actDstOffset = net.g1C;
+    v.act = v1BN;
+    net.headConvs.push_back(v);
+  }
+  KGH_HIP_CHECK(hipStreamSynchronize(stream));
+}
+
+void requireModel(kgh_model* m) {
+  if(m == nullptr) invalid("null model");
+}
+void requireHandle(kgh_handle* h) {
+  if(h == nullptr) invalid("null handle");
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+
+extern "C" {
+
+int32_t kgh_output_row_floats(int32_t nn_x, int32_t nn_y, int32_t num_score_value_channels) {
+  return nn_x * nn_y * 2 + 1 + 3 + num_score_value_channels;
+}
+
+const char* kgh_last_error(void) { return g_lastError.c_str(); }
+
+int kgh_device_count(int32_t* count) {
+  return guarded([&] {
+    if(count == nullptr) invalid("null count");
+    int c = 0;
+    hipError_t e = hipGetDeviceCount(&c);
+    if(e != hipSuccess) c = 0;
+    *count = c;
+  });
+}
+
+int kgh_device_info(int32_t device, char* buf, int32_t buflen) {
+  return guarded([&] {
+    if(buf == nullptr || buflen <= 0) invalid("null buffer");
+    hipDeviceProp_t p;
+    KGH_HIP_CHECK(hipGetDeviceProperties(&p, device));
+    snprintf(buf, (size_t)buflen, "%s (%s), %d CUs, %.1f GiB", p.name, p.gcnArchName, p.multiProcessorCount,
+             (double)p.totalGlobalMem / (1024.0 * 1024.0 * 1024.0));
+  });
+}
+
+int kgh_model_create(int32_t device, const kgh_model_desc* desc, int32_t use_fp16, kgh_model** out) {
+  return guarded([&] {
+    if(desc == nullptr || out == nullptr) invalid("null argument");
+    if(desc->layers == nullptr || desc->num_layers <= 0) invalid("empty layer program");
+    if(desc->weights == nullptr && desc->num_weights > 0) invalid("null weights");
+    *out = nullptr;
+    KGH_HIP_CHECK(hipSetDevice(device));
+    std::unique_ptr<kgh_model> m(new kgh_model());
+    m->device = device;
+    m->net.fp16 = use_fp16 != 0;
+    hipStream_t s;
+    KGH_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    try {
+      buildNet(m.get(), desc, s);
+    }
+    catch(...) {
+      (void)hipStreamDestroy(s);
+      throw;
+    }
+    KGH_HIP_CHECK(hipStreamDestroy(s));
+    *out = m.release();
+  });
+}
+
+int kgh_model_free(kgh_model* model) {
+  return guarded([&] {
+    if(model == nullptr) return;
+    (void)hipSetDevice(model->device);
+    delete model;
+  });
+}
+
+int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t nn_y, int32_t require_exact_nn_len, kgh_handle** out) {
+  return guarded([&] {
+    requireModel(model);
+    if(out == nullptr) invalid("null out");
+    if(max_batch <= 0) invalid("max_batch must be positive");
+    if(nn_x <= 0 || nn_y <= 0 || nn_x > 64 || nn_y > 64) invalid("nn_x and nn_y must be in 1..64");
+    *out = nullptr;
+    KGH_HIP_CHECK(hipSetDevice(model->device));
+    const Net& net = model->net;
+    std::unique_ptr<kgh_handle> h(new kgh_handle());
+    h->model = model;
+    h->maxBatch = max_batch;
+    h->H = nn_y;
+    h->W = nn_x;
+    h->exact = require_exact_nn_len != 0;
+    KGH_HIP_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+    const size_t M = (size_t)max_batch * nn_x * nn_y;
+    const size_t es = net.fp16 ? 2 : 4;
+    DeviceArena& a = h->arena;
+    h->x0 = a.alloc(M * net.inputCPad * es);
+    h->mask = a.allocN<float>(M);
+    h->maskSum = a.allocN<float>(max_batch);
+    h->gbias = a.allocN<float>((size_t)max_batch * net.trunkC);
+    for(int c : net.depthC) {
+      h->R.push_back(a.alloc(M * c * es));
+      h->A.push_back(a.alloc(M * c * es));
+    }
+    size_t tmpC = std::max(net.tmpC, 1);
+    h->tmp1 = a.alloc(M * tmpC * es);
+    h->tmp2 = a.alloc(M * tmpC * es);
+    h->tmp3 = a.alloc(M * tmpC * es);
+    h->nbias = a.allocN<float>((size_t)max_batch * tmpC);
+    h->p1 = a.alloc(M * net.p1C * es);
+    h->gv = a.alloc(M * (net.g1C + net.v1C) * es);
+    h->g1Bias = a.allocN<float>((size_t)max_batch * net.p1C);
+    h->pass = a.allocN<float>((size_t)max_batch * net.policyC);
+    h->value = a.allocN<float>((size_t)max_batch * 3);
+    h->score = a.allocN<float>((size_t)max_batch * net.scoreC);
+    h->policyRaw = a.allocN<float>(M * net.policyC);
+    h->ownRaw = a.allocN<float>(M);
+    h->rowFloats = kgh_output_row_floats(nn_x, nn_y, net.scoreC);
+    h->dSpatial = a.allocN<float>(M * net.inputC);
+    h->dGlobal = a.allocN<float>((size_t)max_batch * net.globalC);
+    h->dSym = a.allocN<int>(max_batch);
+    h->dOpt = a.allocN<float>(max_batch);
+    h->dOut = a.allocN<float>((size_t)max_batch * h->rowFloats);
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hSpatial, M * net.inputC * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hGlobal, (size_t)max_batch * net.globalC * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hSym, (size_t)max_batch * sizeof(int), hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hOpt, (size_t)max_batch * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hOut, (size_t)max_batch * h->rowFloats * sizeof(float), hipHostMallocDefault));
+    *out = h.release();
+  });
+}
+
+int kgh_handle_free(kgh_handle* handle) {
+  return guarded([&] {
+    if(handle == nullptr) return;
+    (void)hipSetDevice(handle->model->device);
+    (void)hipStreamSynchronize(handle->stream);
+    delete handle;
+  });
+}
+
+int kgh_forward_device(kgh_handle* handle, int32_t n, const float* d_spatial, const float* d_global, const int32_t* d_symmetry,
+                       const float* d_policy_optimism, float* d_out) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
+    if(!d_spatial || !d_global || !d_symmetry || !d_policy_optimism || !d_out) invalid("null device pointer");
+    KGH_HIP_CHECK(hipSetDevice(handle->model->device));
+    if(handle->model->net.fp16)
+      forwardImpl<half_t>(handle, n, d_spatial, d_global, d_symmetry, d_policy_optimism, d_out);
+    else
+      forwardImpl<float>(handle, n, d_spatial, d_global, d_symmetry, d_policy_optimism, d_out);
+  });
+}
+
+int kgh_forward(kgh_handle* handle, int32_t n, const float* spatial, const float* global_in, const int32_t* symmetry,
+                const float* policy_optimism, float* out) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
+    if(!spatial || !global_in || !symmetry || !policy_optimism || !out) invalid("null host pointer");
+    for(int i = 0; i < n; i++)
+      if(symmetry[i] < 0 || symmetry[i] > 7) invalid("symmetry must be in 0..7");
+    KGH_HIP_CHECK(hipSetDevice(handle->model->device));
+    const Net& net = handle->model->net;
+    const size_t HW = (size_t)handle->H * handle->W;
+    const size_t spatialBytes = (size_t)n * HW * net.inputC * sizeof(float);
+    const size_t globalBytes = (size_t)n * net.globalC * sizeof(float);
+    memcpy(handle->hSpatial, spatial, spatialBytes);
+    memcpy(handle->hGlobal, global_in, globalBytes);
+    memcpy(handle->hSym, symmetry, (size_t)n * sizeof(int));
+    memcpy(handle->hOpt, policy_optimism, (size_t)n * sizeof(float));
+    hipStream_t s = handle->stream;
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->dSpatial, handle->hSpatial, spatialBytes, hipMemcpyHostToDevice, s));
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->dGlobal, handle->hGlobal, globalBytes, hipMemcpyHostToDevice, s));
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->dSym, handle->hSym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->dOpt, handle->hOpt, (size_t)n * sizeof(float), hipMemcpyHostToDevice, s));
+    if(net.fp16)
+      forwardImpl<half_t>(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
+    else
+      forwardImpl<float>(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
+    const size_t outBytes = (size_t)n * handle->rowFloats * sizeof(float);
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->hOut, handle->dOut, outBytes, hipMemcpyDeviceToHost, s));
+    KGH_HIP_CHECK(hipStreamSynchronize(s));
+    memcpy(out, handle->hOut, outBytes);
+  });
+}
+
+int kgh_handle_synchronize(kgh_handle* handle) {
+  return guarded([&] {
+    requireHandle(handle);
+    KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
+  });
+}
+
+int kgh_device_alloc(int32_t device, size_t bytes, void** ptr) {
+  return guarded([&] {
+    if(ptr == nullptr) invalid("null ptr");
+    KGH_HIP_CHECK(hipSetDevice(device));
+    KGH_HIP_CHECK(hipMalloc(ptr, std::max<size_t>(bytes, 256)));
+  });
+}
+int kgh_device_free(void* ptr) {
+  return guarded([&] {
+    if(ptr != nullptr) KGH_HIP_CHECK(hipFree(ptr));
+  });
+}
+int kgh_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  return guarded([&] { KGH_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice)); });
+}
+int kgh_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  return guarded([&] { KGH_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost)); });
+}
+
+int kgh_handle_set_profiling(kgh_handle* handle, int32_t enabled) {
+  return guarded([&] {
+    requireHandle(handle);
+    KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
+    handle->profiling = enabled != 0;
+    handle->profUsed = 0;
+  });
+}
+
+int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32_t* launches, double* flops) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(!total_ms || !launches || !flops) invalid("null output");
+    KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
+    double ms = 0, fl = 0;
+    int cnt = 0;
+    for(size_t i = 0; i < handle->profUsed; i++) {
+      const ProfRec& r = handle->prof[i];
+      if(kind != 2 && r.kind != kind) continue;
+      float e = 0;
+      KGH_HIP_CHECK(hipEventElapsedTime(&e, r.start, r.stop));
+      ms += e;
+      fl += r.flops;
+      cnt++;
+    }
+    *total_ms = ms;
+    *launches = cnt;
+    *flops = fl;
+  });
+}
+
+int kgh_selftest_mfma(int32_t device) {
+  return guarded([&] {
+    KGH_HIP_CHECK(hipSetDevice(device));
+    int bad = kgh::runMfmaSelfTest();
+    if(bad != 0) throw KghError(KGH_ERR_INTERNAL, "matrix-core layout self-test: " + std::to_string(bad) + " mismatching elements");
+  });
+}
+
+int kgh_evaluate_layers(int32_t device, const kgh_layer* layers, int32_t num_layers, const float* weights, int64_t num_weights,
+                        int32_t use_fp16, int32_t batch, int32_t nn_x, int32_t nn_y, const float* input, const float* mask,
+                        float* output) {
+  return guarded([&] {
+    if(layers == nullptr || num_layers <= 0 || input == nullptr || output == nullptr) invalid("null argument");
+    if(batch <= 0 || nn_x <= 0 || nn_y <= 0) invalid("bad geometry");
+    KGH_HIP_CHECK(hipSetDevice(device));
+    kgh_model model;
+    model.device = device;
+    Net& net = model.net;
+    net.fp16 = use_fp16 != 0;
+    hipStream_t s;
+    KGH_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    struct StreamGuard {
+      hipStream_t s;
+      ~StreamGuard() { (void)hipStreamDestroy(s); }
+    } guard{s};
+    const float* devW = model.arena.allocN<float>((size_t)std::max<int64_t>(num_weights, 1));
+    if(num_weights > 0) KGH_HIP_CHECK(hipMemcpy((void*)devW, weights, (size_t)num_weights * sizeof(float), hipMemcpyHostToDevice));
+    Builder b{layers, num_layers, 0, weights, num_weights, devW, model.arena, net.fp16, s};
+    DeviceArena& a = model.arena;
+    const int HW = nn_x * nn_y;
+    const size_t M = (size_t)batch * HW;
+    const size_t es = net.fp16 ? 2 : 4;
+    float* dMask = a.allocN<float>(M);
+    float* dMaskSum = a.allocN<float>(batch);
+    {
+      std::vector<float> hm(M, 1.0f);
+      if(mask != nullptr) memcpy(hm.data(), mask, M * sizeof(float));
+      KGH_HIP_CHECK(hipMemcpy(dMask, hm.data(), M * sizeof(float), hipMemcpyHostToDevice));
+      std::vector<float> ms(batch, 0.0f);
+      for(int i = 0; i < batch; i++)
+        for(int p = 0; p < HW; p++) ms[i] += hm[(size_t)i * HW + p];
+      KGH_HIP_CHECK(hipMemcpy(dMaskSum, ms.data(), batch * sizeof(float), hipMemcpyHostToDevice));
+    }
+    int op = b.peek();
+    int inC = 0, outC = 0;
+    ConvW cw;
+    BNAct bn;
+    Block blk;
+    if(op == KGH_OP_CONV) {
+      cw = b.conv("conv");
+      inC = cw.cin;
+      outC = cw.cout;
+    }
+    else if(op == KGH_OP_BN) {
+      bn = b.bnAct("batchnorm");
+      inC = outC = bn.C;
+    }
+    else {
+      net.depthC.assign(1, 0);
+      const kgh_layer& first = layers[0];
+      if(first.op == KGH_OP_BLOCK_ORDINARY || first.op == KGH_OP_BLOCK_GPOOL || first.op == KGH_OP_BLOCK_NBT) {
+        // stream channels come from the block's preBN
+        int c = layers[1].op == KGH_OP_BN ? layers[1].i[0] : 0;
+        net.depthC[0] = c;
+        blk = b.block(net, 0, c);
+        inC = outC = c;
+      }
+      else {
+        invalid("kgh_evaluate_layers: program must be a CONV, a BN+ACT pair or one block");
+      }
+    }
+    if(b.pos != b.n) invalid("kgh_evaluate_layers: trailing records in program");
+
+    auto run = [&](auto tag) {
+      using T = decltype(tag);
+      T* x = (T*)a.alloc(M * inC * es);
+      float* xf = a.allocN<float>(M * std::max(inC, outC));
+      KGH_HIP_CHECK(hipMemcpy(xf, input, M * inC * sizeof(float), hipMemcpyHostToDevice));
+      kgh::launchConvertFromFloat<T>(xf, x, M * inC, s);
+      BoardGeom g{batch, nn_y, nn_x};
+      T* y = (T*)a.alloc(M * outC * es);
+      if(op == KGH_OP_CONV) {
+        ConvEpilogue<T> e;
+        memset(&e, 0, sizeof(e));
+        e.outRaw = y;
+        e.ldRaw = outC;
+        e.rawEnd = outC;
+        e.actBegin = INT_MAX;
+        e.mask = dMask;
+        kgh::launchConv<T>(x, inC, cw.cin, cw.cinPad, cw.cout, cw.ky, cw.kx, cw.wPrep, cw.wDirect, g, e, s, nullptr);
+      }
+      else if(op == KGH_OP_BN) {
+        kgh::launchBnAct<T>(x, inC, y, outC, bn.C, bn.scale, bn.bias, bn.act, dMask, nullptr, 0, HW, (int)M, s);
+      }
+      else {
+        std::vector<T*> R{x}, A{(T*)a.alloc(M * inC * es)};
+        for(size_t d = 1; d < net.depthC.size(); d++) {
+          R.push_back((T*)a.alloc(M * net.depthC[d] * es));
+          A.push_back((T*)a.alloc(M * net.depthC[d] * es));
+        }
+        size_t tmpC = std::max(net.tmpC, 1);
+        Runner<T> r{net, nullptr, s, g, (int)M, dMask, dMaskSum, R, A, inC, (T*)a.alloc(M * tmpC * es),
+                    (T*)a.alloc(M * tmpC * es), (T*)a.alloc(M * tmpC * es), a.allocN<float>((size_t)batch * tmpC)};
+        r.bnAct(x, inC, A[0], inC, blk.preBN, nullptr, 0);
+        std::vector<Block> blocks;
+        blocks.push_back(std::move(blk));
+        r.runStack(blocks, 0, nullptr);
+        y = x;
+      }
+      kgh::launchConvertToFloat<T>(y, xf, M * outC, s);
+      KGH_HIP_CHECK(hipStreamSynchronize(s));
+      KGH_HIP_CHECK(hipMemcpy(output, xf, M * outC * sizeof(float), hipMemcpyDeviceToHost));
+    };
+    if(net.fp16) run(half_t());
+    else run(float());
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+// Shared definitions for the gfx950 kernels of libkatago_hip.so.
+#ifndef KGH_COMMON_H
+#define KGH_COMMON_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+typedef _Float16 half_t;
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Activation codes, identical to the model format's (activations.h).
+enum : int {
+  KGH_ACT_IDENTITY = 0,
+  KGH_ACT_RELU = 1,
+  KGH_ACT_MISH = 2,
+  KGH_ACT_SILU = 3,
+  KGH_ACT_MISH_SCALE8 = 12,
+};
+
+// Error raised by host-side library code; converted to a status code and
+// thread-local message at the C-ABI boundary.
+struct KghError : public std::runtime_error {
+  int code;
+  KghError(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define KGH_HIP_CHECK(expr)                                                                          \
+  do {                                                                                               \
+    hipError_t kgh_e_ = (expr);                                                                      \
+    if(kgh_e_ != hipSuccess)                                                                         \
+      throw KghError(2, std::string(#expr) + " failed: " + hipGetErrorString(kgh_e_) + " (" +       \
+                          __FILE__ + ":" + std::to_string(__LINE__) + ")");                          \
+  } while(0)
+
+#define KGH_CHECK_LAUNCH() KGH_HIP_CHECK(hipGetLastError())
+
+// ---------------------------------------------------------------------------
+// Activations in fp32, with the reference's formulas:
+//   mish(x) = x * tanh(log1p(exp(min(x,20))) + max(x,20) - 20)   (eigenbackend.cpp:754)
+//   mish_scale8(x) = x * tanh(softplus(8x))                       (activations.h:16)
+//   silu(x) = x / (1 + exp(-x))                                   (eigenbackend.cpp:756)
+__device__ __forceinline__ float kgh_softplus_clamped(float x) {
+  return log1pf(expf(fminf(x, 20.0f))) + fmaxf(x, 20.0f) - 20.0f;
+}
+
+__device__ __forceinline__ float kgh_activate(float x, int act) {
+  switch(act) {
+    case KGH_ACT_RELU: return fmaxf(x, 0.0f);
+    case KGH_ACT_MISH: return x * tanhf(kgh_softplus_clamped(x));
+    case KGH_ACT_MISH_SCALE8: return x * tanhf(kgh_softplus_clamped(8.0f * x));
+    case KGH_ACT_SILU: return x / (1.0f + expf(-x));
+    default: return x;
+  }
+}
+
+template<typename T> __device__ __forceinline__ float kgh_to_float(T v) { return (float)v; }
+template<typename T> __device__ __forceinline__ T kgh_from_float(float v) { return (T)v; }
+
+// ---------------------------------------------------------------------------
+// Convolution epilogue contract shared by the conv kernels.
+//
+// For output element (m, c) with accumulator acc:
+//   v = acc + (ncBias ? ncBias[n*ldNC + c] : 0)
+//   if residual:  v = residual[m*ldRes + c] + (maskResidualAdd ? v*mask[m] : v)
+//   if c <  rawEnd:   outRaw[m*ldRaw + c]             = v
+//   if c >= actBegin: outAct[m*ldAct + c - actBegin]  = act(v*actScale[c-actBegin] + actBias[c-actBegin]) * mask[m]
+// This expresses every fusion point of the KataGo blocks: next-layer folded
+// BN + activation + mask, residual accumulation, the per-(n,c) bias of the
+// global-input matmul, and the raw/activated split of a combined
+// regular+gpool convolution.
+template<typename T>
+struct ConvEpilogue {
+  T* outRaw;
+  int ldRaw;
+  int rawEnd;
+  T* outAct;
+  int ldAct;
+  int actBegin;
+  const float* actScale;
+  const float* actBias;
+  int actKind;
+  const float* mask;
+  const T* residual;
+  int ldRes;
+  int maskResidualAdd;
+  const float* ncBias;
+  int ldNC;
+};
+
+template<typename T>
+__device__ __forceinline__ void kgh_epilogue_store(const ConvEpilogue<T>& e, int m, int n, int c, float acc) {
+  float v = acc;
+  if(e.ncBias != nullptr) v += e.ncBias[(size_t)n * e.ldNC + c];
+  if(e.residual != nullptr) {
+    float r = kgh_to_float(e.residual[(size_t)m * e.ldRes + c]);
+    v = e.maskResidualAdd ? r + v * e.mask[m] : r + v;
+  }
+  if(c < e.rawEnd) e.outRaw[(size_t)m * e.ldRaw + c] = kgh_from_float<T>(v);
+  if(c >= e.actBegin && e.outAct != nullptr) {
+    int ca = c - e.actBegin;
+    float a = kgh_activate(v * e.actScale[ca] + e.actBias[ca], e.actKind);
+    e.outAct[(size_t)m * e.ldAct + ca] = kgh_from_float<T>(a * e.mask[m]);
+  }
+}
+
+// Geometry of a batch of boards in NHWC: M = batch*H*W rows.
+struct BoardGeom {
+  int batch;
+  int H;
+  int W;
+};
+
+// Host-side launchers (definitions in kgh_conv.hip / kgh_kernels.hip).
+namespace kgh {
+
+// Conv of x[M, cinStride] (first cin channels used) with weights prepared by
+// prepareConvWeights into layout [tap][cout][cinPad]; dispatches to the
+// matrix-core kernel when the shape allows, else to the direct kernel.
+template<typename T>
+void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky, int kx, const void* wPrepared,
+                const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma);
+
+template<typename T>
+bool convMfmaSupported(int cinPad, int cout);
+
+// Converts fp32 weights (oc, ic, y, x) to the kernel layout [tap][oc][cinPad]
+// of type T on device (zero-padded channels).
+template<typename T>
+void prepareConvWeights(const float* dWeightsOIYX, T* dOut, int cout, int cin, int cinPad, int ky, int kx, hipStream_t stream);
+
+template<typename T>
+void launchConvertFromFloat(const float* src, T* dst, size_t n, hipStream_t stream);
+template<typename T>
+void launchConvertToFloat(const T* src, float* dst, size_t n, hipStream_t stream);
+
+}  // namespace kgh
+
+#endif

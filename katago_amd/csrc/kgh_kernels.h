@@ -1,0 +1,93 @@
+// Argument structs and launchers for the non-conv kernels (kgh_kernels.hip).
+#ifndef KGH_KERNELS_H
+#define KGH_KERNELS_H
+
+#include "kgh_common.h"
+
+template<typename T>
+struct HeadRowArgs {
+  const T* g1;  // activated g1 channels, row stride ldG1
+  int ldG1;
+  const T* v1;  // activated v1 channels, row stride ldV1
+  int ldV1;
+  int g1C, v1C, p1C, policyC, passHidden, v2C, scoreC, hiddenMax, HW;
+  const float* mask;
+  const float* maskSum;
+  const float* gpoolToBiasMul;  // [3*g1C][p1C]
+  const float* passMul;         // [3*g1C][passHidden] (v>=15) or [3*g1C][policyC]
+  const float* passBias;        // [passHidden] or null
+  int passAct;
+  const float* passMul2;        // [passHidden][policyC] or null (model version < 15)
+  const float* v2Mul;           // [3*v1C][v2C]
+  const float* v2Bias;
+  int v2Act;
+  const float* v3Mul;           // [v2C][3]
+  const float* v3Bias;
+  const float* sv3Mul;          // [v2C][scoreC]
+  const float* sv3Bias;
+  float* g1Bias;                // out [batch][p1C]
+  float* pass;                  // out [batch][policyC]
+  float* value;                 // out [batch][3]
+  float* score;                 // out [batch][scoreC]
+};
+
+template<typename T>
+struct HeadSpatialArgs {
+  const T* p1;  // raw p1 conv output
+  int ldP1;
+  const T* v1;  // activated v1
+  int ldV1;
+  int p1C, v1C, policyC, M, HW;
+  const float* g1Bias;
+  const float* p1Scale;
+  const float* p1Bias;
+  int p1Act;
+  const float* p2W;   // [policyC][p1C]
+  const float* ownW;  // [v1C]
+  const float* mask;
+  float* policy;     // out [M][policyC]
+  float* ownership;  // out [M]
+};
+
+struct UnpackArgs {
+  const float* policy;  // [M][policyC]
+  const float* pass;    // [batch][policyC]
+  const float* value;   // [batch][3]
+  const float* score;   // [batch][scoreC]
+  const float* ownership;  // [M]
+  const int* sym;
+  const float* optimism;
+  int policyC, scoreC, mixOptimism, batch, H, W, rowFloats;
+  float* out;
+};
+
+namespace kgh {
+
+template<typename T>
+void launchPackInputs(const float* spatial, const int* sym, int batch, int H, int W, int cin, T* x, int cinPad, float* mask,
+                      float* maskSum, hipStream_t stream);
+
+void launchRowMatmul(const float* in, int ldIn, int cin, const float* Wt, int cout, const float* bias, int act, float* out,
+                     int ldOut, int batch, hipStream_t stream);
+
+template<typename T>
+void launchPool(const T* g, int ldG, int C, const float* mask, const float* maskSum, int batch, int HW, bool valueMode,
+                float* pooledOut, int ldPooled, const float* Wt, int cout, float* out, int ldOut, hipStream_t stream);
+
+template<typename T>
+void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, const float* bias, int act, const float* mask,
+                 const float* ncBias, int ldNC, int HW, int M, hipStream_t stream);
+
+template<typename T>
+void launchHeadRow(const HeadRowArgs<T>& a, int batch, hipStream_t stream);
+
+template<typename T>
+void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream);
+
+void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream);
+
+int runMfmaSelfTest();
+
+}  // namespace kgh
+
+#endif

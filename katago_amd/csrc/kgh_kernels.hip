@@ -1,0 +1,373 @@
+// Memory-bound and small kernels of the forward pass: input packing with the
+// dihedral symmetry applied on device, mask sums, masked global pooling fused
+// with its bias matvec, standalone folded-BN + activation + mask, the policy
+// and value heads, and output unpacking with inverse symmetry.
+#include "kgh_kernels.h"
+
+#include <climits>
+
+namespace {
+
+// Destination of source cell (h, w) under symmetry, following
+// SymmetryHelpers::copy{Inputs,Outputs}WithSymmetry (nninputs.cpp:529-597):
+// bit0 flips y, bit1 flips x, bit2 transposes (square boards only). For
+// inputs the flips act before the transpose, for outputs (reverse) after.
+__device__ __forceinline__ void symDest(int h, int w, int H, int W, int sym, bool reverse, int& hd, int& wd) {
+  bool transpose = (sym & 4) != 0 && H == W;
+  bool flipX = (sym & 2) != 0;
+  bool flipY = (sym & 1) != 0;
+  if(transpose && !reverse) {
+    bool t = flipX;
+    flipX = flipY;
+    flipY = t;
+  }
+  if(transpose) {
+    hd = flipY ? H - 1 - w : w;
+    wd = flipX ? W - 1 - h : h;
+  }
+  else {
+    hd = flipY ? H - 1 - h : h;
+    wd = flipX ? W - 1 - w : w;
+  }
+}
+
+template<typename T>
+__global__ void packInputsKernel(const float* __restrict__ spatial, const int* __restrict__ sym, int batch, int H, int W,
+                                 int cin, T* __restrict__ x, int cinPad, float* __restrict__ mask) {
+  int HW = H * W;
+  int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= batch * HW) return;
+  int n = idx / HW;
+  int s = idx - n * HW;
+  int h = s / W;
+  int w = s - h * W;
+  int hd, wd;
+  symDest(h, w, H, W, sym[n], false, hd, wd);
+  int md = n * HW + hd * W + wd;
+  const float* src = spatial + (size_t)idx * cin;
+  T* dst = x + (size_t)md * cinPad;
+  for(int c = 0; c < cin; c++) dst[c] = (T)src[c];
+  for(int c = cin; c < cinPad; c++) dst[c] = (T)0.0f;
+  mask[md] = src[0];
+}
+
+__global__ void maskSumKernel(const float* __restrict__ mask, int HW, float* __restrict__ maskSum) {
+  __shared__ float part[256];
+  int n = blockIdx.x;
+  float s = 0.0f;
+  for(int i = threadIdx.x; i < HW; i += blockDim.x) s += mask[(size_t)n * HW + i];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for(int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
+    if((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
+    __syncthreads();
+  }
+  if(threadIdx.x == 0) maskSum[n] = part[0];
+}
+
+// out[n, co] = act(sum_i in[n, i] * W[i, co] + bias[co]); W ic-major.
+__global__ void rowMatmulKernel(const float* __restrict__ in, int ldIn, int cin, const float* __restrict__ Wt, int cout,
+                                const float* __restrict__ bias, int act, float* __restrict__ out, int ldOut, int batch) {
+  int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= batch * cout) return;
+  int n = idx / cout;
+  int co = idx - n * cout;
+  float acc = 0.0f;
+  for(int i = 0; i < cin; i++) acc += in[(size_t)n * ldIn + i] * Wt[(size_t)i * cout + co];
+  if(bias != nullptr) acc += bias[co];
+  out[(size_t)n * ldOut + co] = kgh_activate(acc, act);
+}
+
+// Masked pooling of C channels of g (already activated and zeroed off-board)
+// into pooled[n, 3C], following poolRowsGPool / poolRowsValueHead
+// (eigenbackend.cpp:152-197):
+//   [mean, mean*(sqrt(S)-14)*0.1, third]
+// where S = maskSum[n] and third is max(-1, max_m(g + mask - 1)) for gpool
+// or mean*((sqrt(S)-14)^2*0.01 - 0.1) for the value head.
+// Then, if Wt != nullptr, out[n, co] = sum_i pooled[n,i] * Wt[i, co].
+template<typename T, bool VALUE_MODE>
+__global__ void poolKernel(const T* __restrict__ g, int ldG, int C, const float* __restrict__ mask,
+                           const float* __restrict__ maskSum, int HW, float* __restrict__ pooledOut, int ldPooled,
+                           const float* __restrict__ Wt, int cout, float* __restrict__ out, int ldOut) {
+  extern __shared__ float smem[];
+  const int n = blockIdx.x;
+  const int groups = blockDim.x / C > 0 ? blockDim.x / C : 1;
+  float* psum = smem;                   // [groups][C]
+  float* pmax = smem + groups * C;      // [groups][C]
+  float* pooled = smem + 2 * groups * C;  // [3C]
+  for(int t = threadIdx.x; t < groups * C; t += blockDim.x) {
+    int grp = t / C;
+    int c = t - grp * C;
+    float s = 0.0f;
+    float mx = -1.0f;
+    for(int p = grp; p < HW; p += groups) {
+      size_t m = (size_t)n * HW + p;
+      float v = kgh_to_float(g[m * ldG + c]);
+      s += v;
+      if(!VALUE_MODE) mx = fmaxf(mx, v + (mask[m] - 1.0f));
+    }
+    psum[t] = s;
+    pmax[t] = mx;
+  }
+  __syncthreads();
+  const float div = maskSum[n];
+  const float sq = sqrtf(div) - 14.0f;
+  for(int c = threadIdx.x; c < C; c += blockDim.x) {
+    float s = 0.0f;
+    float mx = -1.0f;
+    for(int grp = 0; grp < groups; grp++) {
+      s += psum[grp * C + c];
+      mx = fmaxf(mx, pmax[grp * C + c]);
+    }
+    float mean = s / div;
+    pooled[c] = mean;
+    pooled[c + C] = mean * sq * 0.1f;
+    pooled[c + 2 * C] = VALUE_MODE ? mean * (sq * sq * 0.01f - 0.1f) : mx;
+  }
+  __syncthreads();
+  if(pooledOut != nullptr)
+    for(int i = threadIdx.x; i < 3 * C; i += blockDim.x) pooledOut[(size_t)n * ldPooled + i] = pooled[i];
+  if(Wt != nullptr) {
+    for(int co = threadIdx.x; co < cout; co += blockDim.x) {
+      float acc = 0.0f;
+      for(int i = 0; i < 3 * C; i++) acc += pooled[i] * Wt[(size_t)i * cout + co];
+      out[(size_t)n * ldOut + co] = acc;
+    }
+  }
+}
+
+// y[m, c] = act((x[m, c] + ncBias[n, c]) * scale[c] + bias[c]) * mask[m]
+template<typename T>
+__global__ void bnActKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ scale,
+                            const float* __restrict__ bias, int act, const float* __restrict__ mask,
+                            const float* __restrict__ ncBias, int ldNC, int HW, long total) {
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= total) return;
+  int m = (int)(idx / C);
+  int c = (int)(idx - (long)m * C);
+  float v = kgh_to_float(x[(size_t)m * ldX + c]);
+  if(ncBias != nullptr) v += ncBias[(size_t)(m / HW) * ldNC + c];
+  float a = kgh_activate(v * scale[c] + bias[c], act);
+  y[(size_t)m * ldY + c] = kgh_from_float<T>(a * mask[m]);
+}
+
+// Small per-row part of the heads (eigenbackend.cpp:1980-2024, 2067-2102),
+// one workgroup per batch row.
+template<typename T>
+__global__ void headRowKernel(HeadRowArgs<T> a) {
+  extern __shared__ float smem[];
+  const int n = blockIdx.x;
+  const int HW = a.HW;
+  const int G1 = a.g1C, V1 = a.v1C;
+  float* gpool = smem;              // [3*G1]
+  float* vpool = gpool + 3 * G1;    // [3*V1]
+  float* hidden = vpool + 3 * V1;   // [max(p1C, v2C)]
+  float* scratch = hidden + a.hiddenMax;  // partial sums: [blockDim.x]
+
+  // Pool g1 (gpool formula) and v1 (value formula) channels.
+  const float div = a.maskSum[n];
+  const float sq = sqrtf(div) - 14.0f;
+  for(int c = threadIdx.x; c < G1 + V1; c += blockDim.x) {
+    const bool isG = c < G1;
+    const T* src = isG ? a.g1 : a.v1;
+    const int ld = isG ? a.ldG1 : a.ldV1;
+    const int cc = isG ? c : c - G1;
+    float s = 0.0f;
+    float mx = -1.0f;
+    for(int p = 0; p < HW; p++) {
+      size_t m = (size_t)n * HW + p;
+      float v = kgh_to_float(src[m * ld + cc]);
+      s += v;
+      mx = fmaxf(mx, v + (a.mask[m] - 1.0f));
+    }
+    float mean = s / div;
+    if(isG) {
+      gpool[cc] = mean;
+      gpool[cc + G1] = mean * sq * 0.1f;
+      gpool[cc + 2 * G1] = mx;
+    }
+    else {
+      vpool[cc] = mean;
+      vpool[cc + V1] = mean * sq * 0.1f;
+      vpool[cc + 2 * V1] = mean * (sq * sq * 0.01f - 0.1f);
+    }
+  }
+  __syncthreads();
+
+  // Policy bias from the g1 pool.
+  for(int co = threadIdx.x; co < a.p1C; co += blockDim.x) {
+    float acc = 0.0f;
+    for(int i = 0; i < 3 * G1; i++) acc += gpool[i] * a.gpoolToBiasMul[(size_t)i * a.p1C + co];
+    a.g1Bias[(size_t)n * a.p1C + co] = acc;
+  }
+  // Pass logit(s).
+  if(a.passMul2 != nullptr) {
+    for(int co = threadIdx.x; co < a.passHidden; co += blockDim.x) {
+      float acc = 0.0f;
+      for(int i = 0; i < 3 * G1; i++) acc += gpool[i] * a.passMul[(size_t)i * a.passHidden + co];
+      hidden[co] = kgh_activate(acc + a.passBias[co], a.passAct);
+    }
+    __syncthreads();
+    for(int co = threadIdx.x; co < a.policyC; co += blockDim.x) {
+      float acc = 0.0f;
+      for(int i = 0; i < a.passHidden; i++) acc += hidden[i] * a.passMul2[(size_t)i * a.policyC + co];
+      a.pass[(size_t)n * a.policyC + co] = acc;
+    }
+  }
+  else {
+    for(int co = threadIdx.x; co < a.policyC; co += blockDim.x) {
+      float acc = 0.0f;
+      for(int i = 0; i < 3 * G1; i++) acc += gpool[i] * a.passMul[(size_t)i * a.policyC + co];
+      a.pass[(size_t)n * a.policyC + co] = acc;
+    }
+  }
+  __syncthreads();
+  // Value trunk: v2 = act(v2Mul * vpool + v2Bias).
+  for(int co = threadIdx.x; co < a.v2C; co += blockDim.x) {
+    float acc = 0.0f;
+    for(int i = 0; i < 3 * V1; i++) acc += vpool[i] * a.v2Mul[(size_t)i * a.v2C + co];
+    hidden[co] = kgh_activate(acc + a.v2Bias[co], a.v2Act);
+  }
+  __syncthreads();
+  for(int co = threadIdx.x; co < 3 + a.scoreC; co += blockDim.x) {
+    bool isValue = co < 3;
+    int oc = isValue ? co : co - 3;
+    const float* Wt = isValue ? a.v3Mul : a.sv3Mul;
+    int ldW = isValue ? 3 : a.scoreC;
+    float acc = 0.0f;
+    for(int i = 0; i < a.v2C; i++) acc += hidden[i] * Wt[(size_t)i * ldW + oc];
+    if(isValue) a.value[(size_t)n * 3 + oc] = acc + a.v3Bias[oc];
+    else a.score[(size_t)n * a.scoreC + oc] = acc + a.sv3Bias[oc];
+  }
+  (void)scratch;
+}
+
+// Per-position part of the heads: policy = p2Conv(act(p1BN(p1 + g1Bias)) * mask),
+// ownership = ownershipConv(v1).
+template<typename T>
+__global__ void headSpatialKernel(HeadSpatialArgs<T> a) {
+  int m = blockIdx.x * blockDim.x + threadIdx.x;
+  if(m >= a.M) return;
+  int n = m / a.HW;
+  float msk = a.mask[m];
+  float pol[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const T* p1 = a.p1 + (size_t)m * a.ldP1;
+  for(int c = 0; c < a.p1C; c++) {
+    float v = kgh_to_float(p1[c]) + a.g1Bias[(size_t)n * a.p1C + c];
+    float act = kgh_activate(v * a.p1Scale[c] + a.p1Bias[c], a.p1Act) * msk;
+    for(int pc = 0; pc < a.policyC; pc++) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
+  }
+  for(int pc = 0; pc < a.policyC; pc++) a.policy[(size_t)m * a.policyC + pc] = pol[pc];
+  const T* v1 = a.v1 + (size_t)m * a.ldV1;
+  float own = 0.0f;
+  for(int c = 0; c < a.v1C; c++) own += kgh_to_float(v1[c]) * a.ownW[c];
+  a.ownership[m] = own;
+}
+
+// Packs the per-row outputs with policy optimism mixing and inverse symmetry
+// (eigenbackend.cpp:2527-2580).
+__global__ void unpackOutputsKernel(UnpackArgs a) {
+  int HW = a.H * a.W;
+  int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= a.batch * HW) return;
+  int n = idx / HW;
+  int s = idx - n * HW;
+  int h = s / a.W;
+  int w = s - h * a.W;
+  int hd, wd;
+  symDest(h, w, a.H, a.W, a.sym[n], true, hd, wd);
+  int sd = hd * a.W + wd;
+  float* row = a.out + (size_t)n * a.rowFloats;
+  const float* pol = a.policy + (size_t)idx * a.policyC;
+  float opt = a.optimism[n];
+  float p = a.mixOptimism ? pol[0] + (pol[1] - pol[0]) * opt : pol[0];
+  row[sd] = p;
+  row[HW + 1 + 3 + a.scoreC + sd] = a.ownership[idx];
+  if(s == 0) {
+    const float* pass = a.pass + (size_t)n * a.policyC;
+    row[HW] = a.mixOptimism ? pass[0] + (pass[1] - pass[0]) * opt : pass[0];
+    for(int i = 0; i < 3; i++) row[HW + 1 + i] = a.value[(size_t)n * 3 + i];
+    for(int i = 0; i < a.scoreC; i++) row[HW + 4 + i] = a.score[(size_t)n * a.scoreC + i];
+  }
+}
+
+}  // namespace
+
+namespace kgh {
+
+template<typename T>
+void launchPackInputs(const float* spatial, const int* sym, int batch, int H, int W, int cin, T* x, int cinPad, float* mask,
+                      float* maskSum, hipStream_t stream) {
+  int total = batch * H * W;
+  hipLaunchKernelGGL(packInputsKernel<T>, dim3((total + 255) / 256), dim3(256), 0, stream, spatial, sym, batch, H, W, cin, x,
+                     cinPad, mask);
+  KGH_CHECK_LAUNCH();
+  hipLaunchKernelGGL(maskSumKernel, dim3(batch), dim3(256), 0, stream, mask, H * W, maskSum);
+  KGH_CHECK_LAUNCH();
+}
+
+void launchRowMatmul(const float* in, int ldIn, int cin, const float* Wt, int cout, const float* bias, int act, float* out,
+                     int ldOut, int batch, hipStream_t stream) {
+  int total = batch * cout;
+  hipLaunchKernelGGL(rowMatmulKernel, dim3((total + 255) / 256), dim3(256), 0, stream, in, ldIn, cin, Wt, cout, bias, act, out,
+                     ldOut, batch);
+  KGH_CHECK_LAUNCH();
+}
+
+template<typename T>
+void launchPool(const T* g, int ldG, int C, const float* mask, const float* maskSum, int batch, int HW, bool valueMode,
+                float* pooledOut, int ldPooled, const float* Wt, int cout, float* out, int ldOut, hipStream_t stream) {
+  int threads = 256;
+  int groups = threads / C > 0 ? threads / C : 1;
+  size_t smem = (size_t)(2 * groups * C + 3 * C) * sizeof(float);
+  if(valueMode)
+    hipLaunchKernelGGL((poolKernel<T, true>), dim3(batch), dim3(threads), smem, stream, g, ldG, C, mask, maskSum, HW, pooledOut,
+                       ldPooled, Wt, cout, out, ldOut);
+  else
+    hipLaunchKernelGGL((poolKernel<T, false>), dim3(batch), dim3(threads), smem, stream, g, ldG, C, mask, maskSum, HW, pooledOut,
+                       ldPooled, Wt, cout, out, ldOut);
+  KGH_CHECK_LAUNCH();
+}
+
+template<typename T>
+void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, const float* bias, int act, const float* mask,
+                 const float* ncBias, int ldNC, int HW, int M, hipStream_t stream) {
+  long total = (long)M * C;
+  hipLaunchKernelGGL(bnActKernel<T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, x, ldX, y, ldY, C, scale, bias,
+                     act, mask, ncBias, ldNC, HW, total);
+  KGH_CHECK_LAUNCH();
+}
+
+template<typename T>
+void launchHeadRow(const HeadRowArgs<T>& a, int batch, hipStream_t stream) {
+  int threads = 256;
+  size_t smem = (size_t)(3 * a.g1C + 3 * a.v1C + a.hiddenMax + threads) * sizeof(float);
+  hipLaunchKernelGGL(headRowKernel<T>, dim3(batch), dim3(threads), smem, stream, a);
+  KGH_CHECK_LAUNCH();
+}
+
+template<typename T>
+void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream) {
+  hipLaunchKernelGGL(headSpatialKernel<T>, dim3((a.M + 255) / 256), dim3(256), 0, stream, a);
+  KGH_CHECK_LAUNCH();
+}
+
+void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream) {
+  int total = a.batch * a.H * a.W;
+  hipLaunchKernelGGL(unpackOutputsKernel, dim3((total + 255) / 256), dim3(256), 0, stream, a);
+  KGH_CHECK_LAUNCH();
+}
+
+#define KGH_INSTANTIATE(T)                                                                                                  \
+  template void launchPackInputs<T>(const float*, const int*, int, int, int, int, T*, int, float*, float*, hipStream_t);     \
+  template void launchPool<T>(const T*, int, int, const float*, const float*, int, int, bool, float*, int, const float*, int, \
+                              float*, int, hipStream_t);                                                                     \
+  template void launchBnAct<T>(const T*, int, T*, int, int, const float*, const float*, int, const float*, const float*, int, \
+                               int, int, hipStream_t);                                                                       \
+  template void launchHeadRow<T>(const HeadRowArgs<T>&, int, hipStream_t);                                                   \
+  template void launchHeadSpatial<T>(const HeadSpatialArgs<T>&, hipStream_t);
+
+KGH_INSTANTIATE(float)
+KGH_INSTANTIATE(half_t)
+
+}  // namespace kgh

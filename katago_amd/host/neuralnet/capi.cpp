@@ -1,0 +1,216 @@
+// C shim over NeuralNet::* (include/katago_nn.h) for non-C++ callers.
+#include <cstring>
+#include <memory>
+
+#include "../neuralnet/nneval.h"
+#include "../neuralnet/nninterface.h"
+#include "katago_hip.h"
+#include "katago_nn.h"
+
+void hipBackendFlattenModel(const ModelDesc& desc, std::vector<kgh_layer>& layers, std::vector<float>& weights);
+
+using std::string;
+using std::vector;
+
+namespace {
+void setErr(char* err, int32_t errlen, const string& msg) {
+  if(err == nullptr || errlen <= 0) return;
+  size_t n = std::min((size_t)errlen - 1, msg.size());
+  memcpy(err, msg.data(), n);
+  err[n] = '\0';
+}
+}  // namespace
+
+extern "C" {
+
+void* kgn_load_model(const char* path, const char* expected_sha256, char* err, int32_t errlen) {
+  try {
+    return NeuralNet::loadModelFile(path, expected_sha256 ? expected_sha256 : "");
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return nullptr;
+  }
+}
+
+void kgn_free_model(void* m) { NeuralNet::freeLoadedModel((LoadedModel*)m); }
+
+int32_t kgn_model_info(void* m, int32_t* info, float* osm, char* name, int32_t namelen) {
+  if(m == nullptr) return -1;
+  const ModelDesc& d = NeuralNet::getModelDesc((const LoadedModel*)m);
+  if(info != nullptr) {
+    info[0] = d.modelVersion;
+    info[1] = d.numInputChannels;
+    info[2] = d.numInputGlobalChannels;
+    info[3] = d.numPolicyChannels;
+    info[4] = d.numValueChannels;
+    info[5] = d.numScoreValueChannels;
+    info[6] = d.numOwnershipChannels;
+    info[7] = d.trunk.trunkNumChannels;
+    info[8] = d.numInputMetaChannels;
+  }
+  if(osm != nullptr) *osm = d.postProcessParams.outputScaleMultiplier;
+  setErr(name, namelen, d.name);
+  return 0;
+}
+
+int32_t kgn_model_flatten(void* m, int32_t* num_layers, int64_t* num_weights, void* layers_out, float* weights_out) {
+  try {
+    if(m == nullptr || num_layers == nullptr || num_weights == nullptr) return -1;
+    vector<kgh_layer> layers;
+    vector<float> weights;
+    hipBackendFlattenModel(NeuralNet::getModelDesc((const LoadedModel*)m), layers, weights);
+    *num_layers = (int32_t)layers.size();
+    *num_weights = (int64_t)weights.size();
+    if(layers_out != nullptr) memcpy(layers_out, layers.data(), layers.size() * sizeof(kgh_layer));
+    if(weights_out != nullptr) memcpy(weights_out, weights.data(), weights.size() * sizeof(float));
+    return 0;
+  }
+  catch(const std::exception&) {
+    return -1;
+  }
+}
+
+void* kgn_create_context(void* m, int32_t nn_x, int32_t nn_y, int32_t use_fp16, char* err, int32_t errlen) {
+  try {
+    ConfigParser cfg;
+    enabled_t mode = use_fp16 == 0 ? enabled_t::False : use_fp16 == 1 ? enabled_t::True : enabled_t::Auto;
+    return NeuralNet::createComputeContext({0}, nullptr, nn_x, nn_y, "", mode, (const LoadedModel*)m, cfg);
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return nullptr;
+  }
+}
+
+void kgn_free_context(void* c) { NeuralNet::freeComputeContext((ComputeContext*)c); }
+
+void* kgn_create_handle(void* c, void* m, int32_t max_batch, int32_t require_exact, int32_t nhwc, int32_t gpu, char* err,
+                        int32_t errlen) {
+  try {
+    return NeuralNet::createComputeHandle((ComputeContext*)c, (const LoadedModel*)m, nullptr, max_batch, require_exact != 0,
+                                          nhwc != 0, gpu, 0);
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return nullptr;
+  }
+}
+
+void kgn_free_handle(void* h) { NeuralNet::freeComputeHandle((ComputeHandle*)h); }
+
+int32_t kgn_is_using_fp16(void* h) { return NeuralNet::isUsingFP16((const ComputeHandle*)h) ? 1 : 0; }
+
+int32_t kgn_get_output(void* h, void* m, int32_t nn_x, int32_t nn_y, int32_t n, const float* spatial, const float* global_in, const int32_t* symmetry,
+                       const float* policy_optimism, float* policy, float* value, float* score, float* ownership, char* err,
+                       int32_t errlen) {
+  try {
+    const LoadedModel* lm = (const LoadedModel*)m;
+    const ModelDesc& d = NeuralNet::getModelDesc(lm);
+    const int nnX = nn_x, nnY = nn_y;
+    const int HW = nnX * nnY;
+    const size_t spatialElts = (size_t)d.numInputChannels * HW;
+    std::unique_ptr<InputBuffers, void (*)(InputBuffers*)> bufs(NeuralNet::createInputBuffers(lm, n, nnX, nnY),
+                                                                 NeuralNet::freeInputBuffers);
+    vector<std::unique_ptr<NNResultBuf>> rows;
+    vector<NNResultBuf*> rowPtrs;
+    vector<std::unique_ptr<NNOutput>> outs;
+    vector<NNOutput*> outPtrs;
+    vector<vector<float>> owners(n, vector<float>(HW));
+    for(int i = 0; i < n; i++) {
+      rows.emplace_back(new NNResultBuf());
+      NNResultBuf& r = *rows.back();
+      r.rowSpatialBuf.assign(spatial + spatialElts * i, spatial + spatialElts * (i + 1));
+      r.rowGlobalBuf.assign(global_in + (size_t)d.numInputGlobalChannels * i, global_in + (size_t)d.numInputGlobalChannels * (i + 1));
+      r.symmetry = symmetry[i];
+      r.policyOptimism = policy_optimism[i];
+      rowPtrs.push_back(&r);
+      outs.emplace_back(new NNOutput());
+      NNOutput& o = *outs.back();
+      memset(&o, 0, sizeof(o));
+      o.nnXLen = nnX;
+      o.nnYLen = nnY;
+      o.whiteOwnerMap = owners[i].data();
+      outPtrs.push_back(&o);
+    }
+    NeuralNet::getOutput((ComputeHandle*)h, bufs.get(), n, rowPtrs.data(), outPtrs);
+    for(int i = 0; i < n; i++) {
+      const NNOutput& o = *outPtrs[i];
+      memcpy(policy + (size_t)(HW + 1) * i, o.policyProbs, (size_t)(HW + 1) * sizeof(float));
+      value[3 * i + 0] = o.whiteWinProb;
+      value[3 * i + 1] = o.whiteLossProb;
+      value[3 * i + 2] = o.whiteNoResultProb;
+      score[6 * i + 0] = o.whiteScoreMean;
+      score[6 * i + 1] = o.whiteScoreMeanSq;
+      score[6 * i + 2] = o.whiteLead;
+      score[6 * i + 3] = o.varTimeLeft;
+      score[6 * i + 4] = o.shorttermWinlossError;
+      score[6 * i + 5] = o.shorttermScoreError;
+      memcpy(ownership + (size_t)HW * i, owners[i].data(), (size_t)HW * sizeof(float));
+    }
+    return 0;
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return -1;
+  }
+}
+
+int32_t kgn_test_evaluate(int32_t kind, const char* desc_text, int32_t batch, int32_t nn_x, int32_t nn_y, int32_t use_fp16,
+                          int32_t use_nhwc, const float* input, const float* mask, float* output, int64_t output_len, char* err,
+                          int32_t errlen) {
+  try {
+    const int HW = nn_x * nn_y;
+    vector<float> out;
+    vector<float> maskV(mask != nullptr ? mask : nullptr, mask != nullptr ? mask + (size_t)batch * HW : nullptr);
+    if(mask == nullptr) maskV.assign((size_t)batch * HW, 1.0f);
+    bool supported = false;
+    int inC = 0;
+    if(kind == 0) {
+      ConvLayerDesc d;
+      DescText::parseConv(desc_text, d);
+      inC = d.inChannels;
+      vector<float> in(input, input + (size_t)batch * HW * inC);
+      supported = NeuralNet::testEvaluateConv(&d, batch, nn_x, nn_y, use_fp16 != 0, use_nhwc != 0, in, out);
+    }
+    else if(kind == 1) {
+      BatchNormLayerDesc d;
+      DescText::parseBatchNorm(desc_text, d);
+      inC = d.numChannels;
+      vector<float> in(input, input + (size_t)batch * HW * inC);
+      supported = NeuralNet::testEvaluateBatchNorm(&d, batch, nn_x, nn_y, use_fp16 != 0, use_nhwc != 0, in, maskV, out);
+    }
+    else if(kind == 2) {
+      ResidualBlockDesc d;
+      DescText::parseResidualBlock(desc_text, 15, d);
+      inC = d.preBN.numChannels;
+      vector<float> in(input, input + (size_t)batch * HW * inC);
+      supported = NeuralNet::testEvaluateResidualBlock(&d, batch, nn_x, nn_y, use_fp16 != 0, use_nhwc != 0, in, maskV, out);
+    }
+    else if(kind == 3) {
+      GlobalPoolingResidualBlockDesc d;
+      DescText::parseGlobalPoolingResidualBlock(desc_text, 15, d);
+      inC = d.preBN.numChannels;
+      vector<float> in(input, input + (size_t)batch * HW * inC);
+      supported = NeuralNet::testEvaluateGlobalPoolingResidualBlock(&d, batch, nn_x, nn_y, use_fp16 != 0, use_nhwc != 0, in, maskV,
+                                                                    out);
+    }
+    else {
+      setErr(err, errlen, "unknown test kind");
+      return -1;
+    }
+    if(!supported) return 0;
+    if((int64_t)out.size() > output_len) {
+      setErr(err, errlen, "output buffer too small");
+      return -1;
+    }
+    memcpy(output, out.data(), out.size() * sizeof(float));
+    return 1;
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return -1;
+  }
+}
+
+}  // extern "C"

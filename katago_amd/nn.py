@@ -1,0 +1,368 @@
+"""Python binding of the HIP backend's NeuralNet interface (include/katago_nn.h).
+
+Mirrors KataGo's backend API (/root/reference/cpp/neuralnet/nninterface.h):
+``LoadedModel`` (loadModelFile / getModelDesc), ``ComputeContext``
+(createComputeContext) and ``ComputeHandle`` (createComputeHandle,
+getOutput, isUsingFP16), plus the layer-level ``test_evaluate`` hooks.
+Errors raise ``StringError``, the reference's error type.
+
+The native libraries must have been built (``python -m katago_amd.build``);
+there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
+_host = None
+_hip = None
+
+
+class StringError(RuntimeError):
+    """Error raised by the backend (KataGo's StringError)."""
+
+
+def _f32p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _i32p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def hip_library() -> ctypes.CDLL:
+    """libkatago_hip.so (the C ABI of include/katago_hip.h)."""
+    global _hip
+    if _hip is None:
+        path = os.path.join(_LIB_DIR, "libkatago_hip.so")
+        if not os.path.exists(path):
+            raise StringError(f"{path} is not built; run python -m katago_amd.build")
+        lib = ctypes.CDLL(path)
+        lib.kgh_last_error.restype = ctypes.c_char_p
+        lib.kgh_output_row_floats.restype = ctypes.c_int32
+        lib.kgh_output_row_floats.argtypes = [ctypes.c_int32] * 3
+        lib.kgh_device_alloc.argtypes = [ctypes.c_int32, ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]
+        lib.kgh_device_free.argtypes = [ctypes.c_void_p]
+        lib.kgh_memcpy_htod.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        lib.kgh_memcpy_dtoh.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        lib.kgh_device_info.argtypes = [ctypes.c_int32, ctypes.c_char_p, ctypes.c_int32]
+        lib.kgh_selftest_mfma.argtypes = [ctypes.c_int32]
+        _hip = lib
+    return _hip
+
+
+def host_library() -> ctypes.CDLL:
+    """libkatago_host.so (the C ABI of include/katago_nn.h)."""
+    global _host
+    if _host is None:
+        hip_library()
+        path = os.path.join(_LIB_DIR, "libkatago_host.so")
+        if not os.path.exists(path):
+            raise StringError(f"{path} is not built; run python -m katago_amd.build")
+        lib = ctypes.CDLL(path)
+        c = ctypes
+        lib.kgn_load_model.restype = c.c_void_p
+        lib.kgn_load_model.argtypes = [c.c_char_p, c.c_char_p, c.c_char_p, c.c_int32]
+        lib.kgn_free_model.argtypes = [c.c_void_p]
+        lib.kgn_model_info.argtypes = [c.c_void_p, c.POINTER(c.c_int32), c.POINTER(c.c_float), c.c_char_p, c.c_int32]
+        lib.kgn_create_context.restype = c.c_void_p
+        lib.kgn_create_context.argtypes = [c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_char_p, c.c_int32]
+        lib.kgn_free_context.argtypes = [c.c_void_p]
+        lib.kgn_create_handle.restype = c.c_void_p
+        lib.kgn_create_handle.argtypes = [c.c_void_p, c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_char_p,
+                                          c.c_int32]
+        lib.kgn_free_handle.argtypes = [c.c_void_p]
+        lib.kgn_is_using_fp16.argtypes = [c.c_void_p]
+        lib.kgn_get_output.argtypes = [c.c_void_p, c.c_void_p, c.c_int32, c.c_int32, c.c_int32] + [c.c_void_p] * 8 + [
+            c.c_char_p, c.c_int32]
+        lib.kgn_test_evaluate.argtypes = [c.c_int32, c.c_char_p, c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_int32,
+                                          c.c_void_p, c.c_void_p, c.c_void_p, c.c_int64, c.c_char_p, c.c_int32]
+        _host = lib
+    return _host
+
+
+def _errbuf():
+    return ctypes.create_string_buffer(4096)
+
+
+def _raise(err) -> None:
+    raise StringError(err.value.decode(errors="replace"))
+
+
+@dataclass
+class ModelInfo:
+    name: str
+    model_version: int
+    num_input_channels: int
+    num_input_global_channels: int
+    num_policy_channels: int
+    num_value_channels: int
+    num_score_value_channels: int
+    num_ownership_channels: int
+    trunk_num_channels: int
+    num_input_meta_channels: int
+    output_scale_multiplier: float
+
+
+class LoadedModel:
+    """NeuralNet::loadModelFile: parses the file, applies the load-time
+    transforms (reduce-activations and scale8)."""
+
+    def __init__(self, path: str, expected_sha256: str = ""):
+        lib = host_library()
+        err = _errbuf()
+        self._ptr = lib.kgn_load_model(path.encode(), expected_sha256.encode(), err, len(err))
+        if not self._ptr:
+            _raise(err)
+        info = (ctypes.c_int32 * 9)()
+        osm = ctypes.c_float()
+        name = ctypes.create_string_buffer(256)
+        lib.kgn_model_info(self._ptr, info, ctypes.byref(osm), name, len(name))
+        self.info = ModelInfo(name.value.decode(), *list(info), float(osm.value))
+
+    def close(self):
+        if getattr(self, "_ptr", None):
+            host_library().kgn_free_model(self._ptr)
+            self._ptr = None
+
+    def __del__(self):
+        self.close()
+
+
+class ComputeContext:
+    """NeuralNet::createComputeContext. use_fp16: True, False or None (auto)."""
+
+    def __init__(self, model: LoadedModel, nn_x: int = 19, nn_y: int = 19, use_fp16=None):
+        lib = host_library()
+        err = _errbuf()
+        mode = 2 if use_fp16 is None else (1 if use_fp16 else 0)
+        self.model = model
+        self.nn_x, self.nn_y = nn_x, nn_y
+        self._ptr = lib.kgn_create_context(model._ptr, nn_x, nn_y, mode, err, len(err))
+        if not self._ptr:
+            _raise(err)
+
+    def close(self):
+        if getattr(self, "_ptr", None):
+            host_library().kgn_free_context(self._ptr)
+            self._ptr = None
+
+    def __del__(self):
+        self.close()
+
+
+class ComputeHandle:
+    """NeuralNet::createComputeHandle + getOutput."""
+
+    def __init__(self, context: ComputeContext, max_batch: int, require_exact_nn_len: bool = False,
+                 inputs_use_nhwc: bool = True, gpu_idx: int = 0):
+        lib = host_library()
+        err = _errbuf()
+        self.context = context
+        self.model = context.model
+        self.max_batch = max_batch
+        self.inputs_use_nhwc = inputs_use_nhwc
+        self._ptr = lib.kgn_create_handle(context._ptr, context.model._ptr, max_batch, int(require_exact_nn_len),
+                                          int(inputs_use_nhwc), gpu_idx, err, len(err))
+        if not self._ptr:
+            _raise(err)
+
+    @property
+    def using_fp16(self) -> bool:
+        return bool(host_library().kgn_is_using_fp16(self._ptr))
+
+    def get_output(self, spatial, global_in, symmetry=None, policy_optimism=None):
+        """Returns raw outputs as a dict of arrays: policy [n, HW+1] (pass last),
+        value [n, 3], score [n, 6], ownership [n, HW]."""
+        lib = host_library()
+        n = int(np.asarray(global_in).shape[0])
+        hw = self.context.nn_x * self.context.nn_y
+        spatial = np.ascontiguousarray(spatial, dtype=np.float32).reshape(n, -1)
+        global_in = np.ascontiguousarray(global_in, dtype=np.float32).reshape(n, -1)
+        sym = np.ascontiguousarray(np.zeros(n) if symmetry is None else symmetry, dtype=np.int32)
+        opt = np.ascontiguousarray(np.zeros(n) if policy_optimism is None else policy_optimism, dtype=np.float32)
+        policy = np.zeros((n, hw + 1), np.float32)
+        value = np.zeros((n, 3), np.float32)
+        score = np.zeros((n, 6), np.float32)
+        own = np.zeros((n, hw), np.float32)
+        err = _errbuf()
+        rc = lib.kgn_get_output(self._ptr, self.model._ptr, self.context.nn_x, self.context.nn_y, n,
+                                spatial.ctypes.data, global_in.ctypes.data, sym.ctypes.data, opt.ctypes.data,
+                                policy.ctypes.data, value.ctypes.data, score.ctypes.data, own.ctypes.data, err, len(err))
+        if rc != 0:
+            _raise(err)
+        return {"policy": policy, "value": value, "score": score, "ownership": own}
+
+    def close(self):
+        if getattr(self, "_ptr", None):
+            host_library().kgn_free_handle(self._ptr)
+            self._ptr = None
+
+    def __del__(self):
+        self.close()
+
+
+TEST_CONV, TEST_BATCHNORM, TEST_RESIDUAL, TEST_GPOOL = 0, 1, 2, 3
+
+
+def test_evaluate(kind: int, desc_text: str, batch: int, nn_x: int, nn_y: int, use_fp16: bool, use_nhwc: bool,
+                  inputs, mask=None, out_channels: int = 0):
+    """NeuralNet::testEvaluate{Conv,BatchNorm,ResidualBlock,GlobalPoolingResidualBlock}.
+    Returns the output array, or None when the combination is unsupported."""
+    lib = host_library()
+    inp = np.ascontiguousarray(inputs, dtype=np.float32).reshape(-1)
+    m = None if mask is None else np.ascontiguousarray(mask, dtype=np.float32).reshape(-1)
+    out = np.zeros(batch * nn_x * nn_y * max(out_channels, 1) * 4 + inp.size, np.float32)
+    err = _errbuf()
+    rc = lib.kgn_test_evaluate(kind, desc_text.encode(), batch, nn_x, nn_y, int(use_fp16), int(use_nhwc), inp.ctypes.data,
+                               None if m is None else m.ctypes.data, out.ctypes.data, out.size, err, len(err))
+    if rc < 0:
+        _raise(err)
+    if rc == 0:
+        return None
+    return out[: batch * nn_x * nn_y * out_channels]
+
+
+def hip_check(status: int) -> None:
+    if status != 0:
+        raise StringError(hip_library().kgh_last_error().decode(errors="replace"))
+
+
+def device_count() -> int:
+    c = ctypes.c_int32(0)
+    hip_check(hip_library().kgh_device_count(ctypes.byref(c)))
+    return int(c.value)
+
+
+# ---------------------------------------------------------------------------
+# Direct use of the device library's C ABI (include/katago_hip.h).
+
+LAYER_DTYPE = np.dtype([("op", "<i4"), ("i", "<i4", 7), ("f", "<f4", 2), ("w", "<i8", 2), ("wn", "<i8", 2)])
+
+
+class _ModelDescC(ctypes.Structure):
+    _fields_ = [("model_version", ctypes.c_int32), ("num_input_channels", ctypes.c_int32),
+                ("num_input_global_channels", ctypes.c_int32), ("num_input_meta_channels", ctypes.c_int32),
+                ("num_policy_channels", ctypes.c_int32), ("num_value_channels", ctypes.c_int32),
+                ("num_score_value_channels", ctypes.c_int32), ("num_ownership_channels", ctypes.c_int32),
+                ("num_layers", ctypes.c_int32), ("layers", ctypes.c_void_p), ("weights", ctypes.c_void_p),
+                ("num_weights", ctypes.c_int64)]
+
+
+def flatten_model(model: LoadedModel):
+    """The layer program (LAYER_DTYPE records) and weights that the backend
+    passes to kgh_model_create for this model (kgn_model_flatten)."""
+    lib = host_library()
+    lib.kgn_model_flatten.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64),
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    nl = ctypes.c_int32()
+    nw = ctypes.c_int64()
+    if lib.kgn_model_flatten(model._ptr, ctypes.byref(nl), ctypes.byref(nw), None, None) != 0:
+        raise StringError("kgn_model_flatten failed")
+    layers = np.zeros(nl.value, LAYER_DTYPE)
+    weights = np.zeros(nw.value, np.float32)
+    if lib.kgn_model_flatten(model._ptr, ctypes.byref(nl), ctypes.byref(nw), layers.ctypes.data, weights.ctypes.data) != 0:
+        raise StringError("kgn_model_flatten failed")
+    return layers, weights
+
+
+class DeviceModel:
+    """kgh_model: a model's weights uploaded to one device."""
+
+    def __init__(self, model: LoadedModel, use_fp16: bool, device: int = 0):
+        lib = hip_library()
+        self.layers, self.weights = flatten_model(model)
+        info = model.info
+        d = _ModelDescC(info.model_version, info.num_input_channels, info.num_input_global_channels,
+                        info.num_input_meta_channels, info.num_policy_channels, info.num_value_channels,
+                        info.num_score_value_channels, info.num_ownership_channels, len(self.layers),
+                        self.layers.ctypes.data, self.weights.ctypes.data, len(self.weights))
+        self.info = info
+        self._ptr = ctypes.c_void_p()
+        lib.kgh_model_create.argtypes = [ctypes.c_int32, ctypes.POINTER(_ModelDescC), ctypes.c_int32,
+                                         ctypes.POINTER(ctypes.c_void_p)]
+        hip_check(lib.kgh_model_create(device, ctypes.byref(d), int(use_fp16), ctypes.byref(self._ptr)))
+
+    def close(self):
+        if getattr(self, "_ptr", None) and self._ptr.value:
+            hip_library().kgh_model_free(self._ptr)
+            self._ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+
+class DeviceHandle:
+    """kgh_handle: stream and buffers for device-memory forwards."""
+
+    def __init__(self, model: DeviceModel, max_batch: int, nn_x: int = 19, nn_y: int = 19):
+        lib = hip_library()
+        self.model = model
+        self.nn_x, self.nn_y = nn_x, nn_y
+        self._ptr = ctypes.c_void_p()
+        lib.kgh_handle_create.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                          ctypes.POINTER(ctypes.c_void_p)]
+        hip_check(lib.kgh_handle_create(model._ptr, max_batch, nn_x, nn_y, 0, ctypes.byref(self._ptr)))
+        lib.kgh_forward_device.argtypes = [ctypes.c_void_p, ctypes.c_int32] + [ctypes.c_void_p] * 5
+        lib.kgh_handle_synchronize.argtypes = [ctypes.c_void_p]
+        lib.kgh_handle_set_profiling.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+        lib.kgh_handle_profile.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_double)]
+        self.row_floats = lib.kgh_output_row_floats(nn_x, nn_y, model.info.num_score_value_channels)
+
+    def forward_device(self, n, d_spatial, d_global, d_sym, d_opt, d_out):
+        hip_check(hip_library().kgh_forward_device(self._ptr, n, d_spatial, d_global, d_sym, d_opt, d_out))
+
+    def synchronize(self):
+        hip_check(hip_library().kgh_handle_synchronize(self._ptr))
+
+    def set_profiling(self, on: bool):
+        hip_check(hip_library().kgh_handle_set_profiling(self._ptr, int(on)))
+
+    def profile(self, kind: int):
+        ms = ctypes.c_double()
+        cnt = ctypes.c_int32()
+        fl = ctypes.c_double()
+        hip_check(hip_library().kgh_handle_profile(self._ptr, kind, ctypes.byref(ms), ctypes.byref(cnt), ctypes.byref(fl)))
+        return ms.value, cnt.value, fl.value
+
+    def close(self):
+        if getattr(self, "_ptr", None) and self._ptr.value:
+            hip_library().kgh_handle_free(self._ptr)
+            self._ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+
+class DeviceBuffer:
+    """Device memory from kgh_device_alloc, filled from / read into numpy."""
+
+    def __init__(self, nbytes: int, device: int = 0):
+        self.nbytes = nbytes
+        self.ptr = ctypes.c_void_p()
+        hip_check(hip_library().kgh_device_alloc(device, nbytes, ctypes.byref(self.ptr)))
+
+    @classmethod
+    def from_array(cls, a: np.ndarray, device: int = 0):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes, device)
+        hip_check(hip_library().kgh_memcpy_htod(b.ptr, a.ctypes.data, a.nbytes))
+        return b
+
+    def to_array(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        hip_check(hip_library().kgh_memcpy_dtoh(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr.value:
+            hip_library().kgh_device_free(self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        self.free()

@@ -1,0 +1,35 @@
+"""Shared helpers for the test suite."""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+G170_MODEL = os.path.join(GOLDEN, "g170-b6c96-s175395328-d26788732.bin.gz")
+
+
+def load_kats():
+    with open(os.path.join(GOLDEN, "layer_kats.json")) as f:
+        return json.load(f)["kats"]
+
+
+def load_symmetry_cases():
+    with open(os.path.join(GOLDEN, "symmetry_golden.json")) as f:
+        return json.load(f)["cases"]
+
+
+def nchw_to_nhwc(a, n, c, h, w):
+    return np.asarray(a, np.float32).reshape(n, c, h, w).transpose(0, 2, 3, 1).reshape(-1)
+
+
+def approx_equal_kat(x, y, fp16: bool):
+    """testnn.cpp:8-15: 1e-4*max(|x|,|y|,1) in fp32, 0.03*max(|x|,|y|,3) in fp16."""
+    x = np.asarray(x, np.float64)
+    y = np.asarray(y, np.float64)
+    if fp16:
+        tol = 0.03 * np.maximum(np.maximum(np.abs(x), np.abs(y)), 3.0)
+    else:
+        tol = 1e-4 * np.maximum(np.maximum(np.abs(x), np.abs(y)), 1.0)
+    return np.abs(x - y) < tol

@@ -1,0 +1,188 @@
+"""GPU parity of the HIP backend against the CPU oracle, through the C ABI.
+
+Tolerances: the reference's layer-test tolerances for the layer KATs
+(testnn.cpp:8-15); for whole networks, on raw outputs times
+outputScaleMultiplier: policy max-abs <= 1e-3 (fp32) / 2e-2 (fp16) with an
+identical argmax over on-board points and pass, value and score <= 1e-3
+(fp32) / 1e-2 (fp16), ownership as policy.
+"""
+import numpy as np
+import pytest
+
+from helpers import G170_MODEL, approx_equal_kat, load_kats, nchw_to_nhwc
+from katago_amd import modelgen, nn
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+KIND = {"conv": 0, "bn": 1, "residual": 2, "gpool": 3}
+TOL = {False: dict(policy=1e-3, value=1e-3, score=1e-3, ownership=1e-3),
+       True: dict(policy=2e-2, value=1e-2, score=1e-2, ownership=2e-2)}
+
+
+def test_device_present_and_matrix_core_layout():
+    assert nn.device_count() >= 1
+    nn.hip_check(nn.hip_library().kgh_selftest_mfma(0))
+
+
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
+@pytest.mark.parametrize("nhwc", [True, False], ids=["nhwc", "nchw"])
+@pytest.mark.parametrize("kat", load_kats(), ids=lambda k: k["label"])
+def test_layer_kats_on_gpu(kat, nhwc, fp16):
+    n, X, Y = kat["batch"], kat["nnXLen"], kat["nnYLen"]
+    ci, co = kat["inChannels"], kat["outChannels"]
+    inp = nchw_to_nhwc(kat["input_nchw"], n, ci, Y, X) if nhwc else np.asarray(kat["input_nchw"], np.float32)
+    exp = nchw_to_nhwc(kat["expected_nchw"], n, co, Y, X) if nhwc else np.asarray(kat["expected_nchw"], np.float32)
+    out = nn.test_evaluate(KIND[kat["kind"]], kat["desc_text"], n, X, Y, fp16, nhwc, inp, kat["mask"], co)
+    assert out is not None
+    assert approx_equal_kat(out, exp, fp16).all(), (out, exp)
+
+
+def _arr(a):
+    return " ".join(repr(float(v)) for v in np.asarray(a).reshape(-1))
+
+
+def _bn_text(name, c, rng):
+    return (f"{name} {c} 1e-20 1 1\n{_arr(np.zeros(c))}\n{_arr(np.full(c, 1 - 1e-20))}\n"
+            f"{_arr(0.8 + 0.4 * rng.random(c))}\n{_arr(0.1 * rng.standard_normal(c))}\n")
+
+
+def _conv_text(name, k, ci, co, rng, gain=1.0):
+    w = rng.standard_normal((k, k, ci, co)) * gain * np.sqrt(2.0 / (k * k * ci))
+    return f"{name} {k} {k} {ci} {co} 1 1\n{_arr(w)}\n"
+
+
+def _random_block(kind, c, mid, gp, act, rng):
+    if kind == "residual":
+        return ("b\n" + _bn_text("pre", c, rng) + f"pa {act}\n" + _conv_text("c1", 3, c, mid, rng) + _bn_text("mid", mid, rng) +
+                f"ma {act}\n" + _conv_text("c2", 3, mid, c, rng, 0.5))
+    reg = mid - gp
+    return ("b\n" + _bn_text("pre", c, rng) + f"pa {act}\n" + _conv_text("cr", 3, c, reg, rng) + _conv_text("cg", 3, c, gp, rng) +
+            _bn_text("gbn", gp, rng) + f"ga {act}\n" + f"gm {3 * gp} {reg}\n{_arr(rng.standard_normal(3 * gp * reg) * np.sqrt(2 / (3 * gp)))}\n" +
+            _bn_text("mid", reg, rng) + f"ma {act}\n" + _conv_text("c2", 3, reg, c, rng, 0.5))
+
+
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
+@pytest.mark.parametrize("kind,c,mid,gp,act", [
+    ("residual", 64, 64, 0, "ACTIVATION_RELU"),
+    ("residual", 96, 96, 0, "ACTIVATION_MISH"),
+    ("residual", 32, 64, 0, "ACTIVATION_SILU"),
+    ("gpool", 64, 64, 32, "ACTIVATION_MISH"),
+    ("gpool", 96, 96, 32, "ACTIVATION_RELU"),
+])
+def test_random_blocks_match_oracle(kind, c, mid, gp, act, fp16):
+    rng = np.random.default_rng(c + mid + gp)
+    text = _random_block(kind, c, mid, gp, act, rng)
+    n, X, Y = 3, 19, 19
+    x = rng.standard_normal((n, Y, X, c)).astype(np.float32)
+    mask = np.zeros((n, Y, X), np.float32)
+    for i, bs in enumerate((19, 9, 13)):
+        mask[i, :bs, :bs] = 1
+    ref = oracle.test_evaluate(KIND[kind], text, n, X, Y, x, mask, c)
+    out = nn.test_evaluate(KIND[kind], text, n, X, Y, fp16, True, x, mask, c)
+    assert approx_equal_kat(out, ref, fp16).all(), np.abs(out - ref).max()
+
+
+def _compare(gpu, ora, fp16, scale, board_sizes, n, label):
+    tol = TOL[fp16]
+    hw = 361
+    for key in ("value", "ownership"):
+        d = np.abs(gpu[key] * scale - ora[key]).max()
+        assert d <= tol[key], f"{label} {key} max-abs {d}"
+    d = np.abs(gpu["score"] * scale - ora["score"]).max()
+    assert d <= tol["score"], f"{label} score max-abs {d}"
+    gp = gpu["policy"] * scale
+    d = np.abs(gp - ora["policy"]).max()
+    assert d <= tol["policy"], f"{label} policy max-abs {d}"
+    for i in range(n):
+        bs = board_sizes[i % len(board_sizes)]
+        legal = np.zeros(hw + 1, bool)
+        legal[:hw] = (np.arange(hw) // 19 < bs) & (np.arange(hw) % 19 < bs)
+        legal[hw] = True
+        a = np.where(legal, gp[i], -np.inf).argmax()
+        b = np.where(legal, ora["policy"][i], -np.inf).argmax()
+        assert a == b, f"{label} row {i} argmax {a} != {b}"
+
+
+def _run_parity(path, fp16, n, board_sizes=(19,), symmetries=None, seed=5, label=""):
+    om = oracle.OracleModel(path)
+    lm = nn.LoadedModel(path)
+    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=fp16)
+    h = nn.ComputeHandle(ctx, max_batch=n)
+    assert h.using_fp16 == fp16
+    sp, gl = modelgen.synthetic_inputs(seed, n, board_sizes=board_sizes)
+    sym = np.arange(n) % 8 if symmetries is None else symmetries
+    opt = (np.arange(n) % 3) / 2.0
+    gpu = h.get_output(sp, gl, sym, opt)
+    ora = om.forward(sp, gl, sym, opt)
+    _compare(gpu, ora, fp16, lm.info.output_scale_multiplier, board_sizes, n, label)
+    return gpu, ora
+
+
+def test_c0_b6c96_fp32_matches_oracle(model_dir):
+    cfg = modelgen.configs()[0]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), False, cfg.batch, label="C0")
+
+
+def test_c1_b10c128_fp16_matches_oracle(model_dir):
+    cfg = modelgen.configs()[1]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), True, 8, label="C1")
+
+
+def test_c1_b10c128_fp32_matches_oracle(model_dir):
+    cfg = modelgen.configs()[1]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), False, 4, label="C1 fp32")
+
+
+def test_c2_b18c384nbt_fp16_matches_oracle(model_dir):
+    cfg = modelgen.configs()[2]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), True, 4, label="C2")
+
+
+def test_c3_mixed_board_sizes_fp16_matches_oracle(model_dir):
+    cfg = modelgen.configs()[3]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), True, 6, board_sizes=(9, 13, 19), label="C3")
+
+
+def test_c3_batch_one_fp16_matches_oracle(model_dir):
+    cfg = modelgen.configs()[3]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), True, 1, board_sizes=(9,), label="C3 batch 1")
+
+
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
+def test_trained_g170_b6c96_matches_oracle(fp16):
+    _run_parity(G170_MODEL, fp16, 8, symmetries=np.arange(8), label="g170")
+
+
+def test_all_symmetries_fp32(model_dir):
+    cfg = modelgen.configs()[0]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), False, 8, board_sizes=(19, 13), symmetries=np.arange(8),
+                label="symmetries")
+
+
+def test_c2_full_batch_rows_are_independent(model_dir):
+    """At the full benchmark size: a row's outputs do not depend on the other
+    rows of the batch (bitwise, as every reduction is per row)."""
+    cfg = modelgen.configs()[2]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=True)
+    h = nn.ComputeHandle(ctx, max_batch=256)
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, 256)
+    full = h.get_output(sp, gl)
+    rows = [0, 1, 127, 255]
+    part = h.get_output(sp[rows], gl[rows])
+    for k in full:
+        assert np.array_equal(full[k][rows], part[k]), k
+        assert np.isfinite(full[k]).all()
+
+
+def test_errors_are_raised_not_crashed(model_dir):
+    cfg = modelgen.configs()[0]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=False)
+    h = nn.ComputeHandle(ctx, max_batch=2)
+    sp, gl = modelgen.synthetic_inputs(1, 3)
+    with pytest.raises(nn.StringError, match="numBatchEltsFilled"):
+        h.get_output(sp, gl)
+    with pytest.raises(nn.StringError, match="symmetry"):
+        h.get_output(sp[:1], gl[:1], symmetry=[9])
