@@ -100,6 +100,8 @@ struct Block {
   BNAct midBN;   // ordinary/gpool: midBN; nbt: postBN
   ConvW conv2;   // ordinary/gpool: finalConv; nbt: postConv
   int regC = 0, gpC = 0;
+  bool splitGpool = false;  // regular and gpool convs differ in kernel size
+  ConvW convGpool;          // used when splitGpool
   BNAct gpoolBN;
   MatW gpoolMul;
   std::vector<Block> inner;
@@ -281,13 +283,23 @@ struct Builder {
       blk.preBN = bnAct("gpool preBN");
       ConvRec reg = convRec("gpool regularConv");
       ConvRec gp = convRec("gpool gpoolConv");
-      if(reg.ky != gp.ky || reg.kx != gp.kx || reg.cin != gp.cin) unsupported("gpool block: regular and gpool convs differ in shape");
-      // One convolution producing [regular | gpool] output channels.
-      std::vector<float> cat((size_t)(reg.cout + gp.cout) * reg.cin * reg.ky * reg.kx);
-      size_t regCount = (size_t)reg.cout * reg.cin * reg.ky * reg.kx;
-      memcpy(cat.data(), host(*reg.l, 0), regCount * sizeof(float));
-      memcpy(cat.data() + regCount, host(*gp.l, 0), (size_t)gp.cout * gp.cin * gp.ky * gp.kx * sizeof(float));
-      blk.conv1 = makeConv(upload(cat), reg.ky, reg.kx, reg.cin, reg.cout + gp.cout, false);
+      if(reg.cin != gp.cin) invalid("gpool block: regular and gpool convs read different channel counts");
+      if(reg.ky == gp.ky && reg.kx == gp.kx) {
+        // One convolution producing [regular | gpool] output channels.
+        std::vector<float> cat((size_t)(reg.cout + gp.cout) * reg.cin * reg.ky * reg.kx);
+        size_t regCount = (size_t)reg.cout * reg.cin * reg.ky * reg.kx;
+        memcpy(cat.data(), host(*reg.l, 0), regCount * sizeof(float));
+        memcpy(cat.data() + regCount, host(*gp.l, 0), (size_t)gp.cout * gp.cin * gp.ky * gp.kx * sizeof(float));
+        blk.conv1 = makeConv(upload(cat), reg.ky, reg.kx, reg.cin, reg.cout + gp.cout, false);
+      }
+      else {
+        // Differently sized kernels: two convolutions over the same input.
+        blk.conv1 = makeConv(dev(*reg.l, 0, (int64_t)reg.ky * reg.kx * reg.cin * reg.cout, "gpool regularConv"), reg.ky, reg.kx,
+                             reg.cin, reg.cout, false);
+        blk.convGpool = makeConv(dev(*gp.l, 0, (int64_t)gp.ky * gp.kx * gp.cin * gp.cout, "gpool gpoolConv"), gp.ky, gp.kx, gp.cin,
+                                 gp.cout, false);
+        blk.splitGpool = true;
+      }
       blk.regC = reg.cout;
       blk.gpC = gp.cout;
       blk.gpoolBN = bnAct("gpool gpoolBN");
@@ -511,7 +523,20 @@ struct Runner {
       e1.actScale = b.gpoolBN.scale;
       e1.actBias = b.gpoolBN.bias;
       e1.actKind = b.gpoolBN.act;
-      conv(b.conv1, Ad, C, e1);
+      if(!b.splitGpool) {
+        conv(b.conv1, Ad, C, e1);
+      }
+      else {
+        ConvEpilogue<T> er = e1;
+        er.outAct = nullptr;
+        er.actBegin = INT_MAX;
+        conv(b.conv1, Ad, C, er);
+        ConvEpilogue<T> eg = e1;
+        eg.outRaw = nullptr;
+        eg.rawEnd = 0;
+        eg.actBegin = 0;
+        conv(b.convGpool, Ad, C, eg);
+      }
       // masked pooling of the gpool channels, then the bias matvec
       kgh::launchPool<T>(tmp2, b.gpC, b.gpC, mask, maskSum, g.batch, g.H * g.W, false, nullptr, 0, b.gpoolMul.w, b.regC, nbias,
                          b.regC, s);

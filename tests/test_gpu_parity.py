@@ -149,9 +149,41 @@ def test_c3_batch_one_fp16_matches_oracle(model_dir):
     _run_parity(modelgen.ensure_model(model_dir, cfg), True, 1, board_sizes=(9,), label="C3 batch 1")
 
 
-@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
-def test_trained_g170_b6c96_matches_oracle(fp16):
-    _run_parity(G170_MODEL, fp16, 8, symmetries=np.arange(8), label="g170")
+def test_trained_g170_b6c96_fp32_matches_oracle():
+    _run_parity(G170_MODEL, False, 8, symmetries=np.arange(8), label="g170")
+
+
+def _softmax(x):
+    e = np.exp(x - x.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def test_trained_g170_b6c96_fp16_within_reference_fp16_error_bounds():
+    """A trained net's logits reach +-20, where fp16 storage alone gives
+    ~2.5e-3 relative error, so the absolute bounds meant for the synthetic
+    configs do not apply. Checked instead with the reference's fp16 acceptance
+    bounds of testgpuerror (testnnevalcanary.cpp:742-749, max over positions):
+    winrate error <= 5%, policy KL <= 4e-3; plus logits within
+    2e-2 + 3e-3*|logit| and the same top move."""
+    n = 8
+    om = oracle.OracleModel(G170_MODEL)
+    lm = nn.LoadedModel(G170_MODEL)
+    h = nn.ComputeHandle(nn.ComputeContext(lm, 19, 19, use_fp16=True), max_batch=n)
+    sp, gl = modelgen.synthetic_inputs(5, n)
+    sym = np.arange(n)
+    gpu = h.get_output(sp, gl, sym)
+    ora = om.forward(sp, gl, sym)
+    s = lm.info.output_scale_multiplier
+    gp, op = gpu["policy"] * s, ora["policy"]
+    assert (np.abs(gp - op) <= 2e-2 + 3e-3 * np.abs(op)).all(), np.abs(gp - op).max()
+    assert (gp.argmax(axis=1) == op.argmax(axis=1)).all()
+    pg, po = _softmax(gp.astype(np.float64)), _softmax(op.astype(np.float64))
+    kl = (po * (np.log(po) - np.log(pg))).sum(axis=1)
+    assert kl.max() <= 4e-3, kl.max()
+    wg = _softmax(gpu["value"].astype(np.float64) * s)[:, 0]
+    wo = _softmax(ora["value"].astype(np.float64))[:, 0]
+    assert np.abs(wg - wo).max() <= 0.05
+    assert np.abs(gpu["ownership"] * s - ora["ownership"]).max() <= 2e-2 + 3e-3 * np.abs(ora["ownership"]).max()
 
 
 def test_all_symmetries_fp32(model_dir):
