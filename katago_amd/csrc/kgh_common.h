@@ -59,6 +59,27 @@ __device__ __forceinline__ float kgh_activate(float x, int act) {
   }
 }
 
+// Fast forms used in kernel epilogues, from the identity
+//   tanh(log(1 + e^y)) = n / (n + 2),  n = e^y (e^y + 2),
+// so mish needs one exponential and one reciprocal. For y > 20 the factor is
+// 1 to fp32 precision (and n would overflow), as in the clamped reference
+// formula. Relative error against the formulas above is a few ulp.
+__device__ __forceinline__ float kgh_tanh_softplus_fast(float y) {
+  float e = __expf(fminf(y, 20.0f));
+  float n = e * (e + 2.0f);
+  return y > 20.0f ? 1.0f : n * __builtin_amdgcn_rcpf(n + 2.0f);
+}
+
+__device__ __forceinline__ float kgh_activate_fast(float x, int act) {
+  switch(act) {
+    case KGH_ACT_RELU: return fmaxf(x, 0.0f);
+    case KGH_ACT_MISH: return x * kgh_tanh_softplus_fast(x);
+    case KGH_ACT_MISH_SCALE8: return x * kgh_tanh_softplus_fast(8.0f * x);
+    case KGH_ACT_SILU: return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+    default: return x;
+  }
+}
+
 template<typename T> __device__ __forceinline__ float kgh_to_float(T v) { return (float)v; }
 template<typename T> __device__ __forceinline__ T kgh_from_float(float v) { return (T)v; }
 

@@ -16,6 +16,8 @@
 // current step's matrix-core work.
 #include "kgh_common.h"
 
+#include <climits>
+#include <cstdint>
 #include <vector>
 
 namespace {
@@ -67,9 +69,18 @@ __global__ __launch_bounds__(CONV_THREADS) void convMfmaKernel(const T* __restri
   constexpr int B_VECS = BN * VPR;
   constexpr int B_ITERS = (B_VECS + CONV_THREADS - 1) / CONV_THREADS;
   static_assert(BM * VPR % CONV_THREADS == 0, "A staging must divide evenly");
-
-  __shared__ __attribute__((aligned(16))) T As[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) T Bs[2][BN * LDK];
+  // LDS: double-buffered A and B tiles during the K loop; afterwards the same
+  // memory stages each wave's accumulators (fp32, one 32-column block at a
+  // time, rows padded to 36 floats) for the epilogue.
+  constexpr int A_ELEMS = BM * LDK;
+  constexpr int B_ELEMS = BN * LDK;
+  constexpr int STAGE_LD = 36;
+  constexpr int LOOP_BYTES = 2 * (A_ELEMS + B_ELEMS) * (int)sizeof(T);
+  constexpr int STAGE_BYTES = 4 * WTM * STAGE_LD * 4;
+  constexpr int SMEM_BYTES = LOOP_BYTES > STAGE_BYTES ? LOOP_BYTES : STAGE_BYTES;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM_BYTES];
+  T* As = (T*)smem;
+  T* Bs = As + 2 * A_ELEMS;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -138,12 +149,12 @@ __global__ __launch_bounds__(CONV_THREADS) void convMfmaKernel(const T* __restri
   auto storeShared = [&](int buf) {
 #pragma unroll
     for(int i = 0; i < A_ITERS; i++)
-      *(uint4*)&As[buf][aRow[i] * LDK + aCol[i]] = aReg[i];
+      *(uint4*)&As[buf * A_ELEMS + aRow[i] * LDK + aCol[i]] = aReg[i];
 #pragma unroll
     for(int i = 0; i < B_ITERS; i++) {
       int v = tid + i * CONV_THREADS;
       if(v < B_VECS)
-        *(uint4*)&Bs[buf][(v / VPR) * LDK + (v % VPR) * VEC] = bReg[i];
+        *(uint4*)&Bs[buf * B_ELEMS + (v / VPR) * LDK + (v % VPR) * VEC] = bReg[i];
     }
   };
 
@@ -166,8 +177,8 @@ __global__ __launch_bounds__(CONV_THREADS) void convMfmaKernel(const T* __restri
     const int buf = k & 1;
     if(k + 1 < kIters) loadGlobal(k + 1);
 
-    const T* Ab = As[buf];
-    const T* Bb = Bs[buf];
+    const T* Ab = As + buf * A_ELEMS;
+    const T* Bb = Bs + buf * B_ELEMS;
 #pragma unroll
     for(int ks = 0; ks < BK / Cfg::KSUB; ks++) {
       typename Cfg::Frag af[RB];
@@ -190,19 +201,84 @@ __global__ __launch_bounds__(CONV_THREADS) void convMfmaKernel(const T* __restri
     __syncthreads();
   }
 
+  // Epilogue. For each 32-column block the wave writes its accumulators to
+  // its own LDS region, then each lane takes 16 contiguous channels of one
+  // row: 16-byte vector loads of the residual, 16-byte stores of the raw and
+  // activated outputs, and per-column parameters loaded once per block.
+  float* stage = (float*)smem + wave * WTM * STAGE_LD;
+  const int half = lane & 1;      // which 16-channel half of the 32 columns
+  const int lrow = lane >> 1;     // 0..31
 #pragma unroll
-  for(int rb = 0; rb < RB; rb++) {
+  for(int cb = 0; cb < CB; cb++) {
 #pragma unroll
-    for(int cb = 0; cb < CB; cb++) {
+    for(int rb = 0; rb < RB; rb++)
 #pragma unroll
-      for(int r = 0; r < 16; r++) {
-        int i = wm * WTM + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        int j = wn * WTN + cb * 32 + laneRow;
-        int m = m0 + i;
-        int c = n0 + j;
-        if(m < M && c < cout) kgh_epilogue_store(epi, m, m / HW, c, acc[rb][cb][r]);
+      for(int r = 0; r < 16; r++)
+        stage[(rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * STAGE_LD + laneRow] = acc[rb][cb][r];
+    __syncthreads();
+
+    const int c0 = n0 + wn * WTN + cb * 32 + half * 16;  // first of this lane's 16 channels
+    const bool rawCols = c0 < epi.rawEnd;                // the split points are multiples of 16
+    const bool actCols = epi.outAct != nullptr && c0 >= epi.actBegin;
+    float aS[16], aB[16];
+    if(actCols) {
+#pragma unroll
+      for(int j = 0; j < 16; j++) {
+        aS[j] = epi.actScale[c0 - epi.actBegin + j];
+        aB[j] = epi.actBias[c0 - epi.actBegin + j];
       }
     }
+#pragma unroll 1
+    for(int rb = 0; rb < RB; rb++) {
+      const int lr = rb * 32 + lrow;
+      const int m = m0 + wm * WTM + lr;
+      if(m < M) {
+        float v[16];
+        const float4* src = (const float4*)&stage[lr * STAGE_LD + half * 16];
+#pragma unroll
+        for(int q = 0; q < 4; q++) {
+          float4 t = src[q];
+          v[4 * q + 0] = t.x;
+          v[4 * q + 1] = t.y;
+          v[4 * q + 2] = t.z;
+          v[4 * q + 3] = t.w;
+        }
+        const float msk = epi.mask[m];
+        if(epi.ncBias != nullptr) {
+          const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
+#pragma unroll
+          for(int j = 0; j < 16; j++) v[j] += nb[j];
+        }
+        if(epi.residual != nullptr) {
+          T res[16];
+          const uint4* rp = (const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0);
+#pragma unroll
+          for(int q = 0; q < 16 / VEC; q++) ((uint4*)res)[q] = rp[q];
+#pragma unroll
+          for(int j = 0; j < 16; j++) {
+            float r = kgh_to_float(res[j]);
+            v[j] = epi.maskResidualAdd ? r + v[j] * msk : r + v[j];
+          }
+        }
+        if(rawCols) {
+          T o[16];
+#pragma unroll
+          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(v[j]);
+          uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
+#pragma unroll
+          for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+        }
+        if(actCols) {
+          T o[16];
+#pragma unroll
+          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk);
+          uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin));
+#pragma unroll
+          for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+        }
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -299,7 +375,17 @@ template<typename T>
 void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky, int kx, const void* wPrepared,
                 const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma) {
   bool done = false;
-  if(wPrepared != nullptr && convMfmaSupported<T>(cinPad, cout) && cinStride % (16 / (int)sizeof(T)) == 0) {
+  // The matrix-core kernel's epilogue moves 16 channels per lane with 16-byte
+  // accesses: split points must fall on 16-channel boundaries and every row
+  // start must be 16-byte aligned.
+  const int vec = 16 / (int)sizeof(T);
+  auto on16 = [](int v) { return v == INT_MAX || v % 16 == 0; };
+  auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool epiOk = on16(epi.rawEnd) && on16(epi.actBegin) &&
+                     (epi.outRaw == nullptr || (epi.ldRaw % vec == 0 && aligned(epi.outRaw))) &&
+                     (epi.outAct == nullptr || (epi.ldAct % vec == 0 && aligned(epi.outAct))) &&
+                     (epi.residual == nullptr || (epi.ldRes % vec == 0 && aligned(epi.residual)));
+  if(wPrepared != nullptr && epiOk && convMfmaSupported<T>(cinPad, cout) && cinStride % vec == 0) {
     if(ky == 3 && kx == 3) done = dispatchMfmaTile<T, 3>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
     else if(ky == 1 && kx == 1) done = dispatchMfmaTile<T, 1>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
   }
