@@ -51,7 +51,9 @@ constexpr int CONV_THREADS = 256;
 // supplies row (l % 32) of A and column (l % 32) of B for k-group (l / 32);
 // result register r of lane l holds C[(r/4)*8 + (l/32)*4 + r%4][l % 32].
 template<typename T, int KS, int BN, int WM>
-__global__ __launch_bounds__(CONV_THREADS) void convMfmaKernel(const T* __restrict__ x, int cinStride, int cinPad, int cout,
+// Three workgroups per CU (<= 168 registers per lane, ~51 KB LDS each) so a
+// batch-256 19x19 launch (722 row tiles) fits the 768 slots of 256 CUs at once.
+__global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __restrict__ x, int cinStride, int cinPad, int cout,
                                                                const T* __restrict__ w, BoardGeom g, ConvEpilogue<T> epi) {
   using Cfg = MfmaCfg<T>;
   constexpr int BM = CONV_BM;
@@ -89,7 +91,15 @@ __global__ __launch_bounds__(CONV_THREADS) void convMfmaKernel(const T* __restri
   const int wn = wave % WN;
   const int HW = g.H * g.W;
   const int M = g.batch * HW;
-  const int m0 = blockIdx.x * BM;
+  // Workgroups are dealt round-robin to the 8 XCDs; remap so that each XCD
+  // owns a contiguous run of row tiles, whose overlapping 3x3 halo rows then
+  // hit in that XCD's L2.
+  const int tiles = gridDim.x;
+  const int xcd = blockIdx.x & 7;
+  const int perXcd = tiles >> 3;
+  const int extra = tiles & 7;
+  const int tile = xcd * perXcd + (xcd < extra ? xcd : extra) + (blockIdx.x >> 3);
+  const int m0 = tile * BM;
   const int n0 = blockIdx.y * BN;
 
   // Per-thread staging coordinates, fixed for the whole K loop.
