@@ -42,6 +42,22 @@ def conv_flops(layers, hw):
     return f3, f1, other
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "convMfmaKernel_b18c384nbt_b256_fp16_traffic.md")
+
+
+def measured_traffic():
+    """HBM-side bytes per 3x3 conv launch, from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (scaled by a plain-copy calibration); None
+    when the summary is absent."""
+    import re
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
+
+
 def cpu_baseline(path, seconds_target=15.0):
     """The oracle (fp32 Eigen-algorithm restatement) on T host threads, each
     running forwards of batch 8, as the reference's Eigen deployment runs one
@@ -87,11 +103,25 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--model-dir", default=None)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (torch), to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU. Rows are independent and weights replicated, so N GPUs run N independent "
               "handles with no communication; this build does not launch multi-GPU runs.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        import torch
+        nbytes = args.copy_calibration << 20
+        src = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": nbytes, "copies": 5}), flush=True)
+        return
 
     import numpy as np
     from katago_amd import modelgen, nn
@@ -159,7 +189,7 @@ def main():
         "gflop_per_eval": round(flops_per_eval / 1e9, 3),
         "roofline": {"bound": "mfma", "kernel": "convMfmaKernel (3x3, fp16)", "achieved": round(achieved3, 2),
                      "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved3 / PEAK_FP16_TFLOPS, 4),
-                     "traffic": None, "avg_launch_ms": round(avg3_ms, 5), "launches": n3},
+                     "traffic": measured_traffic(), "avg_launch_ms": round(avg3_ms, 5), "launches": n3},
     }
     if not args.no_cpu:
         print("bench: timing CPU baseline", file=sys.stderr, flush=True)
