@@ -126,9 +126,12 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
   uint4 aReg[A_ITERS];
   uint4 bReg[B_ITERS];
 
+  // K order: channel chunk outer, tap inner, so the KS*KS consecutive steps
+  // over one chunk re-read one small window of input rows (L2/L1 hits).
   auto loadGlobal = [&](int k) {
-    int tap = k / cChunks;
-    int c0 = (k - tap * cChunks) * BK;
+    int chunk = k / (KS * KS);
+    int tap = k - chunk * (KS * KS);
+    int c0 = chunk * BK;
     int dy = tap / KS - KS / 2;
     int dx = tap % KS - KS / 2;
 #pragma unroll
