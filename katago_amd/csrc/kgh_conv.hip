@@ -17,6 +17,7 @@
 #include "kgh_common.h"
 
 #include <climits>
+#include <type_traits>
 #include <cstdint>
 #include <vector>
 
@@ -46,6 +47,117 @@ template<> struct MfmaCfg<float> {
 
 constexpr int CONV_BM = 128;
 constexpr int CONV_THREADS = 256;
+constexpr int CONV_STAGE_LD = 36;  // fp32 row stride of the epilogue's accumulator stage
+constexpr int convStageBytes(int WM) { return 4 * (CONV_BM / WM) * CONV_STAGE_LD * 4; }
+
+// Workgroups are dealt round-robin to the 8 XCDs; this remaps blockIdx.x so
+// that each XCD owns a contiguous run of row tiles, whose overlapping 3x3
+// halo rows then hit in that XCD's L2. A bijection on [0, gridDim.x).
+__device__ __forceinline__ int xcdContiguousTile() {
+  const int tiles = gridDim.x;
+  const int xcd = blockIdx.x & 7;
+  const int perXcd = tiles >> 3;
+  const int extra = tiles & 7;
+  return xcd * perXcd + (xcd < extra ? xcd : extra) + (blockIdx.x >> 3);
+}
+
+// Epilogue shared by the matrix-core conv kernels; requires
+// convStageBytes(WM) bytes of LDS at smem and must be reached by every
+// thread of the workgroup (it contains barriers).
+template<typename T, int BN, int WM>
+__device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM / 32][BN / (4 / WM) / 32], unsigned char* smem,
+                                                  int m0, int n0, int M, int HW, const ConvEpilogue<T>& epi) {
+  // Epilogue. For each 32-column block the wave writes its accumulators to
+  // its own LDS region, then each lane takes 16 contiguous channels of one
+  // row: 16-byte vector loads of the residual, 16-byte stores of the raw and
+  // activated outputs, and per-column parameters loaded once per block.
+  constexpr int WN = 4 / WM;
+  constexpr int WTM = CONV_BM / WM;
+  constexpr int WTN = BN / WN;
+  constexpr int RB = WTM / 32;
+  constexpr int CB = WTN / 32;
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int laneRow = lane & 31;
+  float* stage = (float*)smem + wave * WTM * CONV_STAGE_LD;
+  const int half = lane & 1;      // which 16-channel half of the 32 columns
+  const int lrow = lane >> 1;     // 0..31
+#pragma unroll
+  for(int cb = 0; cb < CB; cb++) {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int r = 0; r < 16; r++)
+        stage[(rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * CONV_STAGE_LD + laneRow] = acc[rb][cb][r];
+    __syncthreads();
+
+    const int c0 = n0 + wn * WTN + cb * 32 + half * 16;  // first of this lane's 16 channels
+    const bool rawCols = c0 < epi.rawEnd;                // the split points are multiples of 16
+    const bool actCols = epi.outAct != nullptr && c0 >= epi.actBegin;
+    float aS[16], aB[16];
+    if(actCols) {
+#pragma unroll
+      for(int j = 0; j < 16; j++) {
+        aS[j] = epi.actScale[c0 - epi.actBegin + j];
+        aB[j] = epi.actBias[c0 - epi.actBegin + j];
+      }
+    }
+#pragma unroll 1
+    for(int rb = 0; rb < RB; rb++) {
+      const int lr = rb * 32 + lrow;
+      const int m = m0 + wm * WTM + lr;
+      if(m < M) {
+        float v[16];
+        const float4* src = (const float4*)&stage[lr * CONV_STAGE_LD + half * 16];
+#pragma unroll
+        for(int q = 0; q < 4; q++) {
+          float4 t = src[q];
+          v[4 * q + 0] = t.x;
+          v[4 * q + 1] = t.y;
+          v[4 * q + 2] = t.z;
+          v[4 * q + 3] = t.w;
+        }
+        const float msk = epi.mask[m];
+        if(epi.ncBias != nullptr) {
+          const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
+#pragma unroll
+          for(int j = 0; j < 16; j++) v[j] += nb[j];
+        }
+        if(epi.residual != nullptr) {
+          T res[16];
+          const uint4* rp = (const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0);
+#pragma unroll
+          for(int q = 0; q < 16 / VEC; q++) ((uint4*)res)[q] = rp[q];
+#pragma unroll
+          for(int j = 0; j < 16; j++) {
+            float r = kgh_to_float(res[j]);
+            v[j] = epi.maskResidualAdd ? r + v[j] * msk : r + v[j];
+          }
+        }
+        if(rawCols) {
+          T o[16];
+#pragma unroll
+          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(v[j]);
+          uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
+#pragma unroll
+          for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+        }
+        if(actCols) {
+          T o[16];
+#pragma unroll
+          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk);
+          uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin));
+#pragma unroll
+          for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
 
 // Operand layout of a 32x32 matrix-core tile (both instructions above): lane l
 // supplies row (l % 32) of A and column (l % 32) of B for k-group (l / 32);
@@ -76,9 +188,8 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
   // time, rows padded to 36 floats) for the epilogue.
   constexpr int A_ELEMS = BM * LDK;
   constexpr int B_ELEMS = BN * LDK;
-  constexpr int STAGE_LD = 36;
   constexpr int LOOP_BYTES = 2 * (A_ELEMS + B_ELEMS) * (int)sizeof(T);
-  constexpr int STAGE_BYTES = 4 * WTM * STAGE_LD * 4;
+  constexpr int STAGE_BYTES = convStageBytes(WM);
   constexpr int SMEM_BYTES = LOOP_BYTES > STAGE_BYTES ? LOOP_BYTES : STAGE_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM_BYTES];
   T* As = (T*)smem;
@@ -91,15 +202,7 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
   const int wn = wave % WN;
   const int HW = g.H * g.W;
   const int M = g.batch * HW;
-  // Workgroups are dealt round-robin to the 8 XCDs; remap so that each XCD
-  // owns a contiguous run of row tiles, whose overlapping 3x3 halo rows then
-  // hit in that XCD's L2.
-  const int tiles = gridDim.x;
-  const int xcd = blockIdx.x & 7;
-  const int perXcd = tiles >> 3;
-  const int extra = tiles & 7;
-  const int tile = xcd * perXcd + (xcd < extra ? xcd : extra) + (blockIdx.x >> 3);
-  const int m0 = tile * BM;
+  const int m0 = xcdContiguousTile() * BM;
   const int n0 = blockIdx.y * BN;
 
   // Per-thread staging coordinates, fixed for the whole K loop.
@@ -171,13 +274,27 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
     }
   };
 
+  // For 3x3 convs a plain residual starts the accumulators (lane l, register
+  // r of tile (rb, cb) is C[(r/4)*8 + (l/32)*4 + r%4][l % 32]), exactly as in
+  // the window kernel, so a row rounds identically whichever of the two
+  // kernels its batch size selects. (1x1 convs always run here and add the
+  // residual in the epilogue, from 16-byte vector loads.)
+  const bool resInAcc = KS == 3 && epi.residual != nullptr && !epi.maskResidualAdd;
   floatx16 acc[RB][CB];
 #pragma unroll
   for(int rb = 0; rb < RB; rb++)
 #pragma unroll
     for(int cb = 0; cb < CB; cb++)
 #pragma unroll
-      for(int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+      for(int r = 0; r < 16; r++) {
+        float v = 0.0f;
+        if(resInAcc) {
+          int m = m0 + wm * WTM + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+          m = m < M ? m : M - 1;
+          v = kgh_to_float(epi.residual[(size_t)m * epi.ldRes + n0 + wn * WTN + cb * 32 + (lane & 31)]);
+        }
+        acc[rb][cb][r] = v;
+      }
 
   loadGlobal(0);
   storeShared(0);
@@ -214,24 +331,89 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
     __syncthreads();
   }
 
-  // Epilogue. For each 32-column block the wave writes its accumulators to
-  // its own LDS region, then each lane takes 16 contiguous channels of one
-  // row: 16-byte vector loads of the residual, 16-byte stores of the raw and
-  // activated outputs, and per-column parameters loaded once per block.
-  float* stage = (float*)smem + wave * WTM * STAGE_LD;
-  const int half = lane & 1;      // which 16-channel half of the 32 columns
-  const int lrow = lane >> 1;     // 0..31
+  ConvEpilogue<T> e = epi;
+  if(resInAcc) e.residual = nullptr;
+  storeTileEpilogue<T, BN, WM>(acc, smem, m0, n0, M, HW, e);
+}
+
+// ---------------------------------------------------------------------------
+// 3x3 fp16 convolution for large batches: input window staged once per
+// channel chunk, weights streamed per tap, both by direct global->LDS DMA.
+//
+// A workgroup of 8 wave64s computes a 384-row x BN tile (one tile per CU at
+// batch 256 on 19x19: 241 tiles for 256 CUs); wave (wm, wn) owns a 96 x BN/2
+// sub-tile. The tile's output rows read input rows [m0 - (W+1),
+// m0 + 384 + W+1) over all nine taps, so for each chunk of 32 input channels
+// that window (<= 424 rows, boards up to 19 wide) is staged in LDS once and
+// every tap's A operand is read from it at a row offset of dy*W + dx; a lane
+// zeroes the operand of a tap that leaves the board for its row (a 9-bit
+// mask per row). Only the weights are staged per (chunk, tap) step, three
+// buffers deep; they are shared by all workgroups and stay in L2.
+//
+// global_load_lds_dwordx4 writes lane l's 16 bytes at LDS base + 16 l, so a
+// wave-load fills 16 rows of 64 bytes. LDS rows hold the four 16-byte groups
+// of row r at group index (g ^ ((r >> 1) & 3)), so the eight rows one
+// ds_read_b128 phase touches fall in distinct banks; each lane therefore
+// fetches the global group that belongs in its LDS slot. Every buffer is its
+// own __shared__ array and every access names its array at compile time (the
+// tap loop is unrolled and the chunk loop unrolled by two), so the compiler
+// knows a fragment read never waits on a DMA into another buffer; the waits
+// for DMA completion are explicit vmcnt counts before each barrier.
+constexpr int TW_THREADS = 512;
+constexpr int TW_BM = 384;
+constexpr int TW_PAD_MAX = 20;                   // W + 1 for boards up to 19 wide
+constexpr int TW_WIN_LOADS = 27;                 // 1 KB wave-loads per window: 432 >= 384 + 2 * 20 rows
+constexpr int TW_WIN_BYTES = TW_WIN_LOADS * 1024;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ int swizzled(int row, int group) { return row * 64 + ((group ^ ((row >> 1) & 3)) << 4); }
+
+// s_waitcnt vmcnt(n) (n < 16) leaving the other counters unconstrained.
+template<int N>
+__device__ __forceinline__ void waitVmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0xF70 | N);
+}
+
+// Workgroup barrier without the memory fence of __syncthreads(), whose
+// release semantics would wait for every DMA still in flight (vmcnt(0)).
+// The empty asm statements keep the compiler from moving memory accesses
+// across it; each wave's LDS reads have completed before the barrier (their
+// results feed the matrix instructions before it), and the DMA writes a wave
+// needs after it are covered by the explicit vmcnt wait before it.
+__device__ __forceinline__ void barrierNoFence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Epilogue for one wave's RB x CB block of 32x32 accumulator tiles at rows
+// mBase.., columns nBase..; stage is this wave's 32 x CONV_STAGE_LD floats of
+// LDS. With RES_IN_ACC the accumulators already hold the residual (loaded
+// before the K loop, so its memory latency overlaps the first DMA waits)
+// and only the outputs touch memory here. The stage is private to the wave and a wave's LDS operations execute in order, so no
+// workgroup barrier is needed; the empty asm statements only keep the
+// compiler from reordering the stage accesses.
+template<typename T, int RB, int CB, bool RES_IN_ACC>
+__device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
+                                                  const ConvEpilogue<T>& epi) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int RV = 16 / VEC;  // 16-byte vectors per lane per block
+  const int lane = threadIdx.x & 63;
+  const int laneRow = lane & 31;
+  const int half = lane & 1;   // which 16-channel half of the 32 columns
+  const int lrow = lane >> 1;  // 0..31
+  float msk[RB];
+#pragma unroll
+  for(int rb = 0; rb < RB; rb++) {
+    const int m = mBase + rb * 32 + lrow;
+    msk[rb] = m < M ? epi.mask[m] : 0.0f;
+  }
 #pragma unroll
   for(int cb = 0; cb < CB; cb++) {
-#pragma unroll
-    for(int rb = 0; rb < RB; rb++)
-#pragma unroll
-      for(int r = 0; r < 16; r++)
-        stage[(rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * STAGE_LD + laneRow] = acc[rb][cb][r];
-    __syncthreads();
-
-    const int c0 = n0 + wn * WTN + cb * 32 + half * 16;  // first of this lane's 16 channels
-    const bool rawCols = c0 < epi.rawEnd;                // the split points are multiples of 16
+    const int c0 = nBase + cb * 32 + half * 16;  // first of this lane's 16 channels
+    const bool rawCols = c0 < epi.rawEnd;        // the split points are multiples of 16
     const bool actCols = epi.outAct != nullptr && c0 >= epi.actBegin;
     float aS[16], aB[16];
     if(actCols) {
@@ -241,36 +423,38 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
         aB[j] = epi.actBias[c0 - epi.actBegin + j];
       }
     }
-#pragma unroll 1
-    for(int rb = 0; rb < RB; rb++) {
-      const int lr = rb * 32 + lrow;
-      const int m = m0 + wm * WTM + lr;
-      if(m < M) {
-        float v[16];
-        const float4* src = (const float4*)&stage[lr * STAGE_LD + half * 16];
 #pragma unroll
-        for(int q = 0; q < 4; q++) {
-          float4 t = src[q];
-          v[4 * q + 0] = t.x;
-          v[4 * q + 1] = t.y;
-          v[4 * q + 2] = t.z;
-          v[4 * q + 3] = t.w;
-        }
-        const float msk = epi.mask[m];
+    for(int rb = 0; rb < RB; rb++) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for(int r = 0; r < 16; r++) stage[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * CONV_STAGE_LD + laneRow] = acc[rb][cb][r];
+      asm volatile("" ::: "memory");
+      float v[16];
+      const float4* src = (const float4*)&stage[lrow * CONV_STAGE_LD + half * 16];
+#pragma unroll
+      for(int q = 0; q < 4; q++) {
+        float4 t = src[q];
+        v[4 * q + 0] = t.x;
+        v[4 * q + 1] = t.y;
+        v[4 * q + 2] = t.z;
+        v[4 * q + 3] = t.w;
+      }
+      const int m = mBase + rb * 32 + lrow;
+      if(m < M) {
         if(epi.ncBias != nullptr) {
           const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
 #pragma unroll
           for(int j = 0; j < 16; j++) v[j] += nb[j];
         }
-        if(epi.residual != nullptr) {
-          T res[16];
+        if(!RES_IN_ACC && epi.residual != nullptr) {
+          T rv[16];
           const uint4* rp = (const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0);
 #pragma unroll
-          for(int q = 0; q < 16 / VEC; q++) ((uint4*)res)[q] = rp[q];
+          for(int q = 0; q < RV; q++) ((uint4*)rv)[q] = rp[q];
 #pragma unroll
           for(int j = 0; j < 16; j++) {
-            float r = kgh_to_float(res[j]);
-            v[j] = epi.maskResidualAdd ? r + v[j] * msk : r + v[j];
+            float r = kgh_to_float(rv[j]);
+            v[j] = epi.maskResidualAdd ? r + v[j] * msk[rb] : r + v[j];
           }
         }
         if(rawCols) {
@@ -279,20 +463,265 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
           for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(v[j]);
           uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
 #pragma unroll
-          for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+          for(int q = 0; q < RV; q++) dst[q] = ((const uint4*)o)[q];
         }
         if(actCols) {
           T o[16];
 #pragma unroll
-          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk);
+          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk[rb]);
           uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin));
 #pragma unroll
-          for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+          for(int q = 0; q < RV; q++) dst[q] = ((const uint4*)o)[q];
         }
       }
     }
-    __syncthreads();
   }
+}
+
+template<int BN>
+__global__ __launch_bounds__(TW_THREADS, 1) void convTapWindowKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
+                                                                    int cout, const half_t* __restrict__ w, BoardGeom g,
+                                                                    ConvEpilogue<half_t> epi) {
+  constexpr int WN = 2;
+  constexpr int WTM = TW_BM / 4;  // 96
+  constexpr int WTN = BN / WN;
+  constexpr int RB = WTM / 32;
+  constexpr int CB = WTN / 32;
+  static_assert(WTN % 32 == 0, "wave tile must be a multiple of 32 columns");
+  // Waves 0-3 stream the weights (B_PER 1 KB wave-loads each per step, three
+  // steps ahead into four buffers); waves 4-7 stream the next chunk's window
+  // (seven wave-loads each during taps 0..4 of the current chunk). Each wave
+  // waits only on its own kind of load, with exact vmcnt counts.
+  constexpr int B_PER = BN / 16 / 4;
+  static_assert(B_PER * 64 == BN, "weights split evenly over four waves");
+  constexpr int W_PER = (TW_WIN_LOADS + 3) / 4;  // 7
+  static_assert(W_PER == 7, "window load schedule below assumes seven loads per wave");
+  __shared__ __attribute__((aligned(1024))) unsigned char win0[TW_WIN_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char win1[TW_WIN_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt0[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt1[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt2[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt3[BN * 64];
+  __shared__ __attribute__((aligned(16))) float stage[8 * 32 * CONV_STAGE_LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool weightWave = wave < 4;
+  const int loaderIdx = wave & 3;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int HW = g.H * g.W;
+  const int M = g.batch * HW;
+  const int m0 = xcdContiguousTile() * TW_BM;
+  const int n0 = blockIdx.y * BN;
+  const int pad = g.W + 1;
+  const int laneRow = lane & 31;
+  const int kq = lane >> 5;
+
+  // Tap validity of this lane's A rows: bit t set if tap t = (dy+1)*3 + dx+1
+  // stays on the board.
+  unsigned tapMask[RB];
+#pragma unroll
+  for(int rb = 0; rb < RB; rb++) {
+    const int m = m0 + wm * WTM + rb * 32 + laneRow;
+    unsigned bits = 0;
+    if(m < M) {
+      const int sp = m % HW;
+      const int y = sp / g.W;
+      const int xx = sp - y * g.W;
+#pragma unroll
+      for(int t = 0; t < 9; t++) {
+        const int yy = y + t / 3 - 1;
+        const int xc = xx + t % 3 - 1;
+        if(yy >= 0 && yy < g.H && xc >= 0 && xc < g.W) bits |= 1u << t;
+      }
+    }
+    tapMask[rb] = bits;
+  }
+
+  // DMA sources. Wave-load j fills LDS rows 16 j .. 16 j + 15; lane l writes
+  // row 16 j + (l >> 2), physical group l & 3, and so fetches logical group
+  // (l & 3) ^ ((row >> 1) & 3) of that row. The swizzle term only depends on
+  // (l >> 3) & 3, the same for every j. Element offsets are 32-bit: the host
+  // keeps tensors below 2^31 elements.
+  const int dRow = lane >> 2;
+  const int dGroup = (lane & 3) ^ ((lane >> 3) & 3);
+  // Window wave-load i of this loader covers j = loaderIdx + 4 i.
+  int winSrc[W_PER];
+#pragma unroll
+  for(int i = 0; i < W_PER; i++) {
+    int j = loaderIdx + 4 * i;
+    j = j < TW_WIN_LOADS ? j : TW_WIN_LOADS - 1;
+    int gm = m0 - pad + 16 * j + dRow;
+    gm = gm < 0 ? 0 : (gm >= M ? M - 1 : gm);  // rows outside [0, M) only feed masked taps
+    winSrc[i] = gm * cinStride + dGroup * 8;
+  }
+  // Weight wave-load i of this loader covers j = loaderIdx * B_PER + i.
+  const int wtSrc = (n0 + 16 * loaderIdx * B_PER + dRow) * cinPad + dGroup * 8;
+  const int tapStride = cout * cinPad;
+  const int cChunks = cinPad / 32;
+  const int steps = 9 * cChunks;
+
+  auto loadWindowPart = [&](unsigned char* dst, int c, int i) {
+    const int j = loaderIdx + 4 * i;
+    if(j < TW_WIN_LOADS)
+      __builtin_amdgcn_global_load_lds((const void*)(x + winSrc[i] + c * 32), (lds_void_t*)(dst + j * 1024), 16, 0, 0);
+  };
+  // Steps past the end re-read the last step (valid addresses) into a buffer
+  // nobody reads again, so the vmcnt counts stay constant.
+  auto loadWeights = [&](unsigned char* dst, int s) {
+    s = s < steps ? s : steps - 1;
+    const int c = s / 9;
+    const int t = s - 9 * c;
+#pragma unroll
+    for(int i = 0; i < B_PER; i++)
+      __builtin_amdgcn_global_load_lds((const void*)(w + t * tapStride + wtSrc + i * 16 * cinPad + c * 32),
+                                       (lds_void_t*)(dst + (loaderIdx * B_PER + i) * 1024), 16, 0, 0);
+  };
+
+  int aRow[RB];
+#pragma unroll
+  for(int rb = 0; rb < RB; rb++) aRow[rb] = wm * WTM + rb * 32 + laneRow + pad;
+  int bOff[CB][2];
+#pragma unroll
+  for(int cb = 0; cb < CB; cb++)
+#pragma unroll
+    for(int ks = 0; ks < 2; ks++) bOff[cb][ks] = swizzled(wn * WTN + cb * 32 + laneRow, ks * 2 + kq);
+
+  // The residual (if any) starts the accumulators: lane l, register r of
+  // tile (rb, cb) is C[(r/4)*8 + (l/32)*4 + r%4][l % 32].
+  floatx16 acc[RB][CB];
+  if(epi.residual != nullptr) {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++)
+#pragma unroll
+        for(int r = 0; r < 16; r++) {
+          int m = m0 + wm * WTM + rb * 32 + (r >> 2) * 8 + kq * 4 + (r & 3);
+          m = m < M ? m : M - 1;
+          acc[rb][cb][r] = (float)epi.residual[(size_t)m * epi.ldRes + n0 + wn * WTN + cb * 32 + laneRow];
+        }
+  }
+  else {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++)
+#pragma unroll
+        for(int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+  }
+
+  const half8_t zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  // Fragments of one half step (16 of the 32 channels of a chunk): A rows of
+  // tap t from a window, B columns from a weight buffer.
+  half8_t af[RB], bf[CB];
+  auto readHalf = [&](const unsigned char* winBuf, const unsigned char* wtBuf, const int (&rowsC)[RB], int t, int ks) {
+    const int off = (t / 3 - 1) * g.W + (t % 3 - 1);
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++) {
+      af[rb] = *(const half8_t*)(winBuf + swizzled(rowsC[rb] + off, ks * 2 + kq));
+      if(!((tapMask[rb] >> t) & 1u)) af[rb] = zero;
+    }
+#pragma unroll
+    for(int cb = 0; cb < CB; cb++) bf[cb] = *(const half8_t*)(wtBuf + bOff[cb][ks]);
+  };
+  auto mma = [&](const half8_t (&a)[RB], const half8_t (&b)[CB]) {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++) acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[rb], b[cb], acc[rb][cb], 0, 0, 0);
+  };
+
+  // Prologue: weights of steps 0..2 (0 and 1 landed), window of chunk 0.
+  if(weightWave) {
+    loadWeights(wt0, 0);
+    loadWeights(wt1, 1);
+    loadWeights(wt2, 2);
+    waitVmcnt<B_PER>();
+  }
+  else {
+#pragma unroll
+    for(int i = 0; i < W_PER; i++) loadWindowPart(win0, 0, i);
+    waitVmcnt<0>();
+  }
+  barrierNoFence();
+  {
+    int rows0[RB];
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++) rows0[rb] = aRow[rb];
+    readHalf(win0, wt0, rows0, 0, 0);
+  }
+
+  // Step s = 9c + t uses weight buffer s % 4 = (c + t) % 4 (9 = 1 mod 4), so
+  // the chunk loop is unrolled by four and P = c % 4 is a constant. During
+  // step s: DMA the weights of step s + 3 and parts of the next chunk's
+  // window; read the second half-step fragments of s, then (after the first
+  // half's matrix work) the first half-step fragments of s + 1, whose
+  // weights landed before the previous barrier; the barrier that ends step s
+  // publishes the weights of step s + 2.
+  auto wtBuf = [&](int i) -> unsigned char* {
+    i &= 3;
+    return i == 0 ? wt0 : i == 1 ? wt1 : i == 2 ? wt2 : wt3;
+  };
+  auto chunk = [&](auto pTag, int c) {
+    constexpr int P = decltype(pTag)::value;
+    unsigned char* cur = (P & 1) ? win1 : win0;
+    unsigned char* nxt = (P & 1) ? win0 : win1;
+    const bool moreChunks = c + 1 < cChunks;
+    // Opaque per chunk, so the compiler does not hoist all tap addresses
+    // out of the chunk loop (they would stay live in registers).
+    int rowsC[RB];
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++) {
+      rowsC[rb] = aRow[rb];
+      asm volatile("" : "+v"(rowsC[rb]));
+    }
+#pragma unroll
+    for(int t = 0; t < 9; t++) {
+      const unsigned char* wCur = wtBuf(P + t);
+      if(weightWave) loadWeights(wtBuf(P + t + 3), 9 * c + t + 3);
+      else if(moreChunks && t < 5) {
+        if(t < 2) {
+          loadWindowPart(nxt, c + 1, 2 * t);
+          loadWindowPart(nxt, c + 1, 2 * t + 1);
+        }
+        else loadWindowPart(nxt, c + 1, t + 2);
+      }
+      half8_t a0[RB], b0[CB];
+#pragma unroll
+      for(int rb = 0; rb < RB; rb++) a0[rb] = af[rb];
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++) b0[cb] = bf[cb];
+      readHalf(cur, wCur, rowsC, t, 1);
+      mma(a0, b0);
+      half8_t a1[RB], b1[CB];
+#pragma unroll
+      for(int rb = 0; rb < RB; rb++) a1[rb] = af[rb];
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++) b1[cb] = bf[cb];
+      // First half of step s + 1 (past the last step it re-reads valid
+      // LDS and is discarded).
+      if(t < 8) readHalf(cur, wtBuf(P + t + 1), rowsC, t + 1, 0);
+      else readHalf(nxt, wtBuf(P + t + 1), rowsC, 0, 0);
+      mma(a1, b1);
+      if(weightWave) waitVmcnt<B_PER>();
+      else if(t == 7) waitVmcnt<0>();  // next chunk's window complete before step t = 8 reads it
+      barrierNoFence();
+    }
+  };
+
+  for(int c = 0; c < cChunks; c += 4) {
+    chunk(std::integral_constant<int, 0>(), c);
+    if(c + 1 < cChunks) chunk(std::integral_constant<int, 1>(), c + 1);
+    if(c + 2 < cChunks) chunk(std::integral_constant<int, 2>(), c + 2);
+    if(c + 3 < cChunks) chunk(std::integral_constant<int, 3>(), c + 3);
+  }
+  waitVmcnt<0>();
+  __syncthreads();
+
+  storeWaveEpilogue<half_t, RB, CB, true>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, epi);
 }
 
 // Direct convolution: one thread per output element. Used for shapes the
@@ -363,6 +792,37 @@ void launchMfma(const T* x, int cinStride, int cinPad, int cout, const T* w, Boa
   KGH_CHECK_LAUNCH();
 }
 
+template<int BN>
+void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                     const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  int M = g.batch * g.H * g.W;
+  dim3 grid((M + TW_BM - 1) / TW_BM, cout / BN);
+  hipLaunchKernelGGL((convTapWindowKernel<BN>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  KGH_CHECK_LAUNCH();
+}
+
+// The window kernel: fp16, 3x3, plain residual adds (it starts the
+// accumulators from the residual), boards at most TW_PAD_MAX - 1 wide, enough
+// rows for at least 128 of its 384-row tiles (smaller batches keep more CUs
+// busy with the 128-row kernel), 32-bit element offsets.
+template<typename T>
+bool dispatchTapWindow(const T*, int, int, int, const T*, BoardGeom, const ConvEpilogue<T>&, hipStream_t) {
+  return false;
+}
+template<>
+bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                               const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  const long M = (long)g.batch * g.H * g.W;
+  if(g.W + 1 > TW_PAD_MAX || cinPad % 32 != 0 || cinStride % 8 != 0 || epi.maskResidualAdd) return false;
+  if(M < 128L * TW_BM) return false;
+  if(M * cinStride >= (1L << 31) || 9L * cout * cinPad >= (1L << 31)) return false;
+  if(cout % 192 == 0) launchTapWindow<192>(x, cinStride, cinPad, cout, w, g, epi, stream);
+  else if(cout % 128 == 0) launchTapWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream);
+  else if(cout % 64 == 0) launchTapWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+  else return false;
+  return true;
+}
+
 template<typename T, int KS>
 bool dispatchMfmaTile(const T* x, int cinStride, int cinPad, int cout, const T* w, BoardGeom g, const ConvEpilogue<T>& epi,
                       hipStream_t stream) {
@@ -399,7 +859,10 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
                      (epi.outAct == nullptr || (epi.ldAct % vec == 0 && aligned(epi.outAct))) &&
                      (epi.residual == nullptr || (epi.ldRes % vec == 0 && aligned(epi.residual)));
   if(wPrepared != nullptr && epiOk && convMfmaSupported<T>(cinPad, cout) && cinStride % vec == 0) {
-    if(ky == 3 && kx == 3) done = dispatchMfmaTile<T, 3>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
+    if(ky == 3 && kx == 3) {
+      done = dispatchTapWindow<T>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
+      if(!done) done = dispatchMfmaTile<T, 3>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
+    }
     else if(ky == 1 && kx == 1) done = dispatchMfmaTile<T, 1>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
   }
   if(usedMfma != nullptr) *usedMfma = done;
