@@ -159,6 +159,51 @@ __device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM /
   }
 }
 
+// Loads a wave's RB x CB tiles of a plain residual into the accumulators:
+// 16-byte row-major loads (lane: row lane >> 1, channels 16 * (lane & 1)..),
+// all issued before the first is used, then a transpose through this wave's
+// stage (32 x CONV_STAGE_LD floats) into the matrix-core C layout (lane l,
+// register r of tile (rb, cb) is C[(r/4)*8 + (l/32)*4 + r%4][l % 32]). Rows
+// at or past M read row M - 1; the epilogue never stores them.
+template<typename T, int RB, int CB>
+__device__ __forceinline__ void residualToAcc(floatx16 (&acc)[RB][CB], const T* __restrict__ residual, int ldRes, int mBase,
+                                              int nBase, int M, float* stage) {
+  constexpr int RV = 16 * (int)sizeof(T) / 16;  // 16-byte vectors per 16 channels
+  const int lane = threadIdx.x & 63;
+  const int half = lane & 1;
+  const int lrow = lane >> 1;
+  const int laneRow = lane & 31;
+  uint4 raw[RB][CB][RV];
+#pragma unroll
+  for(int rb = 0; rb < RB; rb++) {
+    int m = mBase + rb * 32 + lrow;
+    m = m < M ? m : M - 1;
+#pragma unroll
+    for(int cb = 0; cb < CB; cb++) {
+      const uint4* rp = (const uint4*)(residual + (size_t)m * ldRes + nBase + cb * 32 + half * 16);
+#pragma unroll
+      for(int q = 0; q < RV; q++) raw[rb][cb][q] = rp[q];
+    }
+  }
+#pragma unroll
+  for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+    for(int cb = 0; cb < CB; cb++) {
+      const T* hv = (const T*)raw[rb][cb];
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for(int q = 0; q < 4; q++) {
+        float4 f = make_float4(kgh_to_float(hv[4 * q]), kgh_to_float(hv[4 * q + 1]), kgh_to_float(hv[4 * q + 2]),
+                               kgh_to_float(hv[4 * q + 3]));
+        *(float4*)&stage[lrow * CONV_STAGE_LD + half * 16 + 4 * q] = f;
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for(int r = 0; r < 16; r++) acc[rb][cb][r] = stage[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * CONV_STAGE_LD + laneRow];
+    }
+  asm volatile("" ::: "memory");
+}
+
 // Operand layout of a 32x32 matrix-core tile (both instructions above): lane l
 // supplies row (l % 32) of A and column (l % 32) of B for k-group (l / 32);
 // result register r of lane l holds C[(r/4)*8 + (l/32)*4 + r%4][l % 32].
@@ -274,27 +319,24 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
     }
   };
 
-  // For 3x3 convs a plain residual starts the accumulators (lane l, register
-  // r of tile (rb, cb) is C[(r/4)*8 + (l/32)*4 + r%4][l % 32]), exactly as in
-  // the window kernel, so a row rounds identically whichever of the two
-  // kernels its batch size selects. (1x1 convs always run here and add the
-  // residual in the epilogue, from 16-byte vector loads.)
-  const bool resInAcc = KS == 3 && epi.residual != nullptr && !epi.maskResidualAdd;
+  // A plain residual starts the accumulators, exactly as in the DMA kernels,
+  // so a row rounds identically whichever kernel its batch size selects. The
+  // transpose goes through LDS before the K loop first uses it.
+  const bool resInAcc = epi.residual != nullptr && !epi.maskResidualAdd;
   floatx16 acc[RB][CB];
+  if(resInAcc) {
+    residualToAcc<T, RB, CB>(acc, epi.residual, epi.ldRes, m0 + wm * WTM, n0 + wn * WTN, M,
+                             (float*)smem + wave * 32 * CONV_STAGE_LD);
+    __syncthreads();
+  }
+  else {
 #pragma unroll
-  for(int rb = 0; rb < RB; rb++)
+    for(int rb = 0; rb < RB; rb++)
 #pragma unroll
-    for(int cb = 0; cb < CB; cb++)
+      for(int cb = 0; cb < CB; cb++)
 #pragma unroll
-      for(int r = 0; r < 16; r++) {
-        float v = 0.0f;
-        if(resInAcc) {
-          int m = m0 + wm * WTM + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-          m = m < M ? m : M - 1;
-          v = kgh_to_float(epi.residual[(size_t)m * epi.ldRes + n0 + wn * WTN + cb * 32 + (lane & 31)]);
-        }
-        acc[rb][cb][r] = v;
-      }
+        for(int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+  }
 
   loadGlobal(0);
   storeShared(0);
@@ -589,20 +631,10 @@ __global__ __launch_bounds__(TW_THREADS, 1) void convTapWindowKernel(const half_
 #pragma unroll
     for(int ks = 0; ks < 2; ks++) bOff[cb][ks] = swizzled(wn * WTN + cb * 32 + laneRow, ks * 2 + kq);
 
-  // The residual (if any) starts the accumulators: lane l, register r of
-  // tile (rb, cb) is C[(r/4)*8 + (l/32)*4 + r%4][l % 32].
+  // The residual (if any) starts the accumulators.
   floatx16 acc[RB][CB];
   if(epi.residual != nullptr) {
-#pragma unroll
-    for(int rb = 0; rb < RB; rb++)
-#pragma unroll
-      for(int cb = 0; cb < CB; cb++)
-#pragma unroll
-        for(int r = 0; r < 16; r++) {
-          int m = m0 + wm * WTM + rb * 32 + (r >> 2) * 8 + kq * 4 + (r & 3);
-          m = m < M ? m : M - 1;
-          acc[rb][cb][r] = (float)epi.residual[(size_t)m * epi.ldRes + n0 + wn * WTN + cb * 32 + laneRow];
-        }
+    residualToAcc<half_t, RB, CB>(acc, epi.residual, epi.ldRes, m0 + wm * WTM, n0 + wn * WTN, M, stage + wave * 32 * CONV_STAGE_LD);
   }
   else {
 #pragma unroll
@@ -724,6 +756,153 @@ __global__ __launch_bounds__(TW_THREADS, 1) void convTapWindowKernel(const half_
   storeWaveEpilogue<half_t, RB, CB, true>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, epi);
 }
 
+// ---------------------------------------------------------------------------
+// 1x1 fp16 convolution (a GEMM over M = N*H*W rows) for large batches, built
+// like the window kernel: 384-row x BN tiles, 8 wave64s with 96 x BN/2 wave
+// tiles, operands moved by global->LDS DMA in the same swizzled 64-byte-row
+// layout. A step covers 32 input channels; waves 0-3 DMA the weights and
+// waves 4-7 the A rows of the step two ahead, into three buffers of each
+// (step s uses buffer s % 3, so the step loop is unrolled by three). At C2
+// shapes the kernel is bound by HBM (A is read once, outputs written once).
+constexpr int G1_A_LOADS = TW_BM / 16;  // 24 wave-loads of A per step
+
+template<int BN>
+__global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
+                                                                 int cout, const half_t* __restrict__ w, BoardGeom g,
+                                                                 ConvEpilogue<half_t> epi) {
+  constexpr int WN = 2;
+  constexpr int WTM = TW_BM / 4;  // 96
+  constexpr int WTN = BN / WN;
+  constexpr int RB = WTM / 32;
+  constexpr int CB = WTN / 32;
+  static_assert(WTN % 32 == 0, "wave tile must be a multiple of 32 columns");
+  constexpr int B_PER = BN / 16 / 4;
+  static_assert(B_PER * 64 == BN, "weights split evenly over four waves");
+  constexpr int A_PER = G1_A_LOADS / 4;  // 6
+  __shared__ __attribute__((aligned(1024))) unsigned char a0s[G1_A_LOADS * 1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char a1s[G1_A_LOADS * 1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char a2s[G1_A_LOADS * 1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char b0s[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char b1s[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char b2s[BN * 64];
+  __shared__ __attribute__((aligned(16))) float stage[8 * 32 * CONV_STAGE_LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool weightWave = wave < 4;
+  const int loaderIdx = wave & 3;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int HW = g.H * g.W;
+  const int M = g.batch * HW;
+  const int m0 = xcdContiguousTile() * TW_BM;
+  const int n0 = blockIdx.y * BN;
+  const int laneRow = lane & 31;
+  const int kq = lane >> 5;
+
+  // DMA sources (see the window kernel for the lane -> LDS slot mapping).
+  const int dRow = lane >> 2;
+  const int dGroup = (lane & 3) ^ ((lane >> 3) & 3);
+  int aSrc[A_PER];
+#pragma unroll
+  for(int i = 0; i < A_PER; i++) {
+    int gm = m0 + 16 * (loaderIdx + 4 * i) + dRow;
+    gm = gm < M ? gm : M - 1;  // rows past M are never stored
+    aSrc[i] = gm * cinStride + dGroup * 8;
+  }
+  const int wtSrc = (n0 + 16 * loaderIdx * B_PER + dRow) * cinPad + dGroup * 8;
+  const int steps = cinPad / 32;
+
+  auto aBuf = [&](int i) -> unsigned char* { return i == 0 ? a0s : i == 1 ? a1s : a2s; };
+  auto bBuf = [&](int i) -> unsigned char* { return i == 0 ? b0s : i == 1 ? b1s : b2s; };
+  // Steps past the end re-read the last step (valid addresses) into a buffer
+  // nobody reads again, so the vmcnt counts stay constant.
+  auto load = [&](int buf, int st) {
+    st = st < steps ? st : steps - 1;
+    // The distinct asm markers keep the compiler from merging the tails of
+    // the two branches, which would turn the DMA target into a select of
+    // buffers and make every later fragment read wait for all DMA.
+    if(weightWave) {
+#pragma unroll
+      for(int i = 0; i < B_PER; i++)
+        __builtin_amdgcn_global_load_lds((const void*)(w + wtSrc + i * 16 * cinPad + st * 32),
+                                         (lds_void_t*)(bBuf(buf) + (loaderIdx * B_PER + i) * 1024), 16, 0, 0);
+      asm volatile("; weight dma");
+    }
+    else {
+#pragma unroll
+      for(int i = 0; i < A_PER; i++)
+        __builtin_amdgcn_global_load_lds((const void*)(x + aSrc[i] + st * 32), (lds_void_t*)(aBuf(buf) + (loaderIdx + 4 * i) * 1024),
+                                         16, 0, 0);
+      asm volatile("; activation dma");
+    }
+  };
+  auto waitStep = [&]() {
+    if(weightWave) waitVmcnt<B_PER>();
+    else waitVmcnt<A_PER>();
+  };
+
+  int aOff[RB][2], bOff[CB][2];
+#pragma unroll
+  for(int ks = 0; ks < 2; ks++) {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++) aOff[rb][ks] = swizzled(wm * WTM + rb * 32 + laneRow, ks * 2 + kq);
+#pragma unroll
+    for(int cb = 0; cb < CB; cb++) bOff[cb][ks] = swizzled(wn * WTN + cb * 32 + laneRow, ks * 2 + kq);
+  }
+
+  load(0, 0);
+  load(1, 1);
+  const bool resInAcc = epi.residual != nullptr && !epi.maskResidualAdd;
+  floatx16 acc[RB][CB];
+  if(resInAcc) {
+    residualToAcc<half_t, RB, CB>(acc, epi.residual, epi.ldRes, m0 + wm * WTM, n0 + wn * WTN, M, stage + wave * 32 * CONV_STAGE_LD);
+  }
+  else {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++)
+#pragma unroll
+        for(int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+  }
+  waitStep();
+  barrierNoFence();
+
+  auto step = [&](auto pTag, int st) {
+    constexpr int P = decltype(pTag)::value;
+    load((P + 2) % 3, st + 2);
+    const unsigned char* A = aBuf(P);
+    const unsigned char* B = bBuf(P);
+#pragma unroll
+    for(int ks = 0; ks < 2; ks++) {
+      half8_t af[RB], bf[CB];
+#pragma unroll
+      for(int rb = 0; rb < RB; rb++) af[rb] = *(const half8_t*)(A + aOff[rb][ks]);
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++) bf[cb] = *(const half8_t*)(B + bOff[cb][ks]);
+#pragma unroll
+      for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for(int cb = 0; cb < CB; cb++) acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], bf[cb], acc[rb][cb], 0, 0, 0);
+    }
+    waitStep();  // step st + 1 landed; st + 2 may be in flight
+    barrierNoFence();
+  };
+  for(int st = 0; st < steps; st += 3) {
+    step(std::integral_constant<int, 0>(), st);
+    if(st + 1 < steps) step(std::integral_constant<int, 1>(), st + 1);
+    if(st + 2 < steps) step(std::integral_constant<int, 2>(), st + 2);
+  }
+  waitVmcnt<0>();
+  __syncthreads();
+
+  ConvEpilogue<half_t> e = epi;
+  if(resInAcc) e.residual = nullptr;
+  storeWaveEpilogue<half_t, RB, CB, false>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, e);
+}
+
 // Direct convolution: one thread per output element. Used for shapes the
 // matrix-core kernel does not take (tiny channel counts, 5x5, dilation-free
 // odd kernels), in particular the layer-level known-answer tests.
@@ -823,6 +1002,34 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
   return true;
 }
 
+template<int BN>
+void launch1x1Dma(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                  const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  int M = g.batch * g.H * g.W;
+  dim3 grid((M + TW_BM - 1) / TW_BM, cout / BN);
+  hipLaunchKernelGGL((conv1x1DmaKernel<BN>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  KGH_CHECK_LAUNCH();
+}
+
+// The 1x1 DMA kernel: fp16, 32-channel steps, at least 128 of its 384-row
+// tiles, 32-bit element offsets.
+template<typename T>
+bool dispatch1x1Dma(const T*, int, int, int, const T*, BoardGeom, const ConvEpilogue<T>&, hipStream_t) {
+  return false;
+}
+template<>
+bool dispatch1x1Dma<half_t>(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                            const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  const long M = (long)g.batch * g.H * g.W;
+  if(cinPad % 32 != 0 || cinStride % 8 != 0 || M < 128L * TW_BM) return false;
+  if(M * cinStride >= (1L << 31) || (long)cout * cinPad >= (1L << 31)) return false;
+  if(cout % 192 == 0) launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream);
+  else if(cout % 128 == 0) launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream);
+  else if(cout % 64 == 0) launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+  else return false;
+  return true;
+}
+
 template<typename T, int KS>
 bool dispatchMfmaTile(const T* x, int cinStride, int cinPad, int cout, const T* w, BoardGeom g, const ConvEpilogue<T>& epi,
                       hipStream_t stream) {
@@ -863,7 +1070,10 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
       done = dispatchTapWindow<T>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
       if(!done) done = dispatchMfmaTile<T, 3>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
     }
-    else if(ky == 1 && kx == 1) done = dispatchMfmaTile<T, 1>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
+    else if(ky == 1 && kx == 1) {
+      done = dispatch1x1Dma<T>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
+      if(!done) done = dispatchMfmaTile<T, 1>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
+    }
   }
   if(usedMfma != nullptr) *usedMfma = done;
   if(done) return;
