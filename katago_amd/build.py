@@ -37,7 +37,7 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result"]
 # x86-64 server CPU these GPU hosts use.
 ORACLE_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-mavx2", "-mfma", "-Wall"]
 
-HIP_SOURCES = ["kgh_conv.hip", "kgh_kernels.hip", "kgh_api.hip"]
+HIP_SOURCES = ["kgh_conv.hip", "kgh_kernels.hip", "kgh_transformer.hip", "kgh_api.hip"]
 HOST_SOURCES = [
     "host/core/global.cpp",
     "host/neuralnet/desc.cpp",

@@ -12,6 +12,7 @@
 #include "kgh_kernels.h"
 
 #include <algorithm>
+#include <cmath>
 #include <climits>
 #include <cstring>
 #include <memory>
@@ -91,7 +92,16 @@ struct BiasW {
   const float* b = nullptr;
 };
 
-enum BlockKind { BK_ORDINARY = 0, BK_GPOOL = 2, BK_NBT = 3 };
+enum BlockKind { BK_ORDINARY = 0, BK_GPOOL = 2, BK_NBT = 3, BK_ATTENTION = 4, BK_FFN = 5 };
+
+// Rotary-embedding parameters of one attention block; the cos/sin tables
+// depend on the board size and are built per handle.
+struct RopeSpec {
+  int dq = 0, kvHeads = 0;
+  bool learnable = false;
+  float theta = 0.0f;
+  std::vector<float> freqs;  // learnable: [kvHead][pair][2] (x, y)
+};
 
 struct Block {
   int kind = BK_ORDINARY;
@@ -105,6 +115,16 @@ struct Block {
   BNAct gpoolBN;
   MatW gpoolMul;
   std::vector<Block> inner;
+  // transformer blocks: pre-RMSNorm, then qkv (attention: [Q | K | V]
+  // projections; FFN: [linear1 | gate] interleaved in blocks of 8 units) and
+  // proj (attention: output projection; FFN: linear2), as 1x1 convs.
+  int C = 0;
+  float normEps = 0.0f;
+  const float* normW = nullptr;
+  int heads = 0, kvHeads = 0, dq = 0, dv = 0, ffnC = 0;
+  int ropeIndex = -1;
+  bool learnableRope = false;
+  ConvW qkv, proj;
 };
 
 struct HeadConv {
@@ -123,8 +143,14 @@ struct Net {
   ConvW initialConv;
   MatW initialMatMul;
   int trunkC = 0;
-  int tipKind = 0;
+  int tipKind = 0;  // 0: BN; otherwise RMSNorm
   BNAct tipBN;
+  bool tipSpatial = false;
+  float tipEps = 0.0f;
+  const float* tipGamma = nullptr;
+  const float* tipBeta = nullptr;
+  int tipAct = KGH_ACT_IDENTITY;
+  std::vector<RopeSpec> ropes;
   std::vector<Block> blocks;
   // heads
   int p1C = 0, g1C = 0, v1C = 0;
@@ -262,6 +288,26 @@ struct Builder {
     return b;
   }
 
+  // A matmul's [cin][cout] weights as the [cout][cin] weights of a 1x1 conv.
+  static void appendTransposed(std::vector<float>& dst, const float* w, int cin, int cout) {
+    size_t base = dst.size();
+    dst.resize(base + (size_t)cin * cout);
+    for(int o = 0; o < cout; o++)
+      for(int i = 0; i < cin; i++) dst[base + (size_t)o * cin + i] = w[(size_t)i * cout + o];
+  }
+  const kgh_layer& matmulRec(const char* what, int cin, int cout) {
+    const kgh_layer& l = take(KGH_OP_MATMUL, what);
+    if(l.i[0] != cin || l.i[1] != cout) invalid(std::string(what) + ": shape mismatch");
+    dev(l, 0, (int64_t)cin * cout, what);
+    return l;
+  }
+  void trmsnorm(Block& blk, const char* what) {
+    const kgh_layer& l = take(KGH_OP_TRMSNORM, what);
+    if(l.i[0] != blk.C) invalid(std::string(what) + ": channel mismatch");
+    blk.normEps = l.f[0];
+    blk.normW = dev(l, 0, blk.C, what);
+  }
+
   Block block(Net& net, int depth, int streamC) {
     Block blk;
     int op = peek();
@@ -327,8 +373,75 @@ struct Builder {
       if(blk.preBN.C != streamC || blk.conv1.cin != streamC || blk.conv2.cout != streamC || blk.midBN.C != midC || blk.conv2.cin != midC)
         invalid("nested bottleneck block: channel mismatch");
     }
-    else if(op == KGH_OP_BLOCK_ATTENTION || op == KGH_OP_BLOCK_FFN) {
-      unsupported("transformer blocks are not supported by this build of the device library");
+    else if(op == KGH_OP_BLOCK_ATTENTION) {
+      const kgh_layer& h = take(op, "attention block");
+      blk.kind = BK_ATTENTION;
+      blk.C = streamC;
+      blk.heads = h.i[0];
+      blk.kvHeads = h.i[1];
+      blk.dq = h.i[2];
+      blk.dv = h.i[3];
+      const bool useRope = h.i[4] != 0;
+      blk.learnableRope = h.i[5] != 0;
+      if(blk.heads < 1 || blk.kvHeads < 1 || blk.heads % blk.kvHeads != 0 || blk.dq < 2 || blk.dq % 2 != 0 || blk.dv < 1)
+        invalid("attention block: bad head configuration");
+      if(useRope) {
+        RopeSpec rs;
+        rs.dq = blk.dq;
+        rs.kvHeads = blk.kvHeads;
+        rs.learnable = blk.learnableRope;
+        rs.theta = h.f[0];
+        if(rs.learnable) {
+          const int64_t count = (int64_t)blk.kvHeads * (blk.dq / 2) * 2;
+          dev(h, 0, count, "attention ropeFreqs");
+          rs.freqs.assign(host(h, 0), host(h, 0) + count);
+        }
+        blk.ropeIndex = (int)net.ropes.size();
+        net.ropes.push_back(std::move(rs));
+      }
+      trmsnorm(blk, "attention preLN");
+      const int qC = blk.heads * blk.dq, kC = blk.kvHeads * blk.dq, vC = blk.kvHeads * blk.dv, aC = blk.heads * blk.dv;
+      const kgh_layer& q = matmulRec("attention qProj", streamC, qC);
+      const kgh_layer& k = matmulRec("attention kProj", streamC, kC);
+      const kgh_layer& v = matmulRec("attention vProj", streamC, vC);
+      const kgh_layer& o = matmulRec("attention outProj", aC, streamC);
+      std::vector<float> wqkv, wo;
+      appendTransposed(wqkv, host(q, 0), streamC, qC);
+      appendTransposed(wqkv, host(k, 0), streamC, kC);
+      appendTransposed(wqkv, host(v, 0), streamC, vC);
+      appendTransposed(wo, host(o, 0), aC, streamC);
+      blk.qkv = makeConv(upload(wqkv), 1, 1, streamC, qC + kC + vC, false);
+      blk.proj = makeConv(upload(wo), 1, 1, aC, streamC, false);
+      net.tmpC = std::max(net.tmpC, std::max(streamC, std::max(qC + kC + vC, aC)));
+    }
+    else if(op == KGH_OP_BLOCK_FFN) {
+      const kgh_layer& h = take(op, "ffn block");
+      blk.kind = BK_FFN;
+      blk.C = streamC;
+      blk.ffnC = h.i[1];
+      if(h.i[0] != streamC) invalid("ffn block: channel mismatch");
+      if(h.i[2] == 0) unsupported("transformer FFN blocks without SwiGLU are not supported (as in the reference)");
+      if(blk.ffnC < 8 || blk.ffnC % 8 != 0) unsupported("transformer FFN widths must be multiples of 8");
+      trmsnorm(blk, "ffn preLN");
+      const int F = blk.ffnC;
+      const kgh_layer& l1 = matmulRec("ffn linear1", streamC, F);
+      const kgh_layer& gt = matmulRec("ffn linearGate", streamC, F);
+      const kgh_layer& l2 = matmulRec("ffn linear2", F, streamC);
+      // [cout = 2F][cin]: blocks of 8 linear1 units followed by the same 8 gate units.
+      std::vector<float> wg((size_t)2 * F * streamC), w2;
+      const float* w1 = host(l1, 0);
+      const float* wgate = host(gt, 0);
+      for(int u = 0; u < F; u++) {
+        const int r1 = (u / 8) * 16 + (u % 8);
+        for(int i = 0; i < streamC; i++) {
+          wg[(size_t)r1 * streamC + i] = w1[(size_t)i * F + u];
+          wg[(size_t)(r1 + 8) * streamC + i] = wgate[(size_t)i * F + u];
+        }
+      }
+      appendTransposed(w2, host(l2, 0), F, streamC);
+      blk.qkv = makeConv(upload(wg), 1, 1, streamC, 2 * F, false);
+      blk.proj = makeConv(upload(w2), 1, 1, F, streamC, false);
+      net.tmpC = std::max(net.tmpC, std::max(streamC, F));
     }
     else {
       invalid("layer program: expected a block at record " + std::to_string(pos));
@@ -395,6 +508,8 @@ struct kgh_handle {
   int* hSym = nullptr;
   float* hOpt = nullptr;
   float* hOut = nullptr;
+
+  std::vector<const float*> ropeCos, ropeSin;  // per RopeSpec of the model: [table][pair][H*W]
 
   bool profiling = false;
   std::vector<ProfRec> prof;
@@ -495,7 +610,7 @@ struct Runner {
   void runBlock(const Block& b, int depth, const BNAct* next) {
     T* Rd = R[depth];
     T* Ad = A[depth];
-    const int C = b.preBN.C;
+    const int C = (b.kind == BK_ATTENTION || b.kind == BK_FFN) ? b.C : b.preBN.C;
     if(b.kind == BK_ORDINARY) {
       // mid = act(midBN(conv1(A))) * mask
       ConvEpilogue<T> e1 = epi();
@@ -572,6 +687,58 @@ struct Runner {
       setAct(e2, next, Ad, C);
       conv(b.conv2, Am, midC, e2);
     }
+    else if(b.kind == BK_ATTENTION) {
+      // trunk += outProj(attention(rope(qkv(rmsnorm(trunk))))) * mask
+      const int HW = g.H * g.W;
+      const int qC = b.heads * b.dq, kC = b.kvHeads * b.dq, qkvC = b.qkv.cout, aC = b.heads * b.dv;
+      T* xn = tmp1;
+      T* qkv = tmp2;
+      T* att = tmp3;
+      kgh::launchRmsNorm<T>(Rd, C, xn, C, C, b.normW, nullptr, b.normEps, KGH_ACT_IDENTITY, mask, M, s);
+      ConvEpilogue<T> e1 = epi();
+      e1.outRaw = qkv;
+      e1.ldRaw = qkvC;
+      e1.rawEnd = INT_MAX;
+      conv(b.qkv, xn, C, e1);
+      if(b.ropeIndex >= 0) {
+        if(h == nullptr) throw KghError(KGH_ERR_INTERNAL, "rotary embedding needs a handle");
+        kgh::launchRope<T>(qkv, qkvC, b.heads, b.kvHeads, b.dq, h->ropeCos[b.ropeIndex], h->ropeSin[b.ropeIndex], b.learnableRope, HW,
+                           M, s);
+      }
+      kgh::launchAttention<T>(qkv, qkvC, qC, qC + kC, b.heads, b.kvHeads, b.dq, b.dv, mask, HW, g.batch, att, aC, s);
+      ConvEpilogue<T> e2 = epi();
+      e2.residual = Rd;
+      e2.ldRes = C;
+      e2.maskResidualAdd = 1;
+      e2.outRaw = Rd;
+      e2.ldRaw = C;
+      e2.rawEnd = C;
+      setAct(e2, next, Ad, C);
+      conv(b.proj, att, aC, e2);
+    }
+    else if(b.kind == BK_FFN) {
+      // trunk += linear2(silu(linear1(x)) * gate(x)) * mask, x = rmsnorm(trunk)
+      const int F = b.ffnC;
+      T* xn = tmp1;
+      T* hid = tmp2;
+      kgh::launchRmsNorm<T>(Rd, C, xn, C, C, b.normW, nullptr, b.normEps, KGH_ACT_IDENTITY, mask, M, s);
+      ConvEpilogue<T> e1 = epi();
+      e1.outAct = hid;
+      e1.ldAct = F;
+      e1.actBegin = 0;
+      e1.actKind = KGH_ACT_SILU;
+      e1.glu = 1;
+      conv(b.qkv, xn, C, e1);
+      ConvEpilogue<T> e2 = epi();
+      e2.residual = Rd;
+      e2.ldRes = C;
+      e2.maskResidualAdd = 1;
+      e2.outRaw = Rd;
+      e2.ldRaw = C;
+      e2.rawEnd = C;
+      setAct(e2, next, Ad, C);
+      conv(b.proj, hid, F, e2);
+    }
     else {
       throw KghError(KGH_ERR_INTERNAL, "unknown block kind");
     }
@@ -612,7 +779,16 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
     Runner<T>::setAct(e, first, r.A[0], net.trunkC);
     r.conv(net.initialConv, (const T*)h->x0, net.inputCPad, e);
   }
-  r.runStack(net.blocks, 0, &net.tipBN);
+  r.runStack(net.blocks, 0, net.tipKind == 0 ? &net.tipBN : nullptr);
+  if(net.tipKind != 0) {
+    // Trunk-tip RMSNorm + activation into A[0], the heads' input.
+    if(net.tipSpatial)
+      kgh::launchRmsNormSpatial<T>(r.R[0], net.trunkC, r.A[0], net.trunkC, net.trunkC, net.tipGamma, net.tipBeta, net.tipEps, net.tipAct,
+                                   h->mask, n, HW, h->nbias, s);
+    else
+      kgh::launchRmsNorm<T>(r.R[0], net.trunkC, r.A[0], net.trunkC, net.trunkC, net.tipGamma, net.tipBeta, net.tipEps, net.tipAct,
+                            h->mask, n * HW, s);
+  }
 
   // Heads: 1x1 convs p1 | g1 | v1 from the activated trunk tip.
   T* p1 = (T*)h->p1;
@@ -727,7 +903,6 @@ void buildNet(kgh_model* m, const kgh_model_desc* d, hipStream_t stream) {
   int numBlocks = t.i[0];
   net.trunkC = t.i[1];
   net.tipKind = t.i[2];
-  if(net.tipKind != 0) unsupported("RMSNorm trunk tips are not supported by this build of the device library");
   net.initialConv = b.conv("initialConv", true);
   net.inputCPad = net.initialConv.cinPad;
   if(net.initialConv.cin != net.inputC || net.initialConv.cout != net.trunkC) invalid("initialConv channel mismatch");
@@ -735,8 +910,21 @@ void buildNet(kgh_model* m, const kgh_model_desc* d, hipStream_t stream) {
   if(net.initialMatMul.cin != net.globalC || net.initialMatMul.cout != net.trunkC) invalid("initialMatMul channel mismatch");
   net.depthC.assign(1, net.trunkC);
   for(int i = 0; i < numBlocks; i++) net.blocks.push_back(b.block(net, 0, net.trunkC));
-  net.tipBN = b.bnAct("trunk tip");
-  if(net.tipBN.C != net.trunkC) invalid("trunk tip channel mismatch");
+  if(net.tipKind == 0) {
+    net.tipBN = b.bnAct("trunk tip");
+    if(net.tipBN.C != net.trunkC) invalid("trunk tip channel mismatch");
+  }
+  else {
+    const kgh_layer& r = b.take(KGH_OP_RMSNORM, "trunk tip RMSNorm");
+    if(r.i[0] != net.trunkC) invalid("trunk tip channel mismatch");
+    net.tipSpatial = r.i[1] != 0;
+    net.tipEps = r.f[0];
+    net.tipGamma = b.dev(r, 0, net.trunkC, "trunk tip gamma");
+    net.tipBeta = b.dev(r, 1, net.trunkC, "trunk tip beta");
+    net.tipAct = b.act("trunk tip activation");
+    if(net.tipAct != KGH_ACT_IDENTITY && net.tipAct != KGH_ACT_SILU && net.tipAct != KGH_ACT_RELU && net.tipAct != KGH_ACT_MISH)
+      invalid("trunk tip: unknown activation");
+  }
 
   // Policy head
   const kgh_layer& ph = b.take(KGH_OP_POLICY_HEAD, "policy head");
@@ -940,6 +1128,39 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     h->score = a.allocN<float>((size_t)max_batch * net.scoreC);
     h->policyRaw = a.allocN<float>(M * net.policyC);
     h->ownRaw = a.allocN<float>(M);
+    // Rotary tables per attention block, [table][pair][y * nn_x + x]: the
+    // angle formulas of TransformerAttentionDesc::computeRopeCosSin
+    // (desc.cpp:1212-1275).
+    for(const RopeSpec& rs : net.ropes) {
+      const int pairs = rs.dq / 2;
+      const int tables = rs.learnable ? rs.kvHeads : 1;
+      const int HW = nn_x * nn_y;
+      std::vector<float> cs((size_t)tables * pairs * HW), sn(cs.size());
+      for(int tb = 0; tb < tables; tb++)
+        for(int p = 0; p < pairs; p++)
+          for(int y = 0; y < nn_y; y++)
+            for(int x = 0; x < nn_x; x++) {
+              float angle;
+              if(rs.learnable) {
+                angle = (float)x * rs.freqs[((size_t)tb * pairs + p) * 2 + 0] + (float)y * rs.freqs[((size_t)tb * pairs + p) * 2 + 1];
+              }
+              else {
+                const int halfPairs = pairs / 2;
+                const int q = p < halfPairs ? p : p - halfPairs;
+                const float freq = 1.0f / powf(rs.theta, (float)(2 * q) / (float)(rs.dq / 2));
+                angle = (float)(p < halfPairs ? y : x) * freq;
+              }
+              const size_t idx = ((size_t)tb * pairs + p) * HW + (size_t)y * nn_x + x;
+              cs[idx] = cosf(angle);
+              sn[idx] = sinf(angle);
+            }
+      float* dc = a.allocN<float>(cs.size());
+      float* ds = a.allocN<float>(sn.size());
+      KGH_HIP_CHECK(hipMemcpy(dc, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
+      KGH_HIP_CHECK(hipMemcpy(ds, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
+      h->ropeCos.push_back(dc);
+      h->ropeSin.push_back(ds);
+    }
     h->rowFloats = kgh_output_row_floats(nn_x, nn_y, net.scoreC);
     h->dSpatial = a.allocN<float>(M * net.inputC);
     h->dGlobal = a.allocN<float>((size_t)max_batch * net.globalC);

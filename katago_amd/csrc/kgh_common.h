@@ -91,10 +91,14 @@ template<typename T> __device__ __forceinline__ T kgh_from_float(float v) { retu
 //   if residual:  v = residual[m*ldRes + c] + (maskResidualAdd ? v*mask[m] : v)
 //   if c <  rawEnd:   outRaw[m*ldRaw + c]             = v
 //   if c >= actBegin: outAct[m*ldAct + c - actBegin]  = act(v*actScale[c-actBegin] + actBias[c-actBegin]) * mask[m]
+// With glu set, the columns from actBegin instead hold gated pairs in blocks
+// of 16 (8 "value" columns, then their 8 gates): for a block starting at c,
+//   outAct[m*ldAct + (c - actBegin)/2 + j] = act(v[c+j]) * v[c+8+j],  j < 8,
+// the SwiGLU of a transformer FFN (act = SiLU, no scale or bias).
 // This expresses every fusion point of the KataGo blocks: next-layer folded
 // BN + activation + mask, residual accumulation, the per-(n,c) bias of the
-// global-input matmul, and the raw/activated split of a combined
-// regular+gpool convolution.
+// global-input matmul, the raw/activated split of a combined regular+gpool
+// convolution, and the gated linear unit.
 template<typename T>
 struct ConvEpilogue {
   T* outRaw;
@@ -112,6 +116,7 @@ struct ConvEpilogue {
   int maskResidualAdd;
   const float* ncBias;
   int ldNC;
+  int glu;
 };
 
 template<typename T>

@@ -98,7 +98,7 @@ __device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM /
     const bool rawCols = c0 < epi.rawEnd;                // the split points are multiples of 16
     const bool actCols = epi.outAct != nullptr && c0 >= epi.actBegin;
     float aS[16], aB[16];
-    if(actCols) {
+    if(actCols && !epi.glu) {
 #pragma unroll
       for(int j = 0; j < 16; j++) {
         aS[j] = epi.actScale[c0 - epi.actBegin + j];
@@ -145,7 +145,15 @@ __device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM /
 #pragma unroll
           for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
         }
-        if(actCols) {
+        if(actCols && epi.glu) {
+          T o[8];
+#pragma unroll
+          for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], epi.actKind) * v[8 + j]);
+          uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin) / 2);
+#pragma unroll
+          for(int q = 0; q < 8 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+        }
+        else if(actCols) {
           T o[16];
 #pragma unroll
           for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk);
@@ -458,7 +466,7 @@ __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float
     const bool rawCols = c0 < epi.rawEnd;        // the split points are multiples of 16
     const bool actCols = epi.outAct != nullptr && c0 >= epi.actBegin;
     float aS[16], aB[16];
-    if(actCols) {
+    if(actCols && !epi.glu) {
 #pragma unroll
       for(int j = 0; j < 16; j++) {
         aS[j] = epi.actScale[c0 - epi.actBegin + j];
@@ -507,7 +515,15 @@ __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float
 #pragma unroll
           for(int q = 0; q < RV; q++) dst[q] = ((const uint4*)o)[q];
         }
-        if(actCols) {
+        if(actCols && epi.glu) {
+          T o[8];
+#pragma unroll
+          for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], epi.actKind) * v[8 + j]);
+          uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin) / 2);
+#pragma unroll
+          for(int q = 0; q < RV / 2; q++) dst[q] = ((const uint4*)o)[q];
+        }
+        else if(actCols) {
           T o[16];
 #pragma unroll
           for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk[rb]);
@@ -1077,6 +1093,7 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
   }
   if(usedMfma != nullptr) *usedMfma = done;
   if(done) return;
+  if(epi.glu) throw KghError(3, "conv: the gated (SwiGLU) epilogue needs the matrix-core kernels (channel counts multiples of 32)");
   if(wDirect == nullptr) throw KghError(5, "conv: no direct-layout weights for a shape the matrix-core kernel does not take");
   long total = (long)g.batch * g.H * g.W * cout;
   int threads = 256;

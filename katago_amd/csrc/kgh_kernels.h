@@ -86,6 +86,24 @@ void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream);
 
 void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream);
 
+// Transformer trunk (kgh_transformer.hip).
+// Per-row RMSNorm: y = act(x * rsqrt(mean(x^2) + eps) * gamma + beta) * (mask != 0); beta may be null.
+template<typename T>
+void launchRmsNorm(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
+                   const float* mask, int M, hipStream_t stream);
+// Per-board (spatial) RMSNorm over masked positions and channels; invScratch holds batch floats.
+template<typename T>
+void launchRmsNormSpatial(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
+                          const float* mask, int batch, int HW, float* invScratch, hipStream_t stream);
+// Rotary embedding in place on the first (H + KV) * dq channels of each QKV row.
+template<typename T>
+void launchRope(T* qkv, int ld, int H, int KV, int dq, const float* cosT, const float* sinT, bool learnable, int HW, int M,
+                hipStream_t stream);
+// Masked softmax attention per board and head; out has H * dv channels per row.
+template<typename T>
+void launchAttention(const T* qkv, int ld, int kOff, int vOff, int H, int KV, int dq, int dv, const float* mask, int HW, int batch,
+                     T* out, int ldOut, hipStream_t stream);
+
 int runMfmaSelfTest();
 
 }  // namespace kgh

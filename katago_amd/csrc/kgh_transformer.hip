@@ -1,0 +1,434 @@
+// Transformer-trunk kernels for gfx950: RMSNorm (block and trunk tip),
+// rotary position embedding, and attention over the board's positions.
+//
+// Semantics follow the reference's Eigen backend:
+//   - TransformerRMSNormLayer (eigenbackend.cpp:867-918): per position
+//     y = x * rsqrt(mean_c(x^2) + eps) * w, zero where mask == 0;
+//   - RMSNormLayer trunk tip (eigenbackend.cpp:923-1022): the same per
+//     position, or with the mean taken over all masked positions and
+//     channels of a board (spatial), then y = y * gamma + beta, then the
+//     tip activation, zero where mask == 0;
+//   - rotary embedding (eigenbackend.cpp:1418-1456, tables desc.cpp:1212-1275):
+//     pairs (2p, 2p+1) of each head rotate by the table angle of the position;
+//   - attention (eigenbackend.cpp:1459-1557): softmax over unmasked keys of
+//     q.k / sqrt(dq), rows of masked queries are zero; query head h reads
+//     kv head h / (H / KV).
+#include "kgh_common.h"
+#include "kgh_kernels.h"
+
+#include <climits>
+
+namespace {
+
+__device__ __forceinline__ float waveSum(float v) {
+#pragma unroll
+  for(int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// One wave per row; each lane moves 16-byte groups of channels.
+template<typename T>
+__global__ void rmsNormRowKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ gamma,
+                                 const float* __restrict__ beta, float eps, int act, const float* __restrict__ mask, int M) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if(row >= M) return;
+  const T* xr = x + (size_t)row * ldX;
+  T* yr = y + (size_t)row * ldY;
+  const bool on = mask[row] != 0.0f;
+  float ss = 0.0f;
+  for(int c = lane * VEC; c < C; c += 64 * VEC) {
+    T v[VEC];
+    *(uint4*)v = *(const uint4*)(xr + c);
+#pragma unroll
+    for(int j = 0; j < VEC; j++) {
+      float f = kgh_to_float(v[j]);
+      ss += f * f;
+    }
+  }
+  ss = waveSum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+  for(int c = lane * VEC; c < C; c += 64 * VEC) {
+    T v[VEC], o[VEC];
+    *(uint4*)v = *(const uint4*)(xr + c);
+#pragma unroll
+    for(int j = 0; j < VEC; j++) {
+      float f = kgh_to_float(v[j]) * inv * gamma[c + j];
+      if(beta != nullptr) f += beta[c + j];
+      f = kgh_activate(f, act);
+      o[j] = kgh_from_float<T>(on ? f : 0.0f);
+    }
+    *(uint4*)(yr + c) = *(const uint4*)o;
+  }
+}
+
+// Spatial RMSNorm, pass 1: per board, 1 / sqrt(sum over masked positions and
+// channels of x^2 / (count * C) + eps).
+template<typename T>
+__global__ void rmsNormBoardKernel(const T* __restrict__ x, int ldX, int C, float eps, const float* __restrict__ mask, int HW,
+                                   float* __restrict__ invOut) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  __shared__ float part[16];
+  __shared__ float cnt[16];
+  const int n = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int waves = blockDim.x >> 6;
+  float ss = 0.0f, count = 0.0f;
+  for(int p = wave; p < HW; p += waves) {
+    const size_t row = (size_t)n * HW + p;
+    if(mask[row] == 0.0f) continue;
+    if(lane == 0) count += 1.0f;
+    const T* xr = x + row * ldX;
+    for(int c = lane * VEC; c < C; c += 64 * VEC) {
+      T v[VEC];
+      *(uint4*)v = *(const uint4*)(xr + c);
+#pragma unroll
+      for(int j = 0; j < VEC; j++) {
+        float f = kgh_to_float(v[j]);
+        ss += f * f;
+      }
+    }
+  }
+  ss = waveSum(ss);
+  count = waveSum(count);
+  if(lane == 0) {
+    part[wave] = ss;
+    cnt[wave] = count;
+  }
+  __syncthreads();
+  if(threadIdx.x == 0) {
+    float s = 0.0f, k = 0.0f;
+    for(int i = 0; i < waves; i++) {
+      s += part[i];
+      k += cnt[i];
+    }
+    invOut[n] = 1.0f / sqrtf(s / (k * (float)C) + eps);
+  }
+}
+
+// Spatial RMSNorm, pass 2: y = act(x * inv[board] * gamma + beta) * (mask != 0).
+template<typename T>
+__global__ void rmsNormApplyKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ gamma,
+                                   const float* __restrict__ beta, int act, const float* __restrict__ mask, int HW, int M,
+                                   const float* __restrict__ inv) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int groups = C / VEC;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= (long)M * groups) return;
+  const int row = (int)(idx / groups);
+  const int c = (int)(idx - (long)row * groups) * VEC;
+  const bool on = mask[row] != 0.0f;
+  const float s = inv[row / HW];
+  T v[VEC], o[VEC];
+  *(uint4*)v = *(const uint4*)(x + (size_t)row * ldX + c);
+#pragma unroll
+  for(int j = 0; j < VEC; j++) {
+    float f = kgh_activate(kgh_to_float(v[j]) * s * gamma[c + j] + beta[c + j], act);
+    o[j] = kgh_from_float<T>(on ? f : 0.0f);
+  }
+  *(uint4*)(y + (size_t)row * ldY + c) = *(const uint4*)o;
+}
+
+// Rotary embedding in place on the Q and K parts of a QKV row: one thread
+// per (row, head, pair). Tables are [table][pair][HW] with table = the kv
+// head for learnable tables, else 0.
+template<typename T>
+__global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, const float* __restrict__ cosT,
+                           const float* __restrict__ sinT, int learnable, int HW, int M) {
+  const int pairs = dq / 2;
+  const int perRow = (H + KV) * pairs;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= (long)M * perRow) return;
+  const int row = (int)(idx / perRow);
+  int rest = (int)(idx - (long)row * perRow);
+  const int head = rest / pairs;  // 0..H-1 query heads, then H..H+KV-1 key heads
+  const int p = rest - head * pairs;
+  int table = 0;
+  if(learnable) table = head < H ? head * KV / H : head - H;
+  const int xy = row % HW;
+  const float cs = cosT[((size_t)table * pairs + p) * HW + xy];
+  const float sn = sinT[((size_t)table * pairs + p) * HW + xy];
+  T* e = qkv + (size_t)row * ld + head * dq + 2 * p;
+  const float x0 = kgh_to_float(e[0]), x1 = kgh_to_float(e[1]);
+  e[0] = kgh_from_float<T>(x0 * cs - x1 * sn);
+  e[1] = kgh_from_float<T>(x0 * sn + x1 * cs);
+}
+
+// ---------------------------------------------------------------------------
+// Attention with matrix cores (fp16). One workgroup of 12 wave64s per
+// (board, query head); K (row-major, rows padded by 16 bytes) and V
+// (transposed, [dim][key], rows padded by 8 bytes) of the board's kv head are
+// staged in LDS once, so each wave then streams the keys from LDS with no
+// further barrier. Wave w owns queries 32w .. 32w+31 and, per block of 32
+// keys, computes S^T = K Q^T (lane = query, 16 keys per lane), an online
+// softmax per lane, and O^T += V^T P^T with P taken straight from the
+// accumulator registers: the key order inside the second product's k slots
+// is the accumulator's row order (lane half kq holds keys kq*4 + {0..3, 8..11}
+// of each 16-key step), and V^T is read in that same order.
+constexpr int FA_THREADS = 768;
+constexpr int FA_MAX_KEYS = 384;
+
+template<int DQ, int DV>
+__global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half_t* __restrict__ qkv, int ld, int kOff, int vOff, int H,
+                                                                     int KV, const float* __restrict__ mask, int HW,
+                                                                     half_t* __restrict__ out, int ldOut, float scale) {
+  static_assert(DQ % 16 == 0 && DV % 16 == 0 && DQ <= 64 && DV <= 64, "head dims (LDS holds all keys)");
+  constexpr int DVP = (DV + 31) / 32 * 32;
+  constexpr int KLD = DQ + 8;             // halves per K row (16-byte pad)
+  constexpr int VLD = FA_MAX_KEYS + 4;    // halves per V^T row (8-byte pad)
+  __shared__ __attribute__((aligned(16))) half_t Ks[FA_MAX_KEYS * KLD];
+  __shared__ __attribute__((aligned(16))) half_t Vt[DVP * VLD];
+  __shared__ float keyOk[FA_MAX_KEYS];
+
+  const int n = blockIdx.x / H;
+  const int h = blockIdx.x - n * H;
+  const int kvh = h / (H / KV);
+  const int tid = threadIdx.x;
+  const size_t rowBase = (size_t)n * HW;
+
+  // Stage K rows (16-byte groups), V^T (8 dims of one key per thread) and the
+  // key mask; keys past HW and dims past DV are zero.
+  for(int i = tid; i < FA_MAX_KEYS * (DQ / 8); i += FA_THREADS) {
+    const int key = i / (DQ / 8);
+    const int g = i - key * (DQ / 8);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if(key < HW) v = *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8);
+    *(uint4*)&Ks[key * KLD + g * 8] = v;
+  }
+  for(int i = tid; i < FA_MAX_KEYS * (DVP / 8); i += FA_THREADS) {
+    const int key = i / (DVP / 8);
+    const int g = i - key * (DVP / 8);
+    half_t v[8];
+    *(uint4*)v = make_uint4(0, 0, 0, 0);
+    if(key < HW && g * 8 < DV) *(uint4*)v = *(const uint4*)(qkv + (rowBase + key) * ld + vOff + kvh * DV + g * 8);
+#pragma unroll
+    for(int j = 0; j < 8; j++) Vt[(g * 8 + j) * VLD + key] = v[j];
+  }
+  for(int i = tid; i < FA_MAX_KEYS; i += FA_THREADS) keyOk[i] = (i < HW && mask[rowBase + i] != 0.0f) ? 1.0f : 0.0f;
+  __syncthreads();
+
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int q0 = wave * 32;
+  if(q0 >= HW) return;  // no barrier follows
+  const int laneRow = lane & 31;
+  const int kq = lane >> 5;
+  const int qi = q0 + laneRow;
+  const int qRow = qi < HW ? qi : HW - 1;
+
+  half8_t qf[DQ / 16];
+#pragma unroll
+  for(int ks = 0; ks < DQ / 16; ks++) qf[ks] = *(const half8_t*)(qkv + (rowBase + qRow) * ld + h * DQ + ks * 16 + kq * 8);
+
+  floatx16 o[DVP / 32];
+#pragma unroll
+  for(int db = 0; db < DVP / 32; db++)
+#pragma unroll
+    for(int r = 0; r < 16; r++) o[db][r] = 0.0f;
+  float mRun = -INFINITY, lRun = 0.0f;
+
+  const int keyTiles = (HW + 31) / 32;
+  for(int kt = 0; kt < keyTiles; kt++) {
+    const int kb = kt * 32;
+    floatx16 s;
+#pragma unroll
+    for(int r = 0; r < 16; r++) s[r] = 0.0f;
+#pragma unroll
+    for(int ks = 0; ks < DQ / 16; ks++) {
+      const half8_t a = *(const half8_t*)&Ks[(kb + laneRow) * KLD + ks * 16 + kq * 8];
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s, 0, 0, 0);
+    }
+    float mTile = -INFINITY;
+#pragma unroll
+    for(int r = 0; r < 16; r++) {
+      const int key = kb + (r >> 2) * 8 + kq * 4 + (r & 3);
+      const float v = keyOk[key] != 0.0f ? s[r] * scale : -INFINITY;
+      s[r] = v;
+      mTile = fmaxf(mTile, v);
+    }
+    mTile = fmaxf(mTile, __shfl_xor(mTile, 32));
+    // Every lane runs every matrix instruction (no divergence around them):
+    // while a query has seen no valid key, mNew is -inf and the reference
+    // point 0 makes corr and every p exactly 0.
+    const float mNew = fmaxf(mRun, mTile);
+    const float mRef = mNew == -INFINITY ? 0.0f : mNew;
+    const float corr = __expf(mRun - mRef);
+    float psum = 0.0f;
+#pragma unroll
+    for(int r = 0; r < 16; r++) {
+      const float p = __expf(s[r] - mRef);
+      s[r] = p;
+      psum += p;
+    }
+    psum += __shfl_xor(psum, 32);
+    lRun = lRun * corr + psum;
+    mRun = mNew;
+#pragma unroll
+    for(int db = 0; db < DVP / 32; db++)
+#pragma unroll
+      for(int r = 0; r < 16; r++) o[db][r] *= corr;
+#pragma unroll
+    for(int j = 0; j < 2; j++) {
+      half8_t b;
+#pragma unroll
+      for(int r = 0; r < 8; r++) b[r] = (half_t)s[8 * j + r];
+      const int k0 = kb + 16 * j + kq * 4;
+#pragma unroll
+      for(int db = 0; db < DVP / 32; db++) {
+        const half_t* vr = &Vt[(db * 32 + laneRow) * VLD + k0];
+        half4_t lo = *(const half4_t*)vr;
+        half4_t hi = *(const half4_t*)(vr + 8);
+        half8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[db], 0, 0, 0);
+      }
+    }
+  }
+
+  if(qi >= HW) return;
+  const size_t row = rowBase + qi;
+  const bool on = mask[row] != 0.0f && lRun > 0.0f;
+  const float invL = on ? 1.0f / lRun : 0.0f;
+  half_t* dst = out + row * ldOut + h * DV;
+#pragma unroll
+  for(int db = 0; db < DVP / 32; db++)
+#pragma unroll
+    for(int g = 0; g < 4; g++) {
+      const int d = db * 32 + g * 8 + kq * 4;
+      if(d < DV) {
+        half4_t v;
+#pragma unroll
+        for(int j = 0; j < 4; j++) v[j] = (half_t)(o[db][4 * g + j] * invL);
+        *(half4_t*)(dst + d) = v;
+      }
+    }
+}
+
+// Attention without matrix cores, for fp32 contexts and head shapes the
+// kernel above does not take: one thread per (board, head, query), two
+// passes over the keys as in the reference.
+template<typename T>
+__global__ void attentionSimpleKernel(const T* __restrict__ qkv, int ld, int kOff, int vOff, int H, int KV, int dq, int dv,
+                                      const float* __restrict__ mask, int HW, int batch, T* __restrict__ out, int ldOut, float scale) {
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= (long)batch * H * HW) return;
+  const int qi = (int)(idx % HW);
+  const int h = (int)((idx / HW) % H);
+  const int n = (int)(idx / ((long)HW * H));
+  const int kvh = h / (H / KV);
+  const size_t rowBase = (size_t)n * HW;
+  T* dst = out + (rowBase + qi) * ldOut + h * dv;
+  if(mask[rowBase + qi] == 0.0f) {
+    for(int e = 0; e < dv; e++) dst[e] = kgh_from_float<T>(0.0f);
+    return;
+  }
+  const T* q = qkv + (rowBase + qi) * ld + h * dq;
+  float mx = -INFINITY;
+  for(int k = 0; k < HW; k++) {
+    if(mask[rowBase + k] == 0.0f) continue;
+    const T* kr = qkv + (rowBase + k) * ld + kOff + kvh * dq;
+    float s = 0.0f;
+    for(int e = 0; e < dq; e++) s += kgh_to_float(q[e]) * kgh_to_float(kr[e]);
+    mx = fmaxf(mx, s * scale);
+  }
+  float acc[128];
+  for(int e = 0; e < dv; e++) acc[e] = 0.0f;
+  float sum = 0.0f;
+  for(int k = 0; k < HW; k++) {
+    if(mask[rowBase + k] == 0.0f) continue;
+    const T* kr = qkv + (rowBase + k) * ld + kOff + kvh * dq;
+    float s = 0.0f;
+    for(int e = 0; e < dq; e++) s += kgh_to_float(q[e]) * kgh_to_float(kr[e]);
+    const float p = expf(s * scale - mx);
+    sum += p;
+    const T* vr = qkv + (rowBase + k) * ld + vOff + kvh * dv;
+    for(int e = 0; e < dv; e++) acc[e] += p * kgh_to_float(vr[e]);
+  }
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  for(int e = 0; e < dv; e++) dst[e] = kgh_from_float<T>(acc[e] * inv);
+}
+
+template<int DQ, int DV>
+bool launchFlash(const half_t* qkv, int ld, int kOff, int vOff, int H, int KV, const float* mask, int HW, int batch, half_t* out,
+                 int ldOut, float scale, hipStream_t stream) {
+  hipLaunchKernelGGL((flashAttentionKernel<DQ, DV>), dim3(batch * H), dim3(FA_THREADS), 0, stream, qkv, ld, kOff, vOff, H, KV, mask, HW,
+                     out, ldOut, scale);
+  KGH_CHECK_LAUNCH();
+  return true;
+}
+
+}  // namespace
+
+namespace kgh {
+
+template<typename T>
+void launchRmsNorm(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
+                   const float* mask, int M, hipStream_t stream) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  if(C % VEC != 0 || ldX % VEC != 0 || ldY % VEC != 0) throw KghError(3, "RMSNorm: channel counts must be multiples of 16 bytes");
+  const int wavesPerBlock = 4;
+  hipLaunchKernelGGL(rmsNormRowKernel<T>, dim3((M + wavesPerBlock - 1) / wavesPerBlock), dim3(64 * wavesPerBlock), 0, stream, x, ldX,
+                     y, ldY, C, gamma, beta, eps, act, mask, M);
+  KGH_CHECK_LAUNCH();
+}
+
+template<typename T>
+void launchRmsNormSpatial(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
+                          const float* mask, int batch, int HW, float* invScratch, hipStream_t stream) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  if(C % VEC != 0 || ldX % VEC != 0 || ldY % VEC != 0) throw KghError(3, "RMSNorm: channel counts must be multiples of 16 bytes");
+  hipLaunchKernelGGL(rmsNormBoardKernel<T>, dim3(batch), dim3(512), 0, stream, x, ldX, C, eps, mask, HW, invScratch);
+  KGH_CHECK_LAUNCH();
+  const long total = (long)batch * HW * (C / VEC);
+  hipLaunchKernelGGL(rmsNormApplyKernel<T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, x, ldX, y, ldY, C, gamma, beta,
+                     act, mask, HW, batch * HW, invScratch);
+  KGH_CHECK_LAUNCH();
+}
+
+template<typename T>
+void launchRope(T* qkv, int ld, int H, int KV, int dq, const float* cosT, const float* sinT, bool learnable, int HW, int M,
+                hipStream_t stream) {
+  const long total = (long)M * (H + KV) * (dq / 2);
+  hipLaunchKernelGGL(ropeKernel<T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, qkv, ld, H, KV, dq, cosT, sinT,
+                     learnable ? 1 : 0, HW, M);
+  KGH_CHECK_LAUNCH();
+}
+
+template<typename T>
+void launchAttention(const T* qkv, int ld, int kOff, int vOff, int H, int KV, int dq, int dv, const float* mask, int HW, int batch,
+                     T* out, int ldOut, hipStream_t stream) {
+  if(H % KV != 0) throw KghError(1, "attention: numHeads must be a multiple of numKVHeads");
+  if(dv > 128) throw KghError(3, "attention: value head dims above 128 are not supported");
+  const float scale = 1.0f / sqrtf((float)dq);
+  bool done = false;
+  if constexpr(sizeof(T) == 2) {
+    const bool aligned = ld % 8 == 0 && kOff % 8 == 0 && vOff % 8 == 0 && ldOut % 4 == 0 && HW <= FA_MAX_KEYS;
+    if(aligned) {
+      if(dq == 64 && dv == 64) done = launchFlash<64, 64>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, stream);
+      else if(dq == 32 && dv == 32) done = launchFlash<32, 32>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, stream);
+      else if(dq == 32 && dv == 16) done = launchFlash<32, 16>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, stream);
+    }
+  }
+  if(done) return;
+  const long total = (long)batch * H * HW;
+  hipLaunchKernelGGL(attentionSimpleKernel<T>, dim3((unsigned)((total + 127) / 128)), dim3(128), 0, stream, qkv, ld, kOff, vOff, H, KV,
+                     dq, dv, mask, HW, batch, out, ldOut, scale);
+  KGH_CHECK_LAUNCH();
+}
+
+template void launchRmsNorm<half_t>(const half_t*, int, half_t*, int, int, const float*, const float*, float, int, const float*, int,
+                                    hipStream_t);
+template void launchRmsNorm<float>(const float*, int, float*, int, int, const float*, const float*, float, int, const float*, int,
+                                   hipStream_t);
+template void launchRmsNormSpatial<half_t>(const half_t*, int, half_t*, int, int, const float*, const float*, float, int, const float*,
+                                           int, int, float*, hipStream_t);
+template void launchRmsNormSpatial<float>(const float*, int, float*, int, int, const float*, const float*, float, int, const float*, int,
+                                          int, float*, hipStream_t);
+template void launchRope<half_t>(half_t*, int, int, int, int, const float*, const float*, bool, int, int, hipStream_t);
+template void launchRope<float>(float*, int, int, int, int, const float*, const float*, bool, int, int, hipStream_t);
+template void launchAttention<half_t>(const half_t*, int, int, int, int, int, int, int, const float*, int, int, half_t*, int,
+                                      hipStream_t);
+template void launchAttention<float>(const float*, int, int, int, int, int, int, int, const float*, int, int, float*, int, hipStream_t);
+
+}  // namespace kgh

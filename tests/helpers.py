@@ -8,6 +8,15 @@ import numpy as np
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 G170_MODEL = os.path.join(GOLDEN, "g170-b6c96-s175395328-d26788732.bin.gz")
+# The reference's in-repo transformer test nets (cpp/tests/models, listed in
+# rungpuerrortest.sh:31-33): fixed RoPE + per-position RMSNorm tip; GQA with
+# dq=32, dv=16, learnable RoPE, BN tip; transformer blocks nested in
+# bottleneck blocks, learnable RoPE, spatial RMSNorm tip with SiLU.
+TRANSFORMER_MODELS = [os.path.join(GOLDEN, f + ".bin.gz") for f in (
+    "b7c96h3tfrs-test5-cnorm",
+    "b7c96h6kv3qk32v16tflrs-fson-bnh",
+    "b4c256h4nbttflrs-fson-silu-rsnh",
+)]
 
 
 def load_kats():

@@ -9,7 +9,9 @@ identical argmax over on-board points and pass, value and score <= 1e-3
 import numpy as np
 import pytest
 
-from helpers import G170_MODEL, approx_equal_kat, load_kats, nchw_to_nhwc
+import os
+
+from helpers import G170_MODEL, TRANSFORMER_MODELS, approx_equal_kat, load_kats, nchw_to_nhwc
 from katago_amd import modelgen, nn
 from oracle import oracle
 
@@ -173,17 +175,74 @@ def test_trained_g170_b6c96_fp16_within_reference_fp16_error_bounds():
     sym = np.arange(n)
     gpu = h.get_output(sp, gl, sym)
     ora = om.forward(sp, gl, sym)
-    s = lm.info.output_scale_multiplier
+    _fp16_reference_bounds(gpu, ora, lm.info.output_scale_multiplier, "g170")
+
+
+def _fp16_reference_bounds(gpu, ora, s, label):
+    """The reference's fp16 acceptance bounds of testgpuerror
+    (testnnevalcanary.cpp:742-749, max over positions): winrate error <= 5%,
+    policy KL <= 4e-3; plus logits within 2e-2 + 3e-3*|logit| and the same
+    top move, ownership within 2e-2 + 3e-3*max|ownership|."""
     gp, op = gpu["policy"] * s, ora["policy"]
-    assert (np.abs(gp - op) <= 2e-2 + 3e-3 * np.abs(op)).all(), np.abs(gp - op).max()
-    assert (gp.argmax(axis=1) == op.argmax(axis=1)).all()
+    assert (np.abs(gp - op) <= 2e-2 + 3e-3 * np.abs(op)).all(), (label, np.abs(gp - op).max())
+    assert (gp.argmax(axis=1) == op.argmax(axis=1)).all(), label
     pg, po = _softmax(gp.astype(np.float64)), _softmax(op.astype(np.float64))
     kl = (po * (np.log(po) - np.log(pg))).sum(axis=1)
-    assert kl.max() <= 4e-3, kl.max()
+    assert kl.max() <= 4e-3, (label, kl.max())
     wg = _softmax(gpu["value"].astype(np.float64) * s)[:, 0]
     wo = _softmax(ora["value"].astype(np.float64))[:, 0]
-    assert np.abs(wg - wo).max() <= 0.05
-    assert np.abs(gpu["ownership"] * s - ora["ownership"]).max() <= 2e-2 + 3e-3 * np.abs(ora["ownership"]).max()
+    assert np.abs(wg - wo).max() <= 0.05, label
+    assert np.abs(gpu["ownership"] * s - ora["ownership"]).max() <= 2e-2 + 3e-3 * np.abs(ora["ownership"]).max(), label
+
+
+def _ref_id(path):
+    return os.path.basename(path).split("-")[0]
+
+
+@pytest.mark.parametrize("path", TRANSFORMER_MODELS, ids=_ref_id)
+def test_reference_transformer_nets_fp32_match_oracle(path):
+    """Attention (matrix-core-free kernel in fp32), SwiGLU FFN, RMSNorm block
+    and tip norms, GQA and both RoPE forms, on mixed board sizes."""
+    _run_parity(path, False, 4, board_sizes=(19, 9, 13), label=_ref_id(path))
+
+
+@pytest.mark.parametrize("path", TRANSFORMER_MODELS, ids=_ref_id)
+def test_reference_transformer_nets_fp16_within_reference_fp16_error_bounds(path):
+    n = 6
+    om = oracle.OracleModel(path)
+    lm = nn.LoadedModel(path)
+    h = nn.ComputeHandle(nn.ComputeContext(lm, 19, 19, use_fp16=True), max_batch=n)
+    sp, gl = modelgen.synthetic_inputs(5, n, board_sizes=(19, 9, 13))
+    sym = np.arange(n) % 8
+    gpu = h.get_output(sp, gl, sym)
+    ora = om.forward(sp, gl, sym)
+    _fp16_reference_bounds(gpu, ora, lm.info.output_scale_multiplier, _ref_id(path))
+
+
+def _tiny_transformer(heads, kv, dq, dv, c, learnable, tip):
+    kinds = ["attention", "ffn", "regular", "attention", "ffn"]
+    return modelgen.Arch(f"tiny-tf-h{heads}kv{kv}q{dq}v{dv}", 17, c, c, 32, kinds, 16, 16, 32, 24, "ACTIVATION_SILU", heads=heads,
+                         kv_heads=kv, q_head_dim=dq, v_head_dim=dv, ffn_c=96, learnable_rope=learnable, trunk_rmsnorm=tip,
+                         transformer_std=0.08, residual_gain=0.5)
+
+
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
+@pytest.mark.parametrize("heads,kv,dq,dv,c,learnable,tip", [
+    (2, 2, 32, 32, 64, False, True),
+    (4, 2, 32, 16, 64, True, True),
+    (2, 1, 64, 64, 128, True, False),
+], ids=["mha-q32v32-fixed", "gqa-q32v16-learnable", "mqa-q64v64-bntip"])
+def test_tiny_transformers_match_oracle(model_dir, heads, kv, dq, dv, c, learnable, tip, fp16):
+    """Head shapes that select each matrix-core attention variant in fp16 (and
+    the plain kernel in fp32)."""
+    arch = _tiny_transformer(heads, kv, dq, dv, c, learnable, tip)
+    path = modelgen.write_model(arch, 31 + heads + dq, f"{model_dir}/{arch.name}-{learnable}-{tip}.bin.gz")
+    _run_parity(path, fp16, 5, board_sizes=(19, 9, 13, 7), label=arch.name)
+
+
+def test_c4_transformer_d384_fp16_matches_oracle(model_dir):
+    cfg = modelgen.configs()[4]
+    _run_parity(modelgen.ensure_model(model_dir, cfg), True, 2, board_sizes=(19, 13), label="C4")
 
 
 def test_all_symmetries_fp32(model_dir):

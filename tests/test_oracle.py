@@ -8,11 +8,12 @@ independence, a small board padded into a 19x19 tensor equals the same board
 evaluated unpadded).
 """
 import math
+import os
 
 import numpy as np
 import pytest
 
-from helpers import G170_MODEL, approx_equal_kat, load_kats, load_symmetry_cases, nchw_to_nhwc
+from helpers import G170_MODEL, TRANSFORMER_MODELS, approx_equal_kat, load_kats, load_symmetry_cases, nchw_to_nhwc
 from katago_amd import modelgen, nn
 from oracle import oracle
 
@@ -112,6 +113,28 @@ def test_oracle_whole_net_nbt_mish_mixed_boards_matches_torch_f64(model_dir):
 
 def test_oracle_whole_net_trained_g170_matches_torch_f64():
     _torch_check(G170_MODEL, rows=2)
+
+
+def _tiny_transformer(learnable_rope=True, kv_heads=2, q_dim=16, v_dim=16, rmsnorm_tip=True):
+    kinds = ["attention", "ffn", "regular", "attention", "ffn"]
+    return modelgen.Arch("tiny-tf", 17, 64, 64, 32, kinds, 16, 16, 32, 24, "ACTIVATION_SILU", heads=4, kv_heads=kv_heads,
+                         q_head_dim=q_dim, v_head_dim=v_dim, ffn_c=96, learnable_rope=learnable_rope, trunk_rmsnorm=rmsnorm_tip,
+                         transformer_std=0.08, residual_gain=0.5)
+
+
+@pytest.mark.parametrize("learnable,kv,tip", [(True, 2, True), (False, 4, True), (True, 1, False)],
+                         ids=["gqa-learnable-rms", "mha-fixed-rms", "mqa-learnable-bn"])
+def test_oracle_whole_net_tiny_transformer_matches_torch_f64(model_dir, learnable, kv, tip):
+    """Attention (torch scaled_dot_product_attention), RMSNorm, SwiGLU and both
+    RoPE forms, mixed with a residual conv block, on mixed board sizes."""
+    arch = _tiny_transformer(learnable_rope=learnable, kv_heads=kv, rmsnorm_tip=tip)
+    path = modelgen.write_model(arch, 21 + kv, f"{model_dir}/tiny-tf-{learnable}-{kv}-{tip}.bin.gz")
+    _torch_check(path, rows=3, board_sizes=(19, 9, 13))
+
+
+@pytest.mark.parametrize("path", TRANSFORMER_MODELS, ids=lambda p: os.path.basename(p).split("-")[0])
+def test_oracle_reference_transformer_nets_match_torch_f64(path):
+    _torch_check(path, rows=2, board_sizes=(19, 11))
 
 
 def test_oracle_batch_independence(model_dir):
