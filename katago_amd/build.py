@@ -12,6 +12,8 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
+import json
 import shutil
 import subprocess
 import sys
@@ -53,11 +55,30 @@ ORACLE_SOURCES = [
 ]
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(l for l in proc.stdout.splitlines() if "packed-fp32-ops" not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    return out
+
+
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|LDS Size \[bytes/block\]|"
+                     r"VGPRs Spill|SGPRs Spill|Occupancy \[waves/SIMD\]):\s*(\S+)")
+_FIELDS = {"VGPRs": "vgpr", "AGPRs": "agpr", "ScratchSize [bytes/lane]": "scratch", "LDS Size [bytes/block]": "lds",
+           "VGPRs Spill": "vgpr_spill", "SGPRs Spill": "sgpr_spill", "Occupancy [waves/SIMD]": "occupancy"}
+
+
+def _resource_usage(compiler_output: str) -> dict:
+    """Per-kernel registers, scratch and LDS from the compiler's
+    kernel-resource-usage remarks."""
+    kernels, cur = {}, None
+    for key, val in _REMARK.findall(compiler_output):
+        if key == "Function Name":
+            cur = kernels.setdefault(val, {})
+        elif cur is not None:
+            cur[_FIELDS[key]] = int(val)
+    return kernels
 
 
 def build_hip(jobs: int = 8) -> str:
@@ -68,9 +89,14 @@ def build_hip(jobs: int = 8) -> str:
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(PKG, "csrc", src), "-o", obj])
+        cmds.append([HIPCC, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", os.path.join(PKG, "csrc", src), "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(_run, cmds))
+        outputs = list(ex.map(_run, cmds))
+    usage = {}
+    for o in outputs:
+        usage.update(_resource_usage(o))
+    with open(os.path.join(LIB_DIR, "kernel_resources.json"), "w") as f:
+        json.dump(usage, f, indent=1, sort_keys=True)
     out = os.path.join(LIB_DIR, "libkatago_hip.so")
     tmp = out + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])

@@ -445,7 +445,7 @@ __device__ __forceinline__ void barrierNoFence() {
 // and only the outputs touch memory here. The stage is private to the wave and a wave's LDS operations execute in order, so no
 // workgroup barrier is needed; the empty asm statements only keep the
 // compiler from reordering the stage accesses.
-template<typename T, int RB, int CB, bool RES_IN_ACC>
+template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU>
 __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
                                                   const ConvEpilogue<T>& epi) {
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -515,13 +515,15 @@ __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float
 #pragma unroll
           for(int q = 0; q < RV; q++) dst[q] = ((const uint4*)o)[q];
         }
-        if(actCols && epi.glu) {
-          T o[8];
+        if constexpr(GLU) {
+          if(actCols) {
+            T o[8];
 #pragma unroll
-          for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], epi.actKind) * v[8 + j]);
-          uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin) / 2);
+            for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], epi.actKind) * v[8 + j]);
+            uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin) / 2);
 #pragma unroll
-          for(int q = 0; q < RV / 2; q++) dst[q] = ((const uint4*)o)[q];
+            for(int q = 0; q < RV / 2; q++) dst[q] = ((const uint4*)o)[q];
+          }
         }
         else if(actCols) {
           T o[16];
@@ -769,7 +771,7 @@ __global__ __launch_bounds__(TW_THREADS, 1) void convTapWindowKernel(const half_
   waitVmcnt<0>();
   __syncthreads();
 
-  storeWaveEpilogue<half_t, RB, CB, true>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, epi);
+  storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -782,7 +784,9 @@ __global__ __launch_bounds__(TW_THREADS, 1) void convTapWindowKernel(const half_
 // shapes the kernel is bound by HBM (A is read once, outputs written once).
 constexpr int G1_A_LOADS = TW_BM / 16;  // 24 wave-loads of A per step
 
-template<int BN>
+// GLU selects the gated epilogue at compile time: the branch alone pushes the
+// accumulators of the non-gated variant out of registers.
+template<int BN, bool GLU>
 __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
                                                                  int cout, const half_t* __restrict__ w, BoardGeom g,
                                                                  ConvEpilogue<half_t> epi) {
@@ -916,7 +920,7 @@ __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* 
 
   ConvEpilogue<half_t> e = epi;
   if(resInAcc) e.residual = nullptr;
-  storeWaveEpilogue<half_t, RB, CB, false>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, e);
+  storeWaveEpilogue<half_t, RB, CB, false, GLU>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, e);
 }
 
 // Direct convolution: one thread per output element. Used for shapes the
@@ -1023,7 +1027,8 @@ void launch1x1Dma(const half_t* x, int cinStride, int cinPad, int cout, const ha
                   const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   int M = g.batch * g.H * g.W;
   dim3 grid((M + TW_BM - 1) / TW_BM, cout / BN);
-  hipLaunchKernelGGL((conv1x1DmaKernel<BN>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  if(epi.glu) hipLaunchKernelGGL((conv1x1DmaKernel<BN, true>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  else hipLaunchKernelGGL((conv1x1DmaKernel<BN, false>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
   KGH_CHECK_LAUNCH();
 }
 

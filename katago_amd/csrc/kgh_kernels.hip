@@ -5,6 +5,7 @@
 #include "kgh_kernels.h"
 
 #include <climits>
+#include <cstdint>
 
 namespace {
 
@@ -85,6 +86,97 @@ __global__ void rowMatmulKernel(const float* __restrict__ in, int ldIn, int cin,
 // where S = maskSum[n] and third is max(-1, max_m(g + mask - 1)) for gpool
 // or mean*((sqrt(S)-14)^2*0.01 - 0.1) for the value head.
 // Then, if Wt != nullptr, out[n, co] = sum_i pooled[n,i] * Wt[i, co].
+// Per-channel masked sum and max (of v + mask - 1, starting from -1: the
+// reference's poolRowsGPool, eigenbackend.cpp:152-177) over the positions of
+// board n, into LDS sums[C] and maxs[C]. Every thread of the block takes
+// part; thread t moves 16-byte channel groups of the positions
+// p = t / CG (mod threads / CG). red holds 2 * blockDim.x * VEC floats.
+// Requires C and ld multiples of the vector width and 16-byte rows.
+template<typename T>
+__device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float* __restrict__ mask, int n, int HW, float* sums,
+                             float* maxs, float* red) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int CG = C / VEC;
+  const int nt = blockDim.x;
+  const int t = threadIdx.x;
+  for(int cg0 = 0; cg0 < CG; cg0 += nt) {
+    const int cgN = min(CG - cg0, nt);
+    const int PG = nt / cgN;
+    const int cgl = t % cgN;
+    const int pg = t / cgN;
+    float sm[VEC], mx[VEC];
+#pragma unroll
+    for(int j = 0; j < VEC; j++) {
+      sm[j] = 0.0f;
+      mx[j] = -1.0f;
+    }
+    if(pg < PG) {
+      const T* base = g + (size_t)n * HW * ld + (cg0 + cgl) * VEC;
+      for(int p = pg; p < HW; p += PG) {
+        T v[VEC];
+        *(uint4*)v = *(const uint4*)(base + (size_t)p * ld);
+        const float mk = mask[(size_t)n * HW + p] - 1.0f;
+#pragma unroll
+        for(int j = 0; j < VEC; j++) {
+          const float f = kgh_to_float(v[j]);
+          sm[j] += f;
+          mx[j] = fmaxf(mx[j], f + mk);
+        }
+      }
+#pragma unroll
+      for(int j = 0; j < VEC; j++) {
+        red[(pg * cgN + cgl) * VEC + j] = sm[j];
+        red[(nt + pg * cgN + cgl) * VEC + j] = mx[j];
+      }
+    }
+    __syncthreads();
+    for(int c = t; c < cgN * VEC; c += nt) {
+      float a = 0.0f, b = -1.0f;
+      for(int q = 0; q < PG; q++) {
+        a += red[q * cgN * VEC + c];
+        b = fmaxf(b, red[(nt + q * cgN) * VEC + c]);
+      }
+      sums[cg0 * VEC + c] = a;
+      maxs[cg0 * VEC + c] = b;
+    }
+    __syncthreads();
+  }
+}
+
+// poolKernel with 16-byte loads spread over all threads (see poolBoardVec).
+template<typename T, bool VALUE_MODE>
+__global__ void poolVecKernel(const T* __restrict__ g, int ldG, int C, const float* __restrict__ mask,
+                              const float* __restrict__ maskSum, int HW, float* __restrict__ pooledOut, int ldPooled,
+                              const float* __restrict__ Wt, int cout, float* __restrict__ out, int ldOut) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  extern __shared__ float smem[];
+  const int n = blockIdx.x;
+  float* sums = smem;                 // [C]
+  float* maxs = sums + C;             // [C]
+  float* pooled = maxs + C;           // [3C]
+  float* red = pooled + 3 * C;        // [2 * blockDim.x * VEC]
+  poolBoardVec<T>(g, ldG, C, mask, n, HW, sums, maxs, red);
+  const float div = maskSum[n];
+  const float sq = sqrtf(div) - 14.0f;
+  for(int c = threadIdx.x; c < C; c += blockDim.x) {
+    const float mean = sums[c] / div;
+    pooled[c] = mean;
+    pooled[c + C] = mean * sq * 0.1f;
+    pooled[c + 2 * C] = VALUE_MODE ? mean * (sq * sq * 0.01f - 0.1f) : maxs[c];
+  }
+  __syncthreads();
+  if(pooledOut != nullptr)
+    for(int i = threadIdx.x; i < 3 * C; i += blockDim.x) pooledOut[(size_t)n * ldPooled + i] = pooled[i];
+  if(Wt != nullptr) {
+    for(int co = threadIdx.x; co < cout; co += blockDim.x) {
+      float acc = 0.0f;
+      for(int i = 0; i < 3 * C; i++) acc += pooled[i] * Wt[(size_t)i * cout + co];
+      out[(size_t)n * ldOut + co] = acc;
+    }
+  }
+  (void)VEC;
+}
+
 template<typename T, bool VALUE_MODE>
 __global__ void poolKernel(const T* __restrict__ g, int ldG, int C, const float* __restrict__ mask,
                            const float* __restrict__ maskSum, int HW, float* __restrict__ pooledOut, int ldPooled,
@@ -151,33 +243,30 @@ __global__ void bnActKernel(const T* __restrict__ x, int ldX, T* __restrict__ y,
   y[(size_t)m * ldY + c] = kgh_from_float<T>(a * mask[m]);
 }
 
-// Same as bnActKernel with one thread per 8 channels of a row (16-byte
-// accesses for fp16). Requires C, ldX, ldY, ldNC multiples of 8.
+// Same as bnActKernel with one thread per 16 bytes of a row (8 fp16 or 4
+// fp32 channels). Requires C, ldX, ldY, ldNC multiples of that and 16-byte
+// aligned rows.
 template<typename T>
-__global__ void bnActKernel8(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ scale,
-                             const float* __restrict__ bias, int act, const float* __restrict__ mask,
-                             const float* __restrict__ ncBias, int ldNC, int HW, long total8) {
-  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if(idx >= total8) return;
-  const int C8 = C >> 3;
-  int m = (int)(idx / C8);
-  int c = (int)(idx - (long)m * C8) * 8;
-  T in[8];
-  const T* src = x + (size_t)m * ldX + c;
-#pragma unroll
-  for(int j = 0; j < 8; j++) in[j] = src[j];
+__global__ void bnActVecKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ scale,
+                               const float* __restrict__ bias, int act, const float* __restrict__ mask,
+                               const float* __restrict__ ncBias, int ldNC, int HW, int total) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= total) return;
+  const int CG = C / VEC;
+  const int m = idx / CG;
+  const int c = (idx - m * CG) * VEC;
+  T in[VEC], out[VEC];
+  *(uint4*)in = *(const uint4*)(x + (size_t)m * ldX + c);
   const float msk = mask[m];
   const float* nb = ncBias != nullptr ? ncBias + (size_t)(m / HW) * ldNC + c : nullptr;
-  T out[8];
 #pragma unroll
-  for(int j = 0; j < 8; j++) {
+  for(int j = 0; j < VEC; j++) {
     float v = kgh_to_float(in[j]);
     if(nb != nullptr) v += nb[j];
     out[j] = kgh_from_float<T>(kgh_activate_fast(v * scale[c + j] + bias[c + j], act) * msk);
   }
-  T* dst = y + (size_t)m * ldY + c;
-#pragma unroll
-  for(int j = 0; j < 8; j++) dst[j] = out[j];
+  *(uint4*)(y + (size_t)m * ldY + c) = *(const uint4*)out;
 }
 
 // Small per-row part of the heads (eigenbackend.cpp:1980-2024, 2067-2102),
@@ -191,11 +280,37 @@ __global__ void headRowKernel(HeadRowArgs<T> a) {
   float* gpool = smem;              // [3*G1]
   float* vpool = gpool + 3 * G1;    // [3*V1]
   float* hidden = vpool + 3 * V1;   // [max(p1C, v2C)]
-  float* scratch = hidden + a.hiddenMax;  // partial sums: [blockDim.x]
+  float* scratch = hidden + a.hiddenMax;  // pooling work area
 
   // Pool g1 (gpool formula) and v1 (value formula) channels.
   const float div = a.maskSum[n];
   const float sq = sqrtf(div) - 14.0f;
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const bool vec = G1 % VEC == 0 && V1 % VEC == 0 && a.ldG1 % VEC == 0 && a.ldV1 % VEC == 0 &&
+                   (((uintptr_t)a.g1 | (uintptr_t)a.v1) & 15) == 0;
+  if(vec) {
+    // scratch: sums/maxs of g1 then v1, then the reduction area.
+    float* sums = scratch;
+    float* maxs = sums + G1 + V1;
+    float* red = maxs + G1 + V1;
+    poolBoardVec<T>(a.g1, a.ldG1, G1, a.mask, n, HW, sums, maxs, red);
+    poolBoardVec<T>(a.v1, a.ldV1, V1, a.mask, n, HW, sums + G1, maxs + G1, red);
+    for(int c = threadIdx.x; c < G1 + V1; c += blockDim.x) {
+      const float mean = sums[c] / div;
+      if(c < G1) {
+        gpool[c] = mean;
+        gpool[c + G1] = mean * sq * 0.1f;
+        gpool[c + 2 * G1] = maxs[c];
+      }
+      else {
+        const int cc = c - G1;
+        vpool[cc] = mean;
+        vpool[cc + V1] = mean * sq * 0.1f;
+        vpool[cc + 2 * V1] = mean * (sq * sq * 0.01f - 0.1f);
+      }
+    }
+  }
+  else
   for(int c = threadIdx.x; c < G1 + V1; c += blockDim.x) {
     const bool isG = c < G1;
     const T* src = isG ? a.g1 : a.v1;
@@ -272,24 +387,53 @@ __global__ void headRowKernel(HeadRowArgs<T> a) {
 }
 
 // Per-position part of the heads: policy = p2Conv(act(p1BN(p1 + g1Bias)) * mask),
-// ownership = ownershipConv(v1).
+// ownership = ownershipConv(v1). 16-byte loads of the p1 and v1 rows when the
+// channel counts and strides allow.
 template<typename T>
 __global__ void headSpatialKernel(HeadSpatialArgs<T> a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
   int m = blockIdx.x * blockDim.x + threadIdx.x;
   if(m >= a.M) return;
   int n = m / a.HW;
   float msk = a.mask[m];
   float pol[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const T* p1 = a.p1 + (size_t)m * a.ldP1;
-  for(int c = 0; c < a.p1C; c++) {
-    float v = kgh_to_float(p1[c]) + a.g1Bias[(size_t)n * a.p1C + c];
-    float act = kgh_activate(v * a.p1Scale[c] + a.p1Bias[c], a.p1Act) * msk;
-    for(int pc = 0; pc < a.policyC; pc++) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
+  const float* gb = a.g1Bias + (size_t)n * a.p1C;
+  const bool vec = a.p1C % VEC == 0 && a.v1C % VEC == 0 && a.ldP1 % VEC == 0 && a.ldV1 % VEC == 0 &&
+                   (((uintptr_t)a.p1 | (uintptr_t)a.v1) & 15) == 0;
+  if(vec) {
+    for(int c0 = 0; c0 < a.p1C; c0 += VEC) {
+      T v[VEC];
+      *(uint4*)v = *(const uint4*)(p1 + c0);
+#pragma unroll
+      for(int j = 0; j < VEC; j++) {
+        const int c = c0 + j;
+        const float act = kgh_activate((kgh_to_float(v[j]) + gb[c]) * a.p1Scale[c] + a.p1Bias[c], a.p1Act) * msk;
+        for(int pc = 0; pc < a.policyC; pc++) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
+      }
+    }
+  }
+  else {
+    for(int c = 0; c < a.p1C; c++) {
+      float v = kgh_to_float(p1[c]) + gb[c];
+      float act = kgh_activate(v * a.p1Scale[c] + a.p1Bias[c], a.p1Act) * msk;
+      for(int pc = 0; pc < a.policyC; pc++) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
+    }
   }
   for(int pc = 0; pc < a.policyC; pc++) a.policy[(size_t)m * a.policyC + pc] = pol[pc];
   const T* v1 = a.v1 + (size_t)m * a.ldV1;
   float own = 0.0f;
-  for(int c = 0; c < a.v1C; c++) own += kgh_to_float(v1[c]) * a.ownW[c];
+  if(vec) {
+    for(int c0 = 0; c0 < a.v1C; c0 += VEC) {
+      T v[VEC];
+      *(uint4*)v = *(const uint4*)(v1 + c0);
+#pragma unroll
+      for(int j = 0; j < VEC; j++) own += kgh_to_float(v[j]) * a.ownW[c0 + j];
+    }
+  }
+  else {
+    for(int c = 0; c < a.v1C; c++) own += kgh_to_float(v1[c]) * a.ownW[c];
+  }
   a.ownership[m] = own;
 }
 
@@ -346,6 +490,19 @@ void launchRowMatmul(const float* in, int ldIn, int cin, const float* Wt, int co
 template<typename T>
 void launchPool(const T* g, int ldG, int C, const float* mask, const float* maskSum, int batch, int HW, bool valueMode,
                 float* pooledOut, int ldPooled, const float* Wt, int cout, float* out, int ldOut, hipStream_t stream) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  if(C % VEC == 0 && ldG % VEC == 0 && ((uintptr_t)g & 15) == 0) {
+    const int threads = 256;
+    const size_t smem = (size_t)(5 * C + 2 * threads * VEC) * sizeof(float);
+    if(valueMode)
+      hipLaunchKernelGGL((poolVecKernel<T, true>), dim3(batch), dim3(threads), smem, stream, g, ldG, C, mask, maskSum, HW, pooledOut,
+                         ldPooled, Wt, cout, out, ldOut);
+    else
+      hipLaunchKernelGGL((poolVecKernel<T, false>), dim3(batch), dim3(threads), smem, stream, g, ldG, C, mask, maskSum, HW, pooledOut,
+                         ldPooled, Wt, cout, out, ldOut);
+    KGH_CHECK_LAUNCH();
+    return;
+  }
   int threads = 256;
   int groups = threads / C > 0 ? threads / C : 1;
   size_t smem = (size_t)(2 * groups * C + 3 * C) * sizeof(float);
@@ -361,10 +518,12 @@ void launchPool(const T* g, int ldG, int C, const float* mask, const float* mask
 template<typename T>
 void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, const float* bias, int act, const float* mask,
                  const float* ncBias, int ldNC, int HW, int M, hipStream_t stream) {
-  if(C % 8 == 0 && ldX % 8 == 0 && ldY % 8 == 0 && (ncBias == nullptr || ldNC % 8 == 0)) {
-    long total8 = (long)M * (C / 8);
-    hipLaunchKernelGGL(bnActKernel8<T>, dim3((unsigned)((total8 + 255) / 256)), dim3(256), 0, stream, x, ldX, y, ldY, C, scale,
-                       bias, act, mask, ncBias, ldNC, HW, total8);
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const bool aligned = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
+  if(aligned && C % VEC == 0 && ldX % VEC == 0 && ldY % VEC == 0 && (long)M * (C / VEC) < INT_MAX) {
+    const int total = M * (C / VEC);
+    hipLaunchKernelGGL(bnActVecKernel<T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, x, ldX, y, ldY, C, scale,
+                       bias, act, mask, ncBias, ldNC, HW, total);
     KGH_CHECK_LAUNCH();
     return;
   }
@@ -377,7 +536,7 @@ void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, 
 template<typename T>
 void launchHeadRow(const HeadRowArgs<T>& a, int batch, hipStream_t stream) {
   int threads = 256;
-  size_t smem = (size_t)(3 * a.g1C + 3 * a.v1C + a.hiddenMax + threads) * sizeof(float);
+  size_t smem = (size_t)(3 * a.g1C + 3 * a.v1C + a.hiddenMax + 2 * (a.g1C + a.v1C) + 2 * threads * (16 / sizeof(T))) * sizeof(float);
   hipLaunchKernelGGL(headRowKernel<T>, dim3(batch), dim3(threads), smem, stream, a);
   KGH_CHECK_LAUNCH();
 }

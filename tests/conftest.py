@@ -16,6 +16,7 @@ def _libs_built() -> bool:
     return all(os.path.exists(p) for p in (
         os.path.join(ROOT, "katago_amd", "lib", "libkatago_hip.so"),
         os.path.join(ROOT, "katago_amd", "lib", "libkatago_host.so"),
+        os.path.join(ROOT, "katago_amd", "lib", "kernel_resources.json"),
         os.path.join(ROOT, "oracle", "liboracle_eigen.so"),
     ))
 

@@ -157,3 +157,24 @@ def test_flattened_program_structure(model_dir):
     assert len(three) == 1 + 2 * 31 + 3 * 5
     assert np.isfinite(weights).all()
     assert (layers["w"][:, 0] + layers["wn"][:, 0] <= len(weights)).all()
+
+
+def test_hot_kernels_keep_everything_in_registers():
+    """The build records the compiler's per-kernel resource report
+    (katago_amd/lib/kernel_resources.json). A matrix-core kernel whose
+    accumulators fall out of registers into scratch runs several times
+    slower with identical results, so this guards it on the CPU."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "katago_amd", "lib", "kernel_resources.json")
+    with open(path) as f:
+        usage = json.load(f)
+    hot = ("convTapWindowKernel", "conv1x1DmaKernel", "convMfmaKernel", "flashAttentionKernel", "poolVecKernel",
+           "bnActVecKernel", "rmsNormRowKernel", "headSpatialKernel")
+    seen = set()
+    for name, u in usage.items():
+        for h in hot:
+            if h in name:
+                seen.add(h)
+                assert u["scratch"] == 0 and u["vgpr_spill"] == 0, (name, u)
+    assert seen == set(hot), set(hot) - seen
