@@ -145,6 +145,14 @@ int kgh_evaluate_layers(int32_t device, const kgh_layer* layers, int32_t num_lay
                         int64_t num_weights, int32_t use_fp16, int32_t batch, int32_t nn_x, int32_t nn_y,
                         const float* input, const float* mask, float* output);
 
+/* HIP graph replay of forwards (no counterpart in the reference, whose
+ * backends launch eagerly): when enabled (the default), a forward whose batch
+ * size and row buffers repeat those of the previous call on the handle is
+ * captured into a graph and replayed from then on (up to 8 graphs per
+ * handle, least recently used evicted). Results are bitwise those of eager
+ * launches. Forwards while profiling is on always run eagerly. */
+int kgh_handle_set_graphs(kgh_handle* handle, int32_t enabled);
+
 /* Per-launch timing of the convolution kernels, measured with HIP events on
  * the handle's stream. kgh_handle_set_profiling(h, 1) clears the records and
  * starts recording every conv launch of the following forwards;

@@ -515,7 +515,21 @@ struct kgh_handle {
   std::vector<ProfRec> prof;
   size_t profUsed = 0;
 
+  // Captured forwards, keyed by batch size and the five row buffers.
+  struct GraphEntry {
+    int n = 0;
+    const void* ptr[5] = {};
+    hipGraphExec_t exec = nullptr;
+    uint64_t lastUse = 0;
+  };
+  bool graphsEnabled = true;
+  std::vector<GraphEntry> graphs;
+  int lastN = -1;
+  const void* lastPtr[5] = {};
+  uint64_t useCounter = 0;
+
   ~kgh_handle() {
+    for(auto& g : graphs) (void)hipGraphExecDestroy(g.exec);
     for(auto& p : prof) {
       (void)hipEventDestroy(p.start);
       (void)hipEventDestroy(p.stop);
@@ -881,6 +895,74 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
   kgh::launchUnpackOutputs(ua, s);
 }
 
+// Runs one forward on the handle's stream. A forward whose batch size and
+// buffers repeat those of the previous call is captured into a HIP graph
+// (the kernels only: no memsets or copies are recorded) and replayed from
+// then on, which removes the per-launch host overhead between the ~150
+// kernels of a forward. Profiling runs eagerly.
+constexpr size_t KGH_MAX_GRAPHS = 8;
+
+void runForward(kgh_handle* h, int n, const float* sp, const float* gl, const int* sym, const float* opt, float* out) {
+  auto eager = [&] {
+    if(h->model->net.fp16) forwardImpl<half_t>(h, n, sp, gl, sym, opt, out);
+    else forwardImpl<float>(h, n, sp, gl, sym, opt, out);
+  };
+  if(!h->graphsEnabled || h->profiling) {
+    eager();
+    return;
+  }
+  const void* key[5] = {sp, gl, sym, opt, out};
+  auto same = [&](const void* const* p) {
+    for(int i = 0; i < 5; i++)
+      if(p[i] != key[i]) return false;
+    return true;
+  };
+  for(auto& g : h->graphs) {
+    if(g.n == n && same(g.ptr)) {
+      g.lastUse = ++h->useCounter;
+      KGH_HIP_CHECK(hipGraphLaunch(g.exec, h->stream));
+      return;
+    }
+  }
+  const bool repeat = h->lastN == n && same(h->lastPtr);
+  h->lastN = n;
+  for(int i = 0; i < 5; i++) h->lastPtr[i] = key[i];
+  if(!repeat) {
+    eager();
+    return;
+  }
+  hipGraph_t graph = nullptr;
+  KGH_HIP_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+  try {
+    eager();
+  }
+  catch(...) {
+    hipGraph_t partial = nullptr;
+    (void)hipStreamEndCapture(h->stream, &partial);
+    if(partial) (void)hipGraphDestroy(partial);
+    throw;
+  }
+  KGH_HIP_CHECK(hipStreamEndCapture(h->stream, &graph));
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  KGH_HIP_CHECK(e);
+  if(h->graphs.size() >= KGH_MAX_GRAPHS) {
+    size_t lru = 0;
+    for(size_t i = 1; i < h->graphs.size(); i++)
+      if(h->graphs[i].lastUse < h->graphs[lru].lastUse) lru = i;
+    (void)hipGraphExecDestroy(h->graphs[lru].exec);
+    h->graphs.erase(h->graphs.begin() + lru);
+  }
+  kgh_handle::GraphEntry ge;
+  ge.n = n;
+  for(int i = 0; i < 5; i++) ge.ptr[i] = key[i];
+  ge.exec = exec;
+  ge.lastUse = ++h->useCounter;
+  h->graphs.push_back(ge);
+  KGH_HIP_CHECK(hipGraphLaunch(exec, h->stream));
+}
+
 void buildNet(kgh_model* m, const kgh_model_desc* d, hipStream_t stream) {
   Net& net = m->net;
   const float* devW = m->arena.allocN<float>((size_t)std::max<int64_t>(d->num_weights, 1));
@@ -1192,10 +1274,7 @@ int kgh_forward_device(kgh_handle* handle, int32_t n, const float* d_spatial, co
     if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
     if(!d_spatial || !d_global || !d_symmetry || !d_policy_optimism || !d_out) invalid("null device pointer");
     KGH_HIP_CHECK(hipSetDevice(handle->model->device));
-    if(handle->model->net.fp16)
-      forwardImpl<half_t>(handle, n, d_spatial, d_global, d_symmetry, d_policy_optimism, d_out);
-    else
-      forwardImpl<float>(handle, n, d_spatial, d_global, d_symmetry, d_policy_optimism, d_out);
+    runForward(handle, n, d_spatial, d_global, d_symmetry, d_policy_optimism, d_out);
   });
 }
 
@@ -1221,10 +1300,7 @@ int kgh_forward(kgh_handle* handle, int32_t n, const float* spatial, const float
     KGH_HIP_CHECK(hipMemcpyAsync(handle->dGlobal, handle->hGlobal, globalBytes, hipMemcpyHostToDevice, s));
     KGH_HIP_CHECK(hipMemcpyAsync(handle->dSym, handle->hSym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
     KGH_HIP_CHECK(hipMemcpyAsync(handle->dOpt, handle->hOpt, (size_t)n * sizeof(float), hipMemcpyHostToDevice, s));
-    if(net.fp16)
-      forwardImpl<half_t>(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
-    else
-      forwardImpl<float>(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
+    runForward(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
     const size_t outBytes = (size_t)n * handle->rowFloats * sizeof(float);
     KGH_HIP_CHECK(hipMemcpyAsync(handle->hOut, handle->dOut, outBytes, hipMemcpyDeviceToHost, s));
     KGH_HIP_CHECK(hipStreamSynchronize(s));
@@ -1256,6 +1332,14 @@ int kgh_memcpy_htod(void* dst, const void* src, size_t bytes) {
 }
 int kgh_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
   return guarded([&] { KGH_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost)); });
+}
+
+int kgh_handle_set_graphs(kgh_handle* handle, int32_t enabled) {
+  return guarded([&] {
+    requireHandle(handle);
+    handle->graphsEnabled = enabled != 0;
+    handle->lastN = -1;
+  });
 }
 
 int kgh_handle_set_profiling(kgh_handle* handle, int32_t enabled) {

@@ -310,6 +310,7 @@ class DeviceHandle:
         lib.kgh_forward_device.argtypes = [ctypes.c_void_p, ctypes.c_int32] + [ctypes.c_void_p] * 5
         lib.kgh_handle_synchronize.argtypes = [ctypes.c_void_p]
         lib.kgh_handle_set_profiling.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+        lib.kgh_handle_set_graphs.argtypes = [ctypes.c_void_p, ctypes.c_int32]
         lib.kgh_handle_profile.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
                                            ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_double)]
         self.row_floats = lib.kgh_output_row_floats(nn_x, nn_y, model.info.num_score_value_channels)
@@ -322,6 +323,10 @@ class DeviceHandle:
 
     def set_profiling(self, on: bool):
         hip_check(hip_library().kgh_handle_set_profiling(self._ptr, int(on)))
+
+    def set_graphs(self, on: bool):
+        """Enables (default) or disables HIP graph replay of repeated forwards."""
+        hip_check(hip_library().kgh_handle_set_graphs(self._ptr, int(on)))
 
     def profile(self, kind: int):
         ms = ctypes.c_double()

@@ -267,6 +267,34 @@ def test_c2_full_batch_rows_are_independent(model_dir):
         assert np.isfinite(full[k]).all()
 
 
+def test_graph_replays_match_eager_forwards(model_dir):
+    """A repeated forward is captured into a HIP graph and replayed. Every
+    replay, with eager work and synchronisations in between (a different
+    batch size on the same handle), must equal the eager result bitwise."""
+    cfg = modelgen.configs()[1]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    dm = nn.DeviceModel(lm, use_fp16=True)
+    h = nn.DeviceHandle(dm, 16)
+    sp, gl = modelgen.synthetic_inputs(3, 16, board_sizes=(19, 9))
+    bufs = [nn.DeviceBuffer.from_array(a) for a in (sp, gl, (np.arange(16) % 8).astype(np.int32), np.zeros(16, np.float32))]
+    out = nn.DeviceBuffer(16 * h.row_floats * 4)
+    other = nn.DeviceBuffer(16 * h.row_floats * 4)
+
+    def run(n, dst):
+        h.forward_device(n, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, dst.ptr)
+        h.synchronize()
+        return dst.to_array(np.float32, (16, h.row_floats))[:n].copy()
+
+    h.set_graphs(False)
+    eager16 = run(16, out)
+    eager5 = run(5, other)
+    h.set_graphs(True)
+    for i in range(5):  # first eager, second captured, then replays
+        assert np.array_equal(run(16, out), eager16), f"replay {i}"
+        assert np.array_equal(run(5, other), eager5), f"interleaved {i}"
+        assert np.array_equal(run(16, out), eager16), f"replay {i} after interleave"
+
+
 def test_errors_are_raised_not_crashed(model_dir):
     cfg = modelgen.configs()[0]
     lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
