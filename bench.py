@@ -44,7 +44,7 @@ def conv_flops(layers, hw):
     return f3, f1, other
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "convMfmaKernel_b18c384nbt_b256_fp16_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "conv3x3_b18c384nbt_b256_fp16_traffic.md")
 
 
 def measured_traffic():
@@ -198,7 +198,7 @@ def main():
                    "global_batch": batch, "board": "19x19", "parallelism": "none (1 GPU)"},
         "mfma_frac_end_to_end": round(value * flops_per_eval / (PEAK_FP16_TFLOPS * 1e12), 4),
         "gflop_per_eval": round(flops_per_eval / 1e9, 3),
-        "roofline": {"bound": "mfma", "kernel": "convMfmaKernel (3x3, fp16)", "achieved": round(achieved3, 2),
+        "roofline": {"bound": "mfma", "kernel": "convTapWindowKernel (3x3, fp16)", "achieved": round(achieved3, 2),
                      "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved3 / PEAK_FP16_TFLOPS, 4),
                      "traffic": measured_traffic(), "avg_launch_ms": round(avg3_ms, 5), "launches": n3,
                      "timing": f"HIP events around each launch over {prof_steps} eager forwards after the timed steps"},

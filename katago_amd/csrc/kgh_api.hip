@@ -491,6 +491,8 @@ struct kgh_handle {
   void* p1 = nullptr;
   void* gv = nullptr;
   float* g1Bias = nullptr;
+  float* headFeat = nullptr;  // per row: g1 pool [3 g1C], v1 pool [3 v1C], hidden [headHidden]
+  int headFeatLd = 0;
   float* pass = nullptr;
   float* value = nullptr;
   float* score = nullptr;
@@ -821,39 +823,30 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
     e.actKind = hc.act.act;
     r.conv(hc.conv, r.A[0], net.trunkC, e);
   }
-  HeadRowArgs<T> ha;
-  ha.g1 = gv;
-  ha.ldG1 = gvC;
-  ha.v1 = gv + net.g1C;
-  ha.ldV1 = gvC;
-  ha.g1C = net.g1C;
-  ha.v1C = net.v1C;
-  ha.p1C = net.p1C;
-  ha.policyC = net.policyC;
-  ha.passHidden = net.passMul2.w != nullptr ? net.passMul.cout : 0;
-  ha.v2C = net.v2Mul.cout;
-  ha.scoreC = net.scoreC;
-  ha.hiddenMax = std::max(ha.passHidden, ha.v2C);
-  ha.HW = HW;
-  ha.mask = h->mask;
-  ha.maskSum = h->maskSum;
-  ha.gpoolToBiasMul = net.gpoolToBiasMul.w;
-  ha.passMul = net.passMul.w;
-  ha.passBias = net.passBias.b;
-  ha.passAct = net.passAct;
-  ha.passMul2 = net.passMul2.w;
-  ha.v2Mul = net.v2Mul.w;
-  ha.v2Bias = net.v2Bias.b;
-  ha.v2Act = net.v2Act;
-  ha.v3Mul = net.v3Mul.w;
-  ha.v3Bias = net.v3Bias.b;
-  ha.sv3Mul = net.sv3Mul.w;
-  ha.sv3Bias = net.sv3Bias.b;
-  ha.g1Bias = h->g1Bias;
-  ha.pass = h->pass;
-  ha.value = h->value;
-  ha.score = h->score;
-  kgh::launchHeadRow<T>(ha, n, s);
+  // Pooled head features per row (vectorised per-board pooling), then the
+  // small matmuls as row-parallel launches (eigenbackend.cpp:1980-2024,
+  // 2067-2102).
+  {
+    const int ld = h->headFeatLd;
+    float* gfeat = h->headFeat;
+    float* vfeat = gfeat + 3 * net.g1C;
+    float* hidden = vfeat + 3 * net.v1C;
+    kgh::launchPool<T>(gv, gvC, net.g1C, h->mask, h->maskSum, n, HW, false, gfeat, ld, nullptr, 0, nullptr, 0, s);
+    kgh::launchPool<T>(gv + net.g1C, gvC, net.v1C, h->mask, h->maskSum, n, HW, true, vfeat, ld, nullptr, 0, nullptr, 0, s);
+    kgh::launchRowMatmul(gfeat, ld, 3 * net.g1C, net.gpoolToBiasMul.w, net.p1C, nullptr, KGH_ACT_IDENTITY, h->g1Bias, net.p1C, n, s);
+    if(net.passMul2.w != nullptr) {
+      kgh::launchRowMatmul(gfeat, ld, 3 * net.g1C, net.passMul.w, net.passMul.cout, net.passBias.b, net.passAct, hidden, ld, n, s);
+      kgh::launchRowMatmul(hidden, ld, net.passMul.cout, net.passMul2.w, net.policyC, nullptr, KGH_ACT_IDENTITY, h->pass, net.policyC,
+                           n, s);
+    }
+    else {
+      kgh::launchRowMatmul(gfeat, ld, 3 * net.g1C, net.passMul.w, net.policyC, nullptr, KGH_ACT_IDENTITY, h->pass, net.policyC, n, s);
+    }
+    kgh::launchRowMatmul(vfeat, ld, 3 * net.v1C, net.v2Mul.w, net.v2Mul.cout, net.v2Bias.b, net.v2Act, hidden, ld, n, s);
+    kgh::launchRowMatmul(hidden, ld, net.v2Mul.cout, net.v3Mul.w, 3, net.v3Bias.b, KGH_ACT_IDENTITY, h->value, 3, n, s);
+    kgh::launchRowMatmul(hidden, ld, net.v2Mul.cout, net.sv3Mul.w, net.scoreC, net.sv3Bias.b, KGH_ACT_IDENTITY, h->score, net.scoreC,
+                         n, s);
+  }
 
   HeadSpatialArgs<T> hs;
   hs.p1 = p1;
@@ -1205,6 +1198,8 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     h->p1 = a.alloc(M * net.p1C * es);
     h->gv = a.alloc(M * (net.g1C + net.v1C) * es);
     h->g1Bias = a.allocN<float>((size_t)max_batch * net.p1C);
+    h->headFeatLd = 3 * net.g1C + 3 * net.v1C + std::max(net.passMul.cout, net.v2Mul.cout);
+    h->headFeat = a.allocN<float>((size_t)max_batch * h->headFeatLd);
     h->pass = a.allocN<float>((size_t)max_batch * net.policyC);
     h->value = a.allocN<float>((size_t)max_batch * 3);
     h->score = a.allocN<float>((size_t)max_batch * net.scoreC);

@@ -4,32 +4,6 @@
 
 #include "kgh_common.h"
 
-template<typename T>
-struct HeadRowArgs {
-  const T* g1;  // activated g1 channels, row stride ldG1
-  int ldG1;
-  const T* v1;  // activated v1 channels, row stride ldV1
-  int ldV1;
-  int g1C, v1C, p1C, policyC, passHidden, v2C, scoreC, hiddenMax, HW;
-  const float* mask;
-  const float* maskSum;
-  const float* gpoolToBiasMul;  // [3*g1C][p1C]
-  const float* passMul;         // [3*g1C][passHidden] (v>=15) or [3*g1C][policyC]
-  const float* passBias;        // [passHidden] or null
-  int passAct;
-  const float* passMul2;        // [passHidden][policyC] or null (model version < 15)
-  const float* v2Mul;           // [3*v1C][v2C]
-  const float* v2Bias;
-  int v2Act;
-  const float* v3Mul;           // [v2C][3]
-  const float* v3Bias;
-  const float* sv3Mul;          // [v2C][scoreC]
-  const float* sv3Bias;
-  float* g1Bias;                // out [batch][p1C]
-  float* pass;                  // out [batch][policyC]
-  float* value;                 // out [batch][3]
-  float* score;                 // out [batch][scoreC]
-};
 
 template<typename T>
 struct HeadSpatialArgs {
@@ -77,9 +51,6 @@ void launchPool(const T* g, int ldG, int C, const float* mask, const float* mask
 template<typename T>
 void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, const float* bias, int act, const float* mask,
                  const float* ncBias, int ldNC, int HW, int M, hipStream_t stream);
-
-template<typename T>
-void launchHeadRow(const HeadRowArgs<T>& a, int batch, hipStream_t stream);
 
 template<typename T>
 void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream);

@@ -73,8 +73,20 @@ __global__ void rowMatmulKernel(const float* __restrict__ in, int ldIn, int cin,
   if(idx >= batch * cout) return;
   int n = idx / cout;
   int co = idx - n * cout;
-  float acc = 0.0f;
-  for(int i = 0; i < cin; i++) acc += in[(size_t)n * ldIn + i] * Wt[(size_t)i * cout + co];
+  // Four partial sums and an unrolled loop keep several independent loads in
+  // flight per thread.
+  const float* x = in + (size_t)n * ldIn;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  int i = 0;
+#pragma unroll 2
+  for(; i + 4 <= cin; i += 4) {
+    a0 += x[i] * Wt[(size_t)i * cout + co];
+    a1 += x[i + 1] * Wt[(size_t)(i + 1) * cout + co];
+    a2 += x[i + 2] * Wt[(size_t)(i + 2) * cout + co];
+    a3 += x[i + 3] * Wt[(size_t)(i + 3) * cout + co];
+  }
+  for(; i < cin; i++) a0 += x[i] * Wt[(size_t)i * cout + co];
+  float acc = (a0 + a1) + (a2 + a3);
   if(bias != nullptr) acc += bias[co];
   out[(size_t)n * ldOut + co] = kgh_activate(acc, act);
 }
@@ -244,12 +256,13 @@ __global__ void bnActKernel(const T* __restrict__ x, int ldX, T* __restrict__ y,
 }
 
 // Same as bnActKernel with one thread per 16 bytes of a row (8 fp16 or 4
-// fp32 channels). Requires C, ldX, ldY, ldNC multiples of that and 16-byte
-// aligned rows.
-template<typename T>
+// fp32 channels) and the activation fixed at compile time, so that every
+// parameter load is issued before the arithmetic. Requires C, ldX, ldY
+// multiples of that and 16-byte aligned rows.
+template<typename T, int ACT>
 __global__ void bnActVecKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ scale,
-                               const float* __restrict__ bias, int act, const float* __restrict__ mask,
-                               const float* __restrict__ ncBias, int ldNC, int HW, int total) {
+                               const float* __restrict__ bias, const float* __restrict__ mask, const float* __restrict__ ncBias,
+                               int ldNC, int HW, int total) {
   constexpr int VEC = 16 / (int)sizeof(T);
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if(idx >= total) return;
@@ -257,133 +270,27 @@ __global__ void bnActVecKernel(const T* __restrict__ x, int ldX, T* __restrict__
   const int m = idx / CG;
   const int c = (idx - m * CG) * VEC;
   T in[VEC], out[VEC];
+  float sc[VEC], bi[VEC], nb[VEC];
   *(uint4*)in = *(const uint4*)(x + (size_t)m * ldX + c);
   const float msk = mask[m];
-  const float* nb = ncBias != nullptr ? ncBias + (size_t)(m / HW) * ldNC + c : nullptr;
 #pragma unroll
   for(int j = 0; j < VEC; j++) {
-    float v = kgh_to_float(in[j]);
-    if(nb != nullptr) v += nb[j];
-    out[j] = kgh_from_float<T>(kgh_activate_fast(v * scale[c + j] + bias[c + j], act) * msk);
+    sc[j] = scale[c + j];
+    bi[j] = bias[c + j];
   }
-  *(uint4*)(y + (size_t)m * ldY + c) = *(const uint4*)out;
-}
-
-// Small per-row part of the heads (eigenbackend.cpp:1980-2024, 2067-2102),
-// one workgroup per batch row.
-template<typename T>
-__global__ void headRowKernel(HeadRowArgs<T> a) {
-  extern __shared__ float smem[];
-  const int n = blockIdx.x;
-  const int HW = a.HW;
-  const int G1 = a.g1C, V1 = a.v1C;
-  float* gpool = smem;              // [3*G1]
-  float* vpool = gpool + 3 * G1;    // [3*V1]
-  float* hidden = vpool + 3 * V1;   // [max(p1C, v2C)]
-  float* scratch = hidden + a.hiddenMax;  // pooling work area
-
-  // Pool g1 (gpool formula) and v1 (value formula) channels.
-  const float div = a.maskSum[n];
-  const float sq = sqrtf(div) - 14.0f;
-  constexpr int VEC = 16 / (int)sizeof(T);
-  const bool vec = G1 % VEC == 0 && V1 % VEC == 0 && a.ldG1 % VEC == 0 && a.ldV1 % VEC == 0 &&
-                   (((uintptr_t)a.g1 | (uintptr_t)a.v1) & 15) == 0;
-  if(vec) {
-    // scratch: sums/maxs of g1 then v1, then the reduction area.
-    float* sums = scratch;
-    float* maxs = sums + G1 + V1;
-    float* red = maxs + G1 + V1;
-    poolBoardVec<T>(a.g1, a.ldG1, G1, a.mask, n, HW, sums, maxs, red);
-    poolBoardVec<T>(a.v1, a.ldV1, V1, a.mask, n, HW, sums + G1, maxs + G1, red);
-    for(int c = threadIdx.x; c < G1 + V1; c += blockDim.x) {
-      const float mean = sums[c] / div;
-      if(c < G1) {
-        gpool[c] = mean;
-        gpool[c + G1] = mean * sq * 0.1f;
-        gpool[c + 2 * G1] = maxs[c];
-      }
-      else {
-        const int cc = c - G1;
-        vpool[cc] = mean;
-        vpool[cc + V1] = mean * sq * 0.1f;
-        vpool[cc + 2 * V1] = mean * (sq * sq * 0.01f - 0.1f);
-      }
-    }
-  }
-  else
-  for(int c = threadIdx.x; c < G1 + V1; c += blockDim.x) {
-    const bool isG = c < G1;
-    const T* src = isG ? a.g1 : a.v1;
-    const int ld = isG ? a.ldG1 : a.ldV1;
-    const int cc = isG ? c : c - G1;
-    float s = 0.0f;
-    float mx = -1.0f;
-    for(int p = 0; p < HW; p++) {
-      size_t m = (size_t)n * HW + p;
-      float v = kgh_to_float(src[m * ld + cc]);
-      s += v;
-      mx = fmaxf(mx, v + (a.mask[m] - 1.0f));
-    }
-    float mean = s / div;
-    if(isG) {
-      gpool[cc] = mean;
-      gpool[cc + G1] = mean * sq * 0.1f;
-      gpool[cc + 2 * G1] = mx;
-    }
-    else {
-      vpool[cc] = mean;
-      vpool[cc + V1] = mean * sq * 0.1f;
-      vpool[cc + 2 * V1] = mean * (sq * sq * 0.01f - 0.1f);
-    }
-  }
-  __syncthreads();
-
-  // Policy bias from the g1 pool.
-  for(int co = threadIdx.x; co < a.p1C; co += blockDim.x) {
-    float acc = 0.0f;
-    for(int i = 0; i < 3 * G1; i++) acc += gpool[i] * a.gpoolToBiasMul[(size_t)i * a.p1C + co];
-    a.g1Bias[(size_t)n * a.p1C + co] = acc;
-  }
-  // Pass logit(s).
-  if(a.passMul2 != nullptr) {
-    for(int co = threadIdx.x; co < a.passHidden; co += blockDim.x) {
-      float acc = 0.0f;
-      for(int i = 0; i < 3 * G1; i++) acc += gpool[i] * a.passMul[(size_t)i * a.passHidden + co];
-      hidden[co] = kgh_activate(acc + a.passBias[co], a.passAct);
-    }
-    __syncthreads();
-    for(int co = threadIdx.x; co < a.policyC; co += blockDim.x) {
-      float acc = 0.0f;
-      for(int i = 0; i < a.passHidden; i++) acc += hidden[i] * a.passMul2[(size_t)i * a.policyC + co];
-      a.pass[(size_t)n * a.policyC + co] = acc;
-    }
+  if(ncBias != nullptr) {
+    const float* nbp = ncBias + (size_t)(m / HW) * ldNC + c;
+#pragma unroll
+    for(int j = 0; j < VEC; j++) nb[j] = nbp[j];
   }
   else {
-    for(int co = threadIdx.x; co < a.policyC; co += blockDim.x) {
-      float acc = 0.0f;
-      for(int i = 0; i < 3 * G1; i++) acc += gpool[i] * a.passMul[(size_t)i * a.policyC + co];
-      a.pass[(size_t)n * a.policyC + co] = acc;
-    }
+#pragma unroll
+    for(int j = 0; j < VEC; j++) nb[j] = 0.0f;
   }
-  __syncthreads();
-  // Value trunk: v2 = act(v2Mul * vpool + v2Bias).
-  for(int co = threadIdx.x; co < a.v2C; co += blockDim.x) {
-    float acc = 0.0f;
-    for(int i = 0; i < 3 * V1; i++) acc += vpool[i] * a.v2Mul[(size_t)i * a.v2C + co];
-    hidden[co] = kgh_activate(acc + a.v2Bias[co], a.v2Act);
-  }
-  __syncthreads();
-  for(int co = threadIdx.x; co < 3 + a.scoreC; co += blockDim.x) {
-    bool isValue = co < 3;
-    int oc = isValue ? co : co - 3;
-    const float* Wt = isValue ? a.v3Mul : a.sv3Mul;
-    int ldW = isValue ? 3 : a.scoreC;
-    float acc = 0.0f;
-    for(int i = 0; i < a.v2C; i++) acc += hidden[i] * Wt[(size_t)i * ldW + oc];
-    if(isValue) a.value[(size_t)n * 3 + oc] = acc + a.v3Bias[oc];
-    else a.score[(size_t)n * a.scoreC + oc] = acc + a.sv3Bias[oc];
-  }
-  (void)scratch;
+#pragma unroll
+  for(int j = 0; j < VEC; j++)
+    out[j] = kgh_from_float<T>(kgh_activate_fast((kgh_to_float(in[j]) + nb[j]) * sc[j] + bi[j], ACT) * msk);
+  *(uint4*)(y + (size_t)m * ldY + c) = *(const uint4*)out;
 }
 
 // Per-position part of the heads: policy = p2Conv(act(p1BN(p1 + g1Bias)) * mask),
@@ -522,8 +429,30 @@ void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, 
   const bool aligned = (((uintptr_t)x | (uintptr_t)y) & 15) == 0;
   if(aligned && C % VEC == 0 && ldX % VEC == 0 && ldY % VEC == 0 && (long)M * (C / VEC) < INT_MAX) {
     const int total = M * (C / VEC);
-    hipLaunchKernelGGL(bnActVecKernel<T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, x, ldX, y, ldY, C, scale,
-                       bias, act, mask, ncBias, ldNC, HW, total);
+    const dim3 grid((unsigned)((total + 255) / 256));
+    switch(act) {
+      case KGH_ACT_IDENTITY:
+        hipLaunchKernelGGL((bnActVecKernel<T, KGH_ACT_IDENTITY>), grid, dim3(256), 0, stream, x, ldX, y, ldY, C, scale, bias, mask, ncBias,
+                           ldNC, HW, total);
+        break;
+      case KGH_ACT_RELU:
+        hipLaunchKernelGGL((bnActVecKernel<T, KGH_ACT_RELU>), grid, dim3(256), 0, stream, x, ldX, y, ldY, C, scale, bias, mask, ncBias,
+                           ldNC, HW, total);
+        break;
+      case KGH_ACT_MISH:
+        hipLaunchKernelGGL((bnActVecKernel<T, KGH_ACT_MISH>), grid, dim3(256), 0, stream, x, ldX, y, ldY, C, scale, bias, mask, ncBias,
+                           ldNC, HW, total);
+        break;
+      case KGH_ACT_SILU:
+        hipLaunchKernelGGL((bnActVecKernel<T, KGH_ACT_SILU>), grid, dim3(256), 0, stream, x, ldX, y, ldY, C, scale, bias, mask, ncBias,
+                           ldNC, HW, total);
+        break;
+      case KGH_ACT_MISH_SCALE8:
+        hipLaunchKernelGGL((bnActVecKernel<T, KGH_ACT_MISH_SCALE8>), grid, dim3(256), 0, stream, x, ldX, y, ldY, C, scale, bias, mask,
+                           ncBias, ldNC, HW, total);
+        break;
+      default: throw KghError(1, "bnAct: unknown activation " + std::to_string(act));
+    }
     KGH_CHECK_LAUNCH();
     return;
   }
@@ -533,13 +462,6 @@ void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, 
   KGH_CHECK_LAUNCH();
 }
 
-template<typename T>
-void launchHeadRow(const HeadRowArgs<T>& a, int batch, hipStream_t stream) {
-  int threads = 256;
-  size_t smem = (size_t)(3 * a.g1C + 3 * a.v1C + a.hiddenMax + 2 * (a.g1C + a.v1C) + 2 * threads * (16 / sizeof(T))) * sizeof(float);
-  hipLaunchKernelGGL(headRowKernel<T>, dim3(batch), dim3(threads), smem, stream, a);
-  KGH_CHECK_LAUNCH();
-}
 
 template<typename T>
 void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream) {
@@ -559,7 +481,6 @@ void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream) {
                               float*, int, hipStream_t);                                                                     \
   template void launchBnAct<T>(const T*, int, T*, int, int, const float*, const float*, int, const float*, const float*, int, \
                                int, int, hipStream_t);                                                                       \
-  template void launchHeadRow<T>(const HeadRowArgs<T>&, int, hipStream_t);                                                   \
   template void launchHeadSpatial<T>(const HeadSpatialArgs<T>&, hipStream_t);
 
 KGH_INSTANTIATE(float)
