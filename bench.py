@@ -22,14 +22,27 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 matrix-core peak (datasheet)
-CFG_INDEX = 2              # b18c384nbt fp16 19x19 batch 256
+CFG_INDEX = 2              # headline: b18c384nbt fp16 19x19 batch 256
 
 
 def conv_flops(layers, hw):
-    """Direct-convolution FLOPs per eval (2*k*k*Cin*Cout*HW per conv) split
-    into 3x3, 1x1 and the rest (other convs + matmuls, 2*in*out)."""
+    """Algorithmic FLOPs per eval split into 3x3 convs, 1x1 convs and the rest:
+    2*k*k*Cin*Cout*HW per conv; 2*in*out per matmul, times HW inside
+    transformer blocks (per-position projections); attention
+    2*HW*HW*(dq + dv) per head."""
     f3 = f1 = other = 0.0
+    per_position = 0  # matmul records still to come inside a transformer block
     for rec in layers:
+        if rec["op"] == 13:  # attention: i = heads, kvHeads, dq, dv
+            heads, dq, dv = int(rec["i"][0]), int(rec["i"][2]), int(rec["i"][3])
+            other += 2.0 * hw * hw * (dq + dv) * heads
+            per_position = 4
+        elif rec["op"] == 14:  # ffn: linear1, gate, linear2
+            per_position = 3 if int(rec["i"][2]) else 2
+        elif rec["op"] == 4 and per_position > 0:
+            other += 2.0 * int(rec["i"][0]) * int(rec["i"][1]) * hw
+            per_position -= 1
+            continue
         if rec["op"] == 1:
             ky, kx, ci, co = (int(v) for v in rec["i"][:4])
             f = 2.0 * ky * kx * ci * co * hw
@@ -105,6 +118,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--model-dir", default=None)
+    ap.add_argument("--config", type=int, default=CFG_INDEX,
+                    help="BASELINE.json config index; 2 (default) is the headline, 4 the transformer trunk")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (torch), to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
@@ -128,7 +143,7 @@ def main():
     import numpy as np
     from katago_amd import modelgen, nn
 
-    cfg = modelgen.configs()[CFG_INDEX]
+    cfg = modelgen.configs()[args.config]
     batch, hw = cfg.batch, 19 * 19
     model_dir = args.model_dir or os.path.join(tempfile.gettempdir(), "katago_amd_models")
     path = modelgen.ensure_model(model_dir, cfg)
@@ -140,7 +155,7 @@ def main():
     f3, f1, fother = conv_flops(dm.layers, hw)
     flops_per_eval = f3 + f1 + fother
 
-    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, batch)
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, batch, board_sizes=cfg.board_sizes)
     d_sp = nn.DeviceBuffer.from_array(sp)
     d_gl = nn.DeviceBuffer.from_array(gl)
     d_sym = nn.DeviceBuffer.from_array(np.zeros(batch, np.int32))
@@ -176,13 +191,22 @@ def main():
 
     evals = batch * args.steps
     value = evals / elapsed
-    avg3_ms = ms3 / max(n3, 1)
-    achieved3 = (fl3 / max(n3, 1)) / (avg3_ms * 1e-3) / 1e12 if n3 else 0.0
     print(f"bench: {args.steps} steps in {elapsed:.3f} s; profiled {prof_steps} eager steps: 3x3 conv {n3} launches "
           f"{ms3:.2f} ms total, 1x1 conv {n1} launches {ms1:.2f} ms total", file=sys.stderr, flush=True)
-
+    headline = args.config == CFG_INDEX
+    # Roofline kernel: the 3x3 conv for the convolutional nets, the 1x1
+    # (per-position GEMM) kernel for a transformer trunk.
+    if n3 > 0:
+        ms_k, n_k, fl_k, kname = ms3, n3, fl3, "convTapWindowKernel (3x3, fp16)"
+    else:
+        ms_k, n_k, fl_k, kname = ms1, n1, fl1, "conv1x1DmaKernel / convMfmaKernel (1x1 GEMM, fp16)"
+    avg_ms = ms_k / max(n_k, 1)
+    achieved = (fl_k / max(n_k, 1)) / (avg_ms * 1e-3) / 1e12 if n_k else 0.0
+    name = cfg.arch.name.replace("-synthetic", "")
+    boards = "x".join(str(b) for b in cfg.board_sizes)
     result = {
-        "metric": "NN evals/sec, b18c384nbt fp16 19x19 batch 256; % of fp16 MFMA peak",
+        "metric": ("NN evals/sec, b18c384nbt fp16 19x19 batch 256; % of fp16 MFMA peak" if headline else
+                   f"NN evals/sec, {name} {'fp16' if cfg.fp16 else 'fp32'} 19x19 batch {batch}"),
         "value": round(value, 2),
         "unit": "evals/s",
         "n_gpus": 1,
@@ -192,15 +216,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic (seeded random-weight b18c384nbt, seeded synthetic positions)",
-        "config": {"workload": "C2: b18c384nbt fp16 19x19, batch 256, symmetry 0, inputs resident in HBM",
+        "dtype": "fp16" if cfg.fp16 else "fp32",
+        "data": f"synthetic (seeded random-weight {name}, seeded synthetic positions)",
+        "config": {"workload": f"C{args.config}: {name} {'fp16' if cfg.fp16 else 'fp32'} boards {boards} in 19x19, batch {batch}, "
+                               f"symmetry 0, inputs resident in HBM",
                    "global_batch": batch, "board": "19x19", "parallelism": "none (1 GPU)"},
         "mfma_frac_end_to_end": round(value * flops_per_eval / (PEAK_FP16_TFLOPS * 1e12), 4),
         "gflop_per_eval": round(flops_per_eval / 1e9, 3),
-        "roofline": {"bound": "mfma", "kernel": "convTapWindowKernel (3x3, fp16)", "achieved": round(achieved3, 2),
-                     "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved3 / PEAK_FP16_TFLOPS, 4),
-                     "traffic": measured_traffic(), "avg_launch_ms": round(avg3_ms, 5), "launches": n3,
+        "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2),
+                     "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                     "traffic": measured_traffic() if headline else None, "avg_launch_ms": round(avg_ms, 5), "launches": n_k,
                      "timing": f"HIP events around each launch over {prof_steps} eager forwards after the timed steps"},
     }
     if not args.no_cpu:
