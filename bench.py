@@ -196,7 +196,7 @@ def main():
     headline = args.config == CFG_INDEX
     # Roofline kernel: the 3x3 conv for the convolutional nets, the 1x1
     # (per-position GEMM) kernel for a transformer trunk.
-    if n3 > 0:
+    if ms3 >= ms1:
         ms_k, n_k, fl_k, kname = ms3, n3, fl3, "convTapWindowKernel (3x3, fp16)"
     else:
         ms_k, n_k, fl_k, kname = ms1, n1, fl1, "conv1x1DmaKernel / convMfmaKernel (1x1 GEMM, fp16)"

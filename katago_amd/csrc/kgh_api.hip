@@ -716,12 +716,15 @@ struct Runner {
       e1.ldRaw = qkvC;
       e1.rawEnd = INT_MAX;
       conv(b.qkv, xn, C, e1);
+      const float* cosT = nullptr;
+      const float* sinT = nullptr;
       if(b.ropeIndex >= 0) {
         if(h == nullptr) throw KghError(KGH_ERR_INTERNAL, "rotary embedding needs a handle");
-        kgh::launchRope<T>(qkv, qkvC, b.heads, b.kvHeads, b.dq, h->ropeCos[b.ropeIndex], h->ropeSin[b.ropeIndex], b.learnableRope, HW,
-                           M, s);
+        cosT = h->ropeCos[b.ropeIndex];
+        sinT = h->ropeSin[b.ropeIndex];
       }
-      kgh::launchAttention<T>(qkv, qkvC, qC, qC + kC, b.heads, b.kvHeads, b.dq, b.dv, mask, HW, g.batch, att, aC, s);
+      kgh::launchAttention<T>(qkv, qkvC, qC, qC + kC, b.heads, b.kvHeads, b.dq, b.dv, mask, HW, g.batch, att, aC, cosT, sinT,
+                              b.learnableRope, s);
       ConvEpilogue<T> e2 = epi();
       e2.residual = Rd;
       e2.ldRes = C;

@@ -61,6 +61,15 @@ __device__ __forceinline__ int xcdContiguousTile() {
   return xcd * perXcd + (xcd < extra ? xcd : extra) + (blockIdx.x >> 3);
 }
 
+// Tile coordinates for a 1-D grid of rowTiles x colTiles workgroups: after
+// the XCD remap the column tiles of one row tile are consecutive, so they run
+// on the same XCD and read the row tile's A operand from that XCD's L2.
+__device__ __forceinline__ void rowColTile(int colTiles, int& rowTile, int& colTile) {
+  const int id = xcdContiguousTile();
+  rowTile = id / colTiles;
+  colTile = id - rowTile * colTiles;
+}
+
 // Epilogue shared by the matrix-core conv kernels; requires
 // convStageBytes(WM) bytes of LDS at smem and must be reached by every
 // thread of the workgroup (it contains barriers).
@@ -590,8 +599,10 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
   const int wn = wave % WN;
   const int HW = g.H * g.W;
   const int M = g.batch * HW;
-  const int m0 = xcdContiguousTile() * TW_BM;
-  const int n0 = blockIdx.y * BN;
+  int rowTile, colTile;
+  rowColTile(cout / BN, rowTile, colTile);
+  const int m0 = rowTile * TW_BM;
+  const int n0 = colTile * BN;
   const int pad = g.W + 1;
   const int laneRow = lane & 31;
   const int kq = lane >> 5;
@@ -831,8 +842,10 @@ __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* 
   const int wn = wave % WN;
   const int HW = g.H * g.W;
   const int M = g.batch * HW;
-  const int m0 = xcdContiguousTile() * TW_BM;
-  const int n0 = blockIdx.y * BN;
+  int rowTile, colTile;
+  rowColTile(cout / BN, rowTile, colTile);
+  const int m0 = rowTile * TW_BM;
+  const int n0 = colTile * BN;
   const int laneRow = lane & 31;
   const int kq = lane >> 5;
 
@@ -1012,7 +1025,7 @@ template<int BN>
 void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                      const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   int M = g.batch * g.H * g.W;
-  dim3 grid((M + TW_BM - 1) / TW_BM, cout / BN);
+  dim3 grid((M + TW_BM - 1) / TW_BM * (cout / BN));
   hipLaunchKernelGGL((convTapWindowKernel<BN, TW_ROW_WAVES>), grid, dim3(TW_ROW_WAVES * 2 * 64), 0, stream, x, cinStride, cinPad, cout,
                      w, g, epi);
   KGH_CHECK_LAUNCH();
@@ -1044,14 +1057,14 @@ template<int BN>
 void launch1x1Dma(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                   const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   int M = g.batch * g.H * g.W;
-  dim3 grid((M + TW_BM - 1) / TW_BM, cout / BN);
+  dim3 grid((M + TW_BM - 1) / TW_BM * (cout / BN));
   if(epi.glu) hipLaunchKernelGGL((conv1x1DmaKernel<BN, true>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
   else hipLaunchKernelGGL((conv1x1DmaKernel<BN, false>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
   KGH_CHECK_LAUNCH();
 }
 
-// The 1x1 DMA kernel: fp16, 32-channel steps, at least 128 of its 384-row
-// tiles, 32-bit element offsets.
+// The 1x1 DMA kernel: fp16, 32-channel steps, enough 384-row x BN tiles
+// (about 128 or more), 32-bit element offsets.
 template<typename T>
 bool dispatch1x1Dma(const T*, int, int, int, const T*, BoardGeom, const ConvEpilogue<T>&, hipStream_t) {
   return false;
@@ -1060,7 +1073,8 @@ template<>
 bool dispatch1x1Dma<half_t>(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                             const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   const long M = (long)g.batch * g.H * g.W;
-  if(cinPad % 32 != 0 || cinStride % 8 != 0 || M < 128L * TW_BM) return false;
+  // Enough workgroups (row tiles x column tiles) to fill most CUs.
+  if(cinPad % 32 != 0 || cinStride % 8 != 0 || (M + TW_BM - 1) / TW_BM * (cout / 64) < 3 * 128) return false;
   if(M * cinStride >= (1L << 31) || (long)cout * cinPad >= (1L << 31)) return false;
   if(cout % 192 == 0) launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream);
   else if(cout % 128 == 0) launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream);

@@ -70,10 +70,12 @@ void launchRmsNormSpatial(const T* x, int ldX, T* y, int ldY, int C, const float
 template<typename T>
 void launchRope(T* qkv, int ld, int H, int KV, int dq, const float* cosT, const float* sinT, bool learnable, int HW, int M,
                 hipStream_t stream);
-// Masked softmax attention per board and head; out has H * dv channels per row.
+// Masked softmax attention per board and head; out has H * dv channels per
+// row. With cosT non-null, Q and K are first rotated (in the attention
+// kernel when it takes the shape, else in place in qkv).
 template<typename T>
-void launchAttention(const T* qkv, int ld, int kOff, int vOff, int H, int KV, int dq, int dv, const float* mask, int HW, int batch,
-                     T* out, int ldOut, hipStream_t stream);
+void launchAttention(T* qkv, int ld, int kOff, int vOff, int H, int KV, int dq, int dv, const float* mask, int HW, int batch, T* out,
+                     int ldOut, const float* cosT, const float* sinT, bool learnable, hipStream_t stream);
 
 int runMfmaSelfTest();
 

@@ -26,40 +26,58 @@ __device__ __forceinline__ float waveSum(float v) {
   return v;
 }
 
-// One wave per row; each lane moves 16-byte groups of channels.
-template<typename T>
+// One wave per row; lane l holds 16-byte channel groups l, l + 64, ... (NG
+// of them) in registers across both passes, with gamma/beta loaded before
+// the reduction and the activation fixed at compile time.
+template<typename T, int NG, int ACT>
 __global__ void rmsNormRowKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ gamma,
-                                 const float* __restrict__ beta, float eps, int act, const float* __restrict__ mask, int M) {
+                                 const float* __restrict__ beta, float eps, const float* __restrict__ mask, int M) {
   constexpr int VEC = 16 / (int)sizeof(T);
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if(row >= M) return;
   const T* xr = x + (size_t)row * ldX;
   T* yr = y + (size_t)row * ldY;
-  const bool on = mask[row] != 0.0f;
-  float ss = 0.0f;
-  for(int c = lane * VEC; c < C; c += 64 * VEC) {
-    T v[VEC];
-    *(uint4*)v = *(const uint4*)(xr + c);
+  T v[NG][VEC];
+  float gm[NG][VEC], bt[NG][VEC];
 #pragma unroll
-    for(int j = 0; j < VEC; j++) {
-      float f = kgh_to_float(v[j]);
-      ss += f * f;
+  for(int i = 0; i < NG; i++) {
+    const int c = (lane + 64 * i) * VEC;
+    if(c < C) {
+      *(uint4*)v[i] = *(const uint4*)(xr + c);
+#pragma unroll
+      for(int j = 0; j < VEC; j++) {
+        gm[i][j] = gamma[c + j];
+        bt[i][j] = beta != nullptr ? beta[c + j] : 0.0f;
+      }
+    }
+    else {
+      *(uint4*)v[i] = make_uint4(0, 0, 0, 0);
     }
   }
-  ss = waveSum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)C + eps);
-  for(int c = lane * VEC; c < C; c += 64 * VEC) {
-    T v[VEC], o[VEC];
-    *(uint4*)v = *(const uint4*)(xr + c);
+  const bool on = mask[row] != 0.0f;
+  float ss = 0.0f;
+#pragma unroll
+  for(int i = 0; i < NG; i++)
 #pragma unroll
     for(int j = 0; j < VEC; j++) {
-      float f = kgh_to_float(v[j]) * inv * gamma[c + j];
-      if(beta != nullptr) f += beta[c + j];
-      f = kgh_activate(f, act);
-      o[j] = kgh_from_float<T>(on ? f : 0.0f);
+      const float f = kgh_to_float(v[i][j]);
+      ss += f * f;
     }
-    *(uint4*)(yr + c) = *(const uint4*)o;
+  ss = waveSum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+#pragma unroll
+  for(int i = 0; i < NG; i++) {
+    const int c = (lane + 64 * i) * VEC;
+    if(c < C) {
+      T o[VEC];
+#pragma unroll
+      for(int j = 0; j < VEC; j++) {
+        const float f = kgh_activate(kgh_to_float(v[i][j]) * inv * gm[i][j] + bt[i][j], ACT);
+        o[j] = kgh_from_float<T>(on ? f : 0.0f);
+      }
+      *(uint4*)(yr + c) = *(const uint4*)o;
+    }
   }
 }
 
@@ -170,10 +188,16 @@ __global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, c
 constexpr int FA_THREADS = 768;
 constexpr int FA_MAX_KEYS = 384;
 
+// With cosT non-null the rotary embedding is applied here, to K rows as they
+// are staged and to Q fragments as they are loaded (tables [table][pair][HW],
+// table = kv head when learnable, else 0): each rotated value is rounded to
+// fp16 once, exactly as when a separate pass rotates Q and K in place.
 template<int DQ, int DV>
 __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half_t* __restrict__ qkv, int ld, int kOff, int vOff, int H,
                                                                      int KV, const float* __restrict__ mask, int HW,
-                                                                     half_t* __restrict__ out, int ldOut, float scale) {
+                                                                     half_t* __restrict__ out, int ldOut, float scale,
+                                                                     const float* __restrict__ cosT, const float* __restrict__ sinT,
+                                                                     int learnable) {
   static_assert(DQ % 16 == 0 && DV % 16 == 0 && DQ <= 64 && DV <= 64, "head dims (LDS holds all keys)");
   constexpr int DVP = (DV + 31) / 32 * 32;
   constexpr int KLD = DQ + 8;             // halves per K row (16-byte pad)
@@ -190,12 +214,27 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
 
   // Stage K rows (16-byte groups), V^T (8 dims of one key per thread) and the
   // key mask; keys past HW and dims past DV are zero.
+  constexpr int PAIRS = DQ / 2;
   for(int i = tid; i < FA_MAX_KEYS * (DQ / 8); i += FA_THREADS) {
     const int key = i / (DQ / 8);
     const int g = i - key * (DQ / 8);
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if(key < HW) v = *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8);
-    *(uint4*)&Ks[key * KLD + g * 8] = v;
+    half_t v[8];
+    *(uint4*)v = make_uint4(0, 0, 0, 0);
+    if(key < HW) {
+      *(uint4*)v = *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8);
+      if(cosT != nullptr) {
+        const size_t tb = (size_t)(learnable ? kvh : 0) * PAIRS;
+#pragma unroll
+        for(int q = 0; q < 4; q++) {
+          const size_t ti = (tb + g * 4 + q) * HW + key;
+          const float c = cosT[ti], sn = sinT[ti];
+          const float x0 = (float)v[2 * q], x1 = (float)v[2 * q + 1];
+          v[2 * q] = (half_t)(x0 * c - x1 * sn);
+          v[2 * q + 1] = (half_t)(x0 * sn + x1 * c);
+        }
+      }
+    }
+    *(uint4*)&Ks[key * KLD + g * 8] = *(const uint4*)v;
   }
   for(int i = tid; i < FA_MAX_KEYS * (DVP / 8); i += FA_THREADS) {
     const int key = i / (DVP / 8);
@@ -220,7 +259,20 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
 
   half8_t qf[DQ / 16];
 #pragma unroll
-  for(int ks = 0; ks < DQ / 16; ks++) qf[ks] = *(const half8_t*)(qkv + (rowBase + qRow) * ld + h * DQ + ks * 16 + kq * 8);
+  for(int ks = 0; ks < DQ / 16; ks++) {
+    qf[ks] = *(const half8_t*)(qkv + (rowBase + qRow) * ld + h * DQ + ks * 16 + kq * 8);
+    if(cosT != nullptr) {
+      const size_t tb = (size_t)(learnable ? h * KV / H : 0) * PAIRS;
+#pragma unroll
+      for(int q = 0; q < 4; q++) {
+        const size_t ti = (tb + (ks * 16 + kq * 8) / 2 + q) * HW + qRow;
+        const float c = cosT[ti], sn = sinT[ti];
+        const float x0 = (float)qf[ks][2 * q], x1 = (float)qf[ks][2 * q + 1];
+        qf[ks][2 * q] = (half_t)(x0 * c - x1 * sn);
+        qf[ks][2 * q + 1] = (half_t)(x0 * sn + x1 * c);
+      }
+    }
+  }
 
   floatx16 o[DVP / 32];
 #pragma unroll
@@ -351,9 +403,9 @@ __global__ void attentionSimpleKernel(const T* __restrict__ qkv, int ld, int kOf
 
 template<int DQ, int DV>
 bool launchFlash(const half_t* qkv, int ld, int kOff, int vOff, int H, int KV, const float* mask, int HW, int batch, half_t* out,
-                 int ldOut, float scale, hipStream_t stream) {
+                 int ldOut, float scale, const float* cosT, const float* sinT, bool learnable, hipStream_t stream) {
   hipLaunchKernelGGL((flashAttentionKernel<DQ, DV>), dim3(batch * H), dim3(FA_THREADS), 0, stream, qkv, ld, kOff, vOff, H, KV, mask, HW,
-                     out, ldOut, scale);
+                     out, ldOut, scale, cosT, sinT, learnable ? 1 : 0);
   KGH_CHECK_LAUNCH();
   return true;
 }
@@ -362,15 +414,39 @@ bool launchFlash(const half_t* qkv, int ld, int kOff, int vOff, int H, int KV, c
 
 namespace kgh {
 
+template<typename T, int NG>
+void launchRmsNormNG(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
+                     const float* mask, int M, hipStream_t stream) {
+  const int wavesPerBlock = 4;
+  const dim3 grid((M + wavesPerBlock - 1) / wavesPerBlock), block(64 * wavesPerBlock);
+  switch(act) {
+    case KGH_ACT_IDENTITY:
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_IDENTITY>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      break;
+    case KGH_ACT_RELU:
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_RELU>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      break;
+    case KGH_ACT_MISH:
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_MISH>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      break;
+    case KGH_ACT_SILU:
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_SILU>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      break;
+    default: throw KghError(1, "RMSNorm: unsupported activation " + std::to_string(act));
+  }
+  KGH_CHECK_LAUNCH();
+}
+
 template<typename T>
 void launchRmsNorm(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
                    const float* mask, int M, hipStream_t stream) {
   constexpr int VEC = 16 / (int)sizeof(T);
   if(C % VEC != 0 || ldX % VEC != 0 || ldY % VEC != 0) throw KghError(3, "RMSNorm: channel counts must be multiples of 16 bytes");
-  const int wavesPerBlock = 4;
-  hipLaunchKernelGGL(rmsNormRowKernel<T>, dim3((M + wavesPerBlock - 1) / wavesPerBlock), dim3(64 * wavesPerBlock), 0, stream, x, ldX,
-                     y, ldY, C, gamma, beta, eps, act, mask, M);
-  KGH_CHECK_LAUNCH();
+  const int groups = (C / VEC + 63) / 64;
+  if(groups <= 1) launchRmsNormNG<T, 1>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
+  else if(groups <= 2) launchRmsNormNG<T, 2>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
+  else if(groups <= 4) launchRmsNormNG<T, 4>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
+  else throw KghError(3, "RMSNorm: more than 256 channel groups per row");
 }
 
 template<typename T>
@@ -396,8 +472,8 @@ void launchRope(T* qkv, int ld, int H, int KV, int dq, const float* cosT, const 
 }
 
 template<typename T>
-void launchAttention(const T* qkv, int ld, int kOff, int vOff, int H, int KV, int dq, int dv, const float* mask, int HW, int batch,
-                     T* out, int ldOut, hipStream_t stream) {
+void launchAttention(T* qkv, int ld, int kOff, int vOff, int H, int KV, int dq, int dv, const float* mask, int HW, int batch, T* out,
+                     int ldOut, const float* cosT, const float* sinT, bool learnable, hipStream_t stream) {
   if(H % KV != 0) throw KghError(1, "attention: numHeads must be a multiple of numKVHeads");
   if(dv > 128) throw KghError(3, "attention: value head dims above 128 are not supported");
   const float scale = 1.0f / sqrtf((float)dq);
@@ -405,12 +481,17 @@ void launchAttention(const T* qkv, int ld, int kOff, int vOff, int H, int KV, in
   if constexpr(sizeof(T) == 2) {
     const bool aligned = ld % 8 == 0 && kOff % 8 == 0 && vOff % 8 == 0 && ldOut % 4 == 0 && HW <= FA_MAX_KEYS;
     if(aligned) {
-      if(dq == 64 && dv == 64) done = launchFlash<64, 64>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, stream);
-      else if(dq == 32 && dv == 32) done = launchFlash<32, 32>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, stream);
-      else if(dq == 32 && dv == 16) done = launchFlash<32, 16>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, stream);
+      if(dq == 64 && dv == 64)
+        done = launchFlash<64, 64>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, cosT, sinT, learnable, stream);
+      else if(dq == 32 && dv == 32)
+        done = launchFlash<32, 32>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, cosT, sinT, learnable, stream);
+      else if(dq == 32 && dv == 16)
+        done = launchFlash<32, 16>(qkv, ld, kOff, vOff, H, KV, mask, HW, batch, out, ldOut, scale, cosT, sinT, learnable, stream);
     }
   }
   if(done) return;
+  // Plain path: rotate Q and K in place, then attend.
+  if(cosT != nullptr) launchRope<T>(qkv, ld, H, KV, dq, cosT, sinT, learnable, HW, batch * HW, stream);
   const long total = (long)batch * H * HW;
   hipLaunchKernelGGL(attentionSimpleKernel<T>, dim3((unsigned)((total + 127) / 128)), dim3(128), 0, stream, qkv, ld, kOff, vOff, H, KV,
                      dq, dv, mask, HW, batch, out, ldOut, scale);
@@ -427,8 +508,9 @@ template void launchRmsNormSpatial<float>(const float*, int, float*, int, int, c
                                           int, float*, hipStream_t);
 template void launchRope<half_t>(half_t*, int, int, int, int, const float*, const float*, bool, int, int, hipStream_t);
 template void launchRope<float>(float*, int, int, int, int, const float*, const float*, bool, int, int, hipStream_t);
-template void launchAttention<half_t>(const half_t*, int, int, int, int, int, int, int, const float*, int, int, half_t*, int,
-                                      hipStream_t);
-template void launchAttention<float>(const float*, int, int, int, int, int, int, int, const float*, int, int, float*, int, hipStream_t);
+template void launchAttention<half_t>(half_t*, int, int, int, int, int, int, int, const float*, int, int, half_t*, int, const float*,
+                                      const float*, bool, hipStream_t);
+template void launchAttention<float>(float*, int, int, int, int, int, int, int, const float*, int, int, float*, int, const float*,
+                                     const float*, bool, hipStream_t);
 
 }  // namespace kgh
