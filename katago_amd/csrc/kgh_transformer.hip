@@ -26,36 +26,44 @@ __device__ __forceinline__ float waveSum(float v) {
   return v;
 }
 
-// One wave per row; lane l holds 16-byte channel groups l, l + 64, ... (NG
-// of them) in registers across both passes, with gamma/beta loaded before
-// the reduction and the activation fixed at compile time.
+// Sixteen lanes per row, four rows per wave: lane l of a row holds 16-byte
+// channel groups l, l + 16, ... (NG of them) in registers across both
+// passes, with gamma/beta loaded before the reduction and the activation
+// fixed at compile time.
 template<typename T, int NG, int ACT>
 __global__ void rmsNormRowKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ gamma,
                                  const float* __restrict__ beta, float eps, const float* __restrict__ mask, int M) {
   constexpr int VEC = 16 / (int)sizeof(T);
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if(row >= M) return;
-  const T* xr = x + (size_t)row * ldX;
-  T* yr = y + (size_t)row * ldY;
+  const int sub = threadIdx.x & 15;
+  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+  const bool live = row < M;  // whole 16-lane groups share one row
+  const int r = live ? row : M - 1;
+  const T* xr = x + (size_t)r * ldX;
+  T* yr = y + (size_t)r * ldY;
+  // Wide rows (NG > 4) load gamma/beta in the second pass instead, to stay
+  // within registers.
+  constexpr bool PRELOAD = NG <= 4;
+  constexpr int NP = PRELOAD ? NG : 1;
   T v[NG][VEC];
-  float gm[NG][VEC], bt[NG][VEC];
+  float gm[NP][VEC], bt[NP][VEC];
 #pragma unroll
   for(int i = 0; i < NG; i++) {
-    const int c = (lane + 64 * i) * VEC;
+    const int c = (sub + 16 * i) * VEC;
     if(c < C) {
       *(uint4*)v[i] = *(const uint4*)(xr + c);
+      if constexpr(PRELOAD) {
 #pragma unroll
-      for(int j = 0; j < VEC; j++) {
-        gm[i][j] = gamma[c + j];
-        bt[i][j] = beta != nullptr ? beta[c + j] : 0.0f;
+        for(int j = 0; j < VEC; j++) {
+          gm[i][j] = gamma[c + j];
+          bt[i][j] = beta != nullptr ? beta[c + j] : 0.0f;
+        }
       }
     }
     else {
       *(uint4*)v[i] = make_uint4(0, 0, 0, 0);
     }
   }
-  const bool on = mask[row] != 0.0f;
+  const bool on = mask[r] != 0.0f;
   float ss = 0.0f;
 #pragma unroll
   for(int i = 0; i < NG; i++)
@@ -64,16 +72,20 @@ __global__ void rmsNormRowKernel(const T* __restrict__ x, int ldX, T* __restrict
       const float f = kgh_to_float(v[i][j]);
       ss += f * f;
     }
-  ss = waveSum(ss);
+#pragma unroll
+  for(int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
   const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+  if(!live) return;
 #pragma unroll
   for(int i = 0; i < NG; i++) {
-    const int c = (lane + 64 * i) * VEC;
+    const int c = (sub + 16 * i) * VEC;
     if(c < C) {
       T o[VEC];
 #pragma unroll
       for(int j = 0; j < VEC; j++) {
-        const float f = kgh_activate(kgh_to_float(v[i][j]) * inv * gm[i][j] + bt[i][j], ACT);
+        const float g = PRELOAD ? gm[PRELOAD ? i : 0][j] : gamma[c + j];
+        const float b = PRELOAD ? bt[PRELOAD ? i : 0][j] : (beta != nullptr ? beta[c + j] : 0.0f);
+        const float f = kgh_activate(kgh_to_float(v[i][j]) * inv * g + b, ACT);
         o[j] = kgh_from_float<T>(on ? f : 0.0f);
       }
       *(uint4*)(yr + c) = *(const uint4*)o;
@@ -417,8 +429,8 @@ namespace kgh {
 template<typename T, int NG>
 void launchRmsNormNG(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
                      const float* mask, int M, hipStream_t stream) {
-  const int wavesPerBlock = 4;
-  const dim3 grid((M + wavesPerBlock - 1) / wavesPerBlock), block(64 * wavesPerBlock);
+  const int rowsPerBlock = 16;  // 256 threads, 16 lanes per row
+  const dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock), block(256);
   switch(act) {
     case KGH_ACT_IDENTITY:
       hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_IDENTITY>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
@@ -442,11 +454,13 @@ void launchRmsNorm(const T* x, int ldX, T* y, int ldY, int C, const float* gamma
                    const float* mask, int M, hipStream_t stream) {
   constexpr int VEC = 16 / (int)sizeof(T);
   if(C % VEC != 0 || ldX % VEC != 0 || ldY % VEC != 0) throw KghError(3, "RMSNorm: channel counts must be multiples of 16 bytes");
-  const int groups = (C / VEC + 63) / 64;
+  const int groups = (C / VEC + 15) / 16;  // 16-byte groups per lane
   if(groups <= 1) launchRmsNormNG<T, 1>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
   else if(groups <= 2) launchRmsNormNG<T, 2>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
+  else if(groups <= 3) launchRmsNormNG<T, 3>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
   else if(groups <= 4) launchRmsNormNG<T, 4>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
-  else throw KghError(3, "RMSNorm: more than 256 channel groups per row");
+  else if(groups <= 8) launchRmsNormNG<T, 8>(x, ldX, y, ldY, C, gamma, beta, eps, act, mask, M, stream);
+  else throw KghError(3, "RMSNorm: more than 128 channel groups per row");
 }
 
 template<typename T>

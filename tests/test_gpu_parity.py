@@ -3,8 +3,9 @@
 Tolerances: the reference's layer-test tolerances for the layer KATs
 (testnn.cpp:8-15); for whole networks, on raw outputs times
 outputScaleMultiplier: policy max-abs <= 1e-3 (fp32) / 2e-2 (fp16) with an
-identical argmax over on-board points and pass, value and score <= 1e-3
-(fp32) / 1e-2 (fp16), ownership as policy.
+identical argmax over on-board points and pass (where the oracle's top two
+moves are further apart than that tolerance; closer, the device may pick
+either), value and score <= 1e-3 (fp32) / 1e-2 (fp16), ownership as policy.
 """
 import numpy as np
 import pytest
@@ -103,7 +104,11 @@ def _compare(gpu, ora, fp16, scale, board_sizes, n, label):
         legal[hw] = True
         a = np.where(legal, gp[i], -np.inf).argmax()
         b = np.where(legal, ora["policy"][i], -np.inf).argmax()
-        assert a == b, f"{label} row {i} argmax {a} != {b}"
+        # Identical argmax, unless the oracle's own top moves lie closer
+        # together than the policy tolerance (a tie at this precision): then
+        # the device's pick must be one of the oracle's tied moves.
+        gap = ora["policy"][i][b] - ora["policy"][i][a]
+        assert a == b or gap <= tol["policy"], f"{label} row {i} argmax {a} != {b} (oracle gap {gap})"
 
 
 def _run_parity(path, fp16, n, board_sizes=(19,), symmetries=None, seed=5, label=""):
