@@ -111,6 +111,27 @@ def cpu_baseline(path, seconds_target=15.0):
                       f"{iters} forwards x batch 8 = {done[0]} evals in {wall:.1f} s"}
 
 
+def serve_rate(lm, cfg, batch, server_threads=2, rounds=40):
+    """Evals/s with rows coming from host memory through the batching
+    evaluator (NNEvaluator's serve loop): 2*batch native client threads keep
+    both server threads' batches full; each batch is packed into pinned
+    memory, copied to the device, run, copied back and unpacked. Not the
+    headline value, which has inputs resident in HBM."""
+    from katago_amd import modelgen, nn
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, batch, board_sizes=cfg.board_sizes)
+    ev = nn.Evaluator(lm, max_batch=batch, use_fp16=cfg.fp16, num_server_threads=server_threads)
+    clients = server_threads * batch
+    ev.run_clients(sp, gl, num_clients=clients, evals_per_client=2)  # warm up (graph capture per handle)
+    ev.clear_stats()
+    secs, _ = ev.run_clients(sp, gl, num_clients=clients, evals_per_client=rounds)
+    rows, batches = ev.stats()
+    ev.close()
+    print(f"bench: serve {rows} rows in {batches} batches, {secs:.3f} s", file=sys.stderr, flush=True)
+    return {"value": round(rows / secs, 2), "unit": "evals/s", "server_threads": server_threads, "clients": clients,
+            "avg_batch": round(rows / max(batches, 1), 1),
+            "path": "featurized rows in host memory -> NNEvaluator batching -> pinned staging -> H2D -> forward -> D2H -> rows"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +141,8 @@ def main():
     ap.add_argument("--model-dir", default=None)
     ap.add_argument("--config", type=int, default=CFG_INDEX,
                     help="BASELINE.json config index; 2 (default) is the headline, 4 the transformer trunk")
+    ap.add_argument("--no-serve", action="store_true",
+                    help="skip the PCIe-inclusive measurement through the batching evaluator")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (torch), to scale rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
@@ -228,6 +251,8 @@ def main():
                      "traffic": measured_traffic() if headline else None, "avg_launch_ms": round(avg_ms, 5), "launches": n_k,
                      "timing": f"HIP events around each launch over {prof_steps} eager forwards after the timed steps"},
     }
+    if not args.no_serve:
+        result["pcie_inclusive"] = serve_rate(lm, cfg, batch)
     if not args.no_cpu:
         print("bench: timing CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(path)

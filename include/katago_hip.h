@@ -123,6 +123,19 @@ int kgh_handle_free(kgh_handle* handle);
 int kgh_forward(kgh_handle* handle, int32_t n, const float* spatial, const float* global_in,
                 const int32_t* symmetry, const float* policy_optimism, float* out);
 
+/* The handle's pinned host staging buffers, laid out as kgh_forward's
+ * arguments for max_batch rows (spatial NHWC, global, symmetry, policy
+ * optimism, packed outputs); valid until kgh_handle_free. With
+ * kgh_forward_staged a caller builds its batch in place and reads the outputs
+ * in place, saving the two host copies kgh_forward makes. No counterpart in
+ * the reference: the HIP backend's NeuralNet::getOutput (nninterface.h:114-122)
+ * uses it to pack rows straight into DMA-able memory. */
+int kgh_handle_staging(kgh_handle* handle, float** spatial, float** global_in, int32_t** symmetry,
+                       float** policy_optimism, float** out);
+/* kgh_forward on the first n rows already in the staging buffers; the outputs
+ * land in the staging output buffer. Synchronous. */
+int kgh_forward_staged(kgh_handle* handle, int32_t n);
+
 /* Device-memory forward on the handle's stream: every pointer is a device
  * pointer with the same layout as kgh_forward. Asynchronous; call
  * kgh_handle_synchronize before reading out. */

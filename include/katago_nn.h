@@ -68,6 +68,37 @@ int32_t kgn_test_evaluate(int32_t kind, const char* desc_text, int32_t batch, in
                           int32_t use_nhwc, const float* input, const float* mask, float* output, int64_t output_len,
                           char* err, int32_t errlen);
 
+/* NNEvaluator's batching server loop (nneval.cpp:342-420, 549-750) over this
+ * backend: num_server_threads threads on device gpu, each with its own
+ * compute handle (stream) and batches of up to max_batch queued rows;
+ * debug_skip_nn answers from the rows themselves without a device
+ * (debugSkipNeuralNet). The threads are running on return. */
+void* kgn_evaluator_create(void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t max_batch, int32_t use_fp16,
+                           int32_t num_server_threads, int32_t gpu, int32_t debug_skip_nn, char* err, int32_t errlen);
+void kgn_evaluator_free(void* evaluator);
+
+/* One featurized row through the evaluator (NNEvaluator::evaluate after
+ * fillRowBufs, nneval.cpp:906-926): blocks until a server thread has run it in
+ * some batch. Thread-safe. Outputs are raw, as kgn_get_output writes them for
+ * one row; ownership may be NULL (no owner map requested). */
+int32_t kgn_evaluator_evaluate(void* evaluator, const float* spatial, int32_t spatial_len, const float* global_in,
+                               int32_t global_len, int32_t board_x, int32_t board_y, int32_t symmetry, float policy_optimism,
+                               float* policy, float* value, float* score, float* ownership, char* err, int32_t errlen);
+
+/* numRowsProcessed / numBatchesProcessed (nneval.h:193-197) and clearStats. */
+void kgn_evaluator_stats(void* evaluator, uint64_t* rows, uint64_t* batches);
+void kgn_evaluator_clear_stats(void* evaluator);
+
+/* Serving benchmark driver: num_clients native threads, standing in for
+ * search threads, each evaluate evals_per_client rows (row (c + k*num_clients)
+ * mod num_rows of the given featurized rows) through the evaluator; *seconds
+ * is the wall time. If policy_out is not NULL, client c < num_rows writes the
+ * raw policy of its first evaluation (row c) at policy_out + c*(nn_x*nn_y+1). */
+int32_t kgn_evaluator_run_clients(void* evaluator, int32_t num_clients, int32_t evals_per_client, int32_t num_rows,
+                                  const float* spatial_rows, int32_t spatial_len, const float* global_rows, int32_t global_len,
+                                  int32_t board_x, int32_t board_y, float* policy_out, double* seconds, char* err,
+                                  int32_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ HOST_SOURCES = [
     "host/neuralnet/desc.cpp",
     "host/neuralnet/nninputs.cpp",
     "host/neuralnet/hipbackend.cpp",
+    "host/neuralnet/nneval.cpp",
     "host/neuralnet/capi.cpp",
 ]
 ORACLE_SOURCES = [

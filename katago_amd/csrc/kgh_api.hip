@@ -1276,33 +1276,64 @@ int kgh_forward_device(kgh_handle* handle, int32_t n, const float* d_spatial, co
   });
 }
 
+namespace {
+// The rows already in the handle's pinned staging buffers: H2D, forward, D2H
+// into the staging output, all on the handle's stream, then wait.
+void forwardStaged(kgh_handle* handle, int n) {
+  if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
+  for(int i = 0; i < n; i++)
+    if(handle->hSym[i] < 0 || handle->hSym[i] > 7) invalid("symmetry must be in 0..7");
+  KGH_HIP_CHECK(hipSetDevice(handle->model->device));
+  const Net& net = handle->model->net;
+  const size_t HW = (size_t)handle->H * handle->W;
+  const size_t spatialBytes = (size_t)n * HW * net.inputC * sizeof(float);
+  const size_t globalBytes = (size_t)n * net.globalC * sizeof(float);
+  hipStream_t s = handle->stream;
+  KGH_HIP_CHECK(hipMemcpyAsync(handle->dSpatial, handle->hSpatial, spatialBytes, hipMemcpyHostToDevice, s));
+  KGH_HIP_CHECK(hipMemcpyAsync(handle->dGlobal, handle->hGlobal, globalBytes, hipMemcpyHostToDevice, s));
+  KGH_HIP_CHECK(hipMemcpyAsync(handle->dSym, handle->hSym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+  KGH_HIP_CHECK(hipMemcpyAsync(handle->dOpt, handle->hOpt, (size_t)n * sizeof(float), hipMemcpyHostToDevice, s));
+  runForward(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
+  const size_t outBytes = (size_t)n * handle->rowFloats * sizeof(float);
+  KGH_HIP_CHECK(hipMemcpyAsync(handle->hOut, handle->dOut, outBytes, hipMemcpyDeviceToHost, s));
+  KGH_HIP_CHECK(hipStreamSynchronize(s));
+}
+}  // namespace
+
 int kgh_forward(kgh_handle* handle, int32_t n, const float* spatial, const float* global_in, const int32_t* symmetry,
                 const float* policy_optimism, float* out) {
   return guarded([&] {
     requireHandle(handle);
     if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
     if(!spatial || !global_in || !symmetry || !policy_optimism || !out) invalid("null host pointer");
-    for(int i = 0; i < n; i++)
-      if(symmetry[i] < 0 || symmetry[i] > 7) invalid("symmetry must be in 0..7");
-    KGH_HIP_CHECK(hipSetDevice(handle->model->device));
     const Net& net = handle->model->net;
     const size_t HW = (size_t)handle->H * handle->W;
-    const size_t spatialBytes = (size_t)n * HW * net.inputC * sizeof(float);
-    const size_t globalBytes = (size_t)n * net.globalC * sizeof(float);
-    memcpy(handle->hSpatial, spatial, spatialBytes);
-    memcpy(handle->hGlobal, global_in, globalBytes);
+    memcpy(handle->hSpatial, spatial, (size_t)n * HW * net.inputC * sizeof(float));
+    memcpy(handle->hGlobal, global_in, (size_t)n * net.globalC * sizeof(float));
     memcpy(handle->hSym, symmetry, (size_t)n * sizeof(int));
     memcpy(handle->hOpt, policy_optimism, (size_t)n * sizeof(float));
-    hipStream_t s = handle->stream;
-    KGH_HIP_CHECK(hipMemcpyAsync(handle->dSpatial, handle->hSpatial, spatialBytes, hipMemcpyHostToDevice, s));
-    KGH_HIP_CHECK(hipMemcpyAsync(handle->dGlobal, handle->hGlobal, globalBytes, hipMemcpyHostToDevice, s));
-    KGH_HIP_CHECK(hipMemcpyAsync(handle->dSym, handle->hSym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
-    KGH_HIP_CHECK(hipMemcpyAsync(handle->dOpt, handle->hOpt, (size_t)n * sizeof(float), hipMemcpyHostToDevice, s));
-    runForward(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
-    const size_t outBytes = (size_t)n * handle->rowFloats * sizeof(float);
-    KGH_HIP_CHECK(hipMemcpyAsync(handle->hOut, handle->dOut, outBytes, hipMemcpyDeviceToHost, s));
-    KGH_HIP_CHECK(hipStreamSynchronize(s));
-    memcpy(out, handle->hOut, outBytes);
+    forwardStaged(handle, n);
+    memcpy(out, handle->hOut, (size_t)n * handle->rowFloats * sizeof(float));
+  });
+}
+
+int kgh_handle_staging(kgh_handle* handle, float** spatial, float** global_in, int32_t** symmetry, float** policy_optimism,
+                       float** out) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(!spatial || !global_in || !symmetry || !policy_optimism || !out) invalid("null pointer");
+    *spatial = handle->hSpatial;
+    *global_in = handle->hGlobal;
+    *symmetry = handle->hSym;
+    *policy_optimism = handle->hOpt;
+    *out = handle->hOut;
+  });
+}
+
+int kgh_forward_staged(kgh_handle* handle, int32_t n) {
+  return guarded([&] {
+    requireHandle(handle);
+    forwardStaged(handle, n);
   });
 }
 

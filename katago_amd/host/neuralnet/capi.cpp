@@ -1,6 +1,8 @@
 // C shim over NeuralNet::* (include/katago_nn.h) for non-C++ callers.
+#include <chrono>
 #include <cstring>
 #include <memory>
+#include <thread>
 
 #include "../neuralnet/nneval.h"
 #include "../neuralnet/nninterface.h"
@@ -206,6 +208,122 @@ int32_t kgn_test_evaluate(int32_t kind, const char* desc_text, int32_t batch, in
     }
     memcpy(output, out.data(), out.size() * sizeof(float));
     return 1;
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// NNEvaluator (the batching server loop) for callers without C++.
+
+void* kgn_evaluator_create(void* m, int32_t nn_x, int32_t nn_y, int32_t max_batch, int32_t use_fp16, int32_t num_server_threads,
+                           int32_t gpu, int32_t debug_skip_nn, char* err, int32_t errlen) {
+  try {
+    if(num_server_threads <= 0) throw StringError("num_server_threads must be positive");
+    enabled_t mode = use_fp16 == 0 ? enabled_t::False : use_fp16 == 1 ? enabled_t::True : enabled_t::Auto;
+    std::unique_ptr<NNEvaluator> ev(new NNEvaluator((const LoadedModel*)m, nullptr, max_batch, nn_x, nn_y, false, true,
+                                                    debug_skip_nn != 0, mode, vector<int>(num_server_threads, gpu), 0));
+    ev->spawnServerThreads();
+    return ev.release();
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return nullptr;
+  }
+}
+
+void kgn_evaluator_free(void* ev) { delete (NNEvaluator*)ev; }
+
+namespace {
+void copyRowOutput(const NNOutput& o, int HW, float* policy, float* value, float* score, float* ownership) {
+  if(policy != nullptr) memcpy(policy, o.policyProbs, (size_t)(HW + 1) * sizeof(float));
+  if(value != nullptr) {
+    value[0] = o.whiteWinProb;
+    value[1] = o.whiteLossProb;
+    value[2] = o.whiteNoResultProb;
+  }
+  if(score != nullptr) {
+    score[0] = o.whiteScoreMean;
+    score[1] = o.whiteScoreMeanSq;
+    score[2] = o.whiteLead;
+    score[3] = o.varTimeLeft;
+    score[4] = o.shorttermWinlossError;
+    score[5] = o.shorttermScoreError;
+  }
+  if(ownership != nullptr && o.whiteOwnerMap != nullptr) memcpy(ownership, o.whiteOwnerMap, (size_t)HW * sizeof(float));
+}
+}  // namespace
+
+int32_t kgn_evaluator_evaluate(void* evp, const float* spatial, int32_t spatial_len, const float* global_in, int32_t global_len,
+                               int32_t board_x, int32_t board_y, int32_t symmetry, float policy_optimism, float* policy,
+                               float* value, float* score, float* ownership, char* err, int32_t errlen) {
+  try {
+    NNEvaluator* ev = (NNEvaluator*)evp;
+    NNResultBuf buf;
+    buf.rowSpatialBuf.assign(spatial, spatial + spatial_len);
+    buf.rowGlobalBuf.assign(global_in, global_in + global_len);
+    buf.boardXSizeForServer = board_x;
+    buf.boardYSizeForServer = board_y;
+    buf.symmetry = symmetry;
+    buf.policyOptimism = policy_optimism;
+    buf.includeOwnerMap = ownership != nullptr;
+    ev->evaluateRow(buf);
+    copyRowOutput(*buf.result, ev->getNNXLen() * ev->getNNYLen(), policy, value, score, ownership);
+    return 0;
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return -1;
+  }
+}
+
+void kgn_evaluator_stats(void* ev, uint64_t* rows, uint64_t* batches) {
+  if(rows != nullptr) *rows = ((NNEvaluator*)ev)->numRowsProcessed();
+  if(batches != nullptr) *batches = ((NNEvaluator*)ev)->numBatchesProcessed();
+}
+
+void kgn_evaluator_clear_stats(void* ev) { ((NNEvaluator*)ev)->clearStats(); }
+
+int32_t kgn_evaluator_run_clients(void* evp, int32_t num_clients, int32_t evals_per_client, int32_t num_rows, const float* spatial_rows,
+                                  int32_t spatial_len, const float* global_rows, int32_t global_len, int32_t board_x, int32_t board_y,
+                                  float* policy_out, double* seconds, char* err, int32_t errlen) {
+  try {
+    NNEvaluator* ev = (NNEvaluator*)evp;
+    if(num_clients <= 0 || evals_per_client <= 0 || num_rows <= 0) throw StringError("counts must be positive");
+    const int HW = ev->getNNXLen() * ev->getNNYLen();
+    vector<std::string> errors(num_clients);
+    auto client = [&](int c) {
+      try {
+        NNResultBuf buf;
+        buf.boardXSizeForServer = board_x;
+        buf.boardYSizeForServer = board_y;
+        for(int k = 0; k < evals_per_client; k++) {
+          const int r = (c + k * num_clients) % num_rows;
+          // The row as a search thread's featurization would leave it.
+          buf.rowSpatialBuf.assign(spatial_rows + (size_t)spatial_len * r, spatial_rows + (size_t)spatial_len * (r + 1));
+          buf.rowGlobalBuf.assign(global_rows + (size_t)global_len * r, global_rows + (size_t)global_len * (r + 1));
+          buf.symmetry = 0;
+          buf.policyOptimism = 0.0;
+          ev->evaluateRow(buf);
+          if(policy_out != nullptr && k == 0 && c < num_rows)
+            memcpy(policy_out + (size_t)(HW + 1) * c, buf.result->policyProbs, (size_t)(HW + 1) * sizeof(float));
+        }
+      }
+      catch(const std::exception& e) {
+        errors[c] = e.what();
+      }
+    };
+    const auto t0 = std::chrono::steady_clock::now();
+    vector<std::thread> threads;
+    for(int c = 0; c < num_clients; c++) threads.emplace_back(client, c);
+    for(std::thread& t: threads) t.join();
+    const auto t1 = std::chrono::steady_clock::now();
+    if(seconds != nullptr) *seconds = std::chrono::duration<double>(t1 - t0).count();
+    for(const std::string& e: errors)
+      if(!e.empty()) throw StringError(e);
+    return 0;
   }
   catch(const std::exception& e) {
     setErr(err, errlen, e.what());

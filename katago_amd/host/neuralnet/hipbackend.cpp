@@ -313,6 +313,13 @@ struct ComputeHandle {
   int maxBatchSize = 0;
   kgh_model* model = nullptr;
   kgh_handle* handle = nullptr;
+  // The device library's pinned staging buffers of this handle: rows are
+  // packed straight into them and outputs read from them.
+  float* stSpatial = nullptr;
+  float* stGlobal = nullptr;
+  int32_t* stSymmetry = nullptr;
+  float* stOptimism = nullptr;
+  float* stOutput = nullptr;
   ~ComputeHandle() {
     if(handle != nullptr) kgh_handle_free(handle);
     if(context != nullptr && model != nullptr) {
@@ -326,17 +333,13 @@ struct ComputeHandle {
   }
 };
 
+// Row sizes of one server thread's batches; the batch itself is assembled in
+// the compute handle's pinned staging buffers.
 struct InputBuffers {
   int maxBatchSize;
   size_t singleInputElts;
   size_t singleInputGlobalElts;
   size_t singleOutputElts;
-  vector<float> spatial;  // NHWC batch
-  vector<float> global;
-  vector<int32_t> symmetry;
-  vector<float> optimism;
-  vector<float> output;
-  vector<float> scratch;
 };
 
 // ---------------------------------------------------------------------------
@@ -408,6 +411,8 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
   }
   checkKgh(kgh_handle_create(h->model, maxBatchSize, context->nnXLen, context->nnYLen, requireExactNNLen ? 1 : 0, &h->handle),
            "kgh_handle_create");
+  checkKgh(kgh_handle_staging(h->handle, &h->stSpatial, &h->stGlobal, &h->stSymmetry, &h->stOptimism, &h->stOutput),
+           "kgh_handle_staging");
 
   if(logger != nullptr) {
     char buf[512] = {0};
@@ -438,12 +443,6 @@ InputBuffers* NeuralNet::createInputBuffers(const LoadedModel* loadedModel, int 
   b->singleInputElts = (size_t)m.numInputChannels * nnXLen * nnYLen;
   b->singleInputGlobalElts = (size_t)m.numInputGlobalChannels;
   b->singleOutputElts = (size_t)kgh_output_row_floats(nnXLen, nnYLen, m.numScoreValueChannels);
-  b->spatial.resize(b->singleInputElts * maxBatchSize);
-  b->global.resize(b->singleInputGlobalElts * maxBatchSize);
-  b->symmetry.resize(maxBatchSize);
-  b->optimism.resize(maxBatchSize);
-  b->output.resize(b->singleOutputElts * maxBatchSize);
-  b->scratch.resize(b->singleInputElts);
   return b;
 }
 
@@ -459,25 +458,28 @@ void NeuralNet::getOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFil
   const int nnY = h->context->nnYLen;
   const int HW = nnX * nnY;
 
+  if(b->singleInputElts != (size_t)h->numSpatial * HW || b->singleInputGlobalElts != (size_t)h->numGlobal)
+    throw StringError("HIP backend: input buffers were created for another board size or model");
+  // Rows go straight into the handle's pinned staging memory (one host copy),
+  // from which the forward's H2D copy reads.
   for(int i = 0; i < n; i++) {
     const NNResultBuf& row = *inputBufs[i];
     if(row.rowSpatialBuf.size() < b->singleInputElts || row.rowGlobalBuf.size() < b->singleInputGlobalElts)
       throw StringError("HIP backend: row input buffers too small");
     if(row.hasRowMeta) throw StringError("HIP backend: row metadata given for a model without a metadata encoder");
-    float* dst = b->spatial.data() + b->singleInputElts * i;
+    float* dst = h->stSpatial + b->singleInputElts * i;
     if(h->inputsUseNHWC) memcpy(dst, row.rowSpatialBuf.data(), b->singleInputElts * sizeof(float));
     else nchwToNhwc(row.rowSpatialBuf.data(), dst, 1, h->numSpatial, nnY, nnX);
-    memcpy(b->global.data() + b->singleInputGlobalElts * i, row.rowGlobalBuf.data(), b->singleInputGlobalElts * sizeof(float));
-    b->symmetry[i] = row.symmetry;
-    b->optimism[i] = (float)row.policyOptimism;
+    memcpy(h->stGlobal + b->singleInputGlobalElts * i, row.rowGlobalBuf.data(), b->singleInputGlobalElts * sizeof(float));
+    h->stSymmetry[i] = row.symmetry;
+    h->stOptimism[i] = (float)row.policyOptimism;
   }
-  checkKgh(kgh_forward(h->handle, n, b->spatial.data(), b->global.data(), b->symmetry.data(), b->optimism.data(), b->output.data()),
-           "kgh_forward");
+  checkKgh(kgh_forward_staged(h->handle, n), "kgh_forward_staged");
 
   for(int i = 0; i < n; i++) {
     NNOutput* out = outputs[i];
     if(out->nnXLen != nnX || out->nnYLen != nnY) throw StringError("HIP backend: NNOutput board size mismatch");
-    const float* r = b->output.data() + b->singleOutputElts * i;
+    const float* r = h->stOutput + b->singleOutputElts * i;
     memcpy(out->policyProbs, r, (size_t)(HW + 1) * sizeof(float));
     out->whiteWinProb = r[HW + 1];
     out->whiteLossProb = r[HW + 2];

@@ -19,6 +19,7 @@ namespace NNPos {
 }
 
 namespace NNInputs {
+  constexpr int SYMMETRY_NOTSPECIFIED = -1;
   constexpr int NUM_FEATURES_SPATIAL_V7 = 22;
   constexpr int NUM_FEATURES_GLOBAL_V7 = 19;
 }

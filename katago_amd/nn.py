@@ -81,6 +81,16 @@ def host_library() -> ctypes.CDLL:
             c.c_char_p, c.c_int32]
         lib.kgn_test_evaluate.argtypes = [c.c_int32, c.c_char_p, c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_int32,
                                           c.c_void_p, c.c_void_p, c.c_void_p, c.c_int64, c.c_char_p, c.c_int32]
+        lib.kgn_evaluator_create.restype = c.c_void_p
+        lib.kgn_evaluator_create.argtypes = [c.c_void_p] + [c.c_int32] * 7 + [c.c_char_p, c.c_int32]
+        lib.kgn_evaluator_free.argtypes = [c.c_void_p]
+        lib.kgn_evaluator_evaluate.argtypes = [c.c_void_p, c.c_void_p, c.c_int32, c.c_void_p, c.c_int32, c.c_int32, c.c_int32,
+                                               c.c_int32, c.c_float] + [c.c_void_p] * 4 + [c.c_char_p, c.c_int32]
+        lib.kgn_evaluator_stats.argtypes = [c.c_void_p, c.POINTER(c.c_uint64), c.POINTER(c.c_uint64)]
+        lib.kgn_evaluator_clear_stats.argtypes = [c.c_void_p]
+        lib.kgn_evaluator_run_clients.argtypes = [c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_void_p, c.c_int32,
+                                                  c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_void_p,
+                                                  c.POINTER(c.c_double), c.c_char_p, c.c_int32]
         _host = lib
     return _host
 
@@ -200,6 +210,84 @@ class ComputeHandle:
     def close(self):
         if getattr(self, "_ptr", None):
             host_library().kgn_free_handle(self._ptr)
+            self._ptr = None
+
+    def __del__(self):
+        self.close()
+
+
+class Evaluator:
+    """NNEvaluator's batching server loop (nneval.cpp:549-739) over this
+    backend: server threads with one compute handle each, batches of whatever
+    rows are queued up to max_batch. evaluate() is thread-safe and blocks.
+    With model=None and debug_skip_nn the threads answer without a device."""
+
+    def __init__(self, model, nn_x: int = 19, nn_y: int = 19, max_batch: int = 256, use_fp16=True,
+                 num_server_threads: int = 1, gpu: int = 0, debug_skip_nn: bool = False):
+        lib = host_library()
+        err = _errbuf()
+        self.model = model
+        self.nn_x, self.nn_y = nn_x, nn_y
+        fp16 = 2 if use_fp16 is None else int(bool(use_fp16))
+        self._ptr = lib.kgn_evaluator_create(model._ptr if model is not None else None, nn_x, nn_y, max_batch, fp16,
+                                             num_server_threads, gpu, int(debug_skip_nn), err, len(err))
+        if not self._ptr:
+            _raise(err)
+
+    def evaluate(self, spatial, global_in, board_x: int = None, board_y: int = None, symmetry: int = 0,
+                 policy_optimism: float = 0.0, include_owner_map: bool = True):
+        """One featurized row (NHWC spatial, globals) -> raw outputs dict."""
+        lib = host_library()
+        hw = self.nn_x * self.nn_y
+        spatial = np.ascontiguousarray(spatial, dtype=np.float32).reshape(-1)
+        global_in = np.ascontiguousarray(global_in, dtype=np.float32).reshape(-1)
+        policy = np.zeros(hw + 1, np.float32)
+        value = np.zeros(3, np.float32)
+        score = np.zeros(6, np.float32)
+        own = np.zeros(hw, np.float32) if include_owner_map else None
+        err = _errbuf()
+        rc = lib.kgn_evaluator_evaluate(self._ptr, spatial.ctypes.data, spatial.size, global_in.ctypes.data, global_in.size,
+                                        board_x or self.nn_x, board_y or self.nn_y, symmetry, policy_optimism,
+                                        policy.ctypes.data, value.ctypes.data, score.ctypes.data,
+                                        own.ctypes.data if own is not None else None, err, len(err))
+        if rc != 0:
+            _raise(err)
+        return {"policy": policy, "value": value, "score": score, "ownership": own}
+
+    def stats(self):
+        rows, batches = ctypes.c_uint64(0), ctypes.c_uint64(0)
+        host_library().kgn_evaluator_stats(self._ptr, ctypes.byref(rows), ctypes.byref(batches))
+        return rows.value, batches.value
+
+    def clear_stats(self):
+        host_library().kgn_evaluator_clear_stats(self._ptr)
+
+    def run_clients(self, spatial_rows, global_rows, num_clients: int, evals_per_client: int, board_x: int = None,
+                    board_y: int = None, want_policy: bool = False):
+        """Native client threads evaluating rows in a loop; returns (seconds,
+        policy of each client's first row or None)."""
+        lib = host_library()
+        spatial_rows = np.ascontiguousarray(spatial_rows, dtype=np.float32)
+        global_rows = np.ascontiguousarray(global_rows, dtype=np.float32)
+        n = global_rows.shape[0]
+        spatial_rows = spatial_rows.reshape(n, -1)
+        global_rows = global_rows.reshape(n, -1)
+        hw = self.nn_x * self.nn_y
+        policy = np.zeros((min(num_clients, n), hw + 1), np.float32) if want_policy else None
+        secs = ctypes.c_double(0.0)
+        err = _errbuf()
+        rc = lib.kgn_evaluator_run_clients(self._ptr, num_clients, evals_per_client, n, spatial_rows.ctypes.data,
+                                           spatial_rows.shape[1], global_rows.ctypes.data, global_rows.shape[1],
+                                           board_x or self.nn_x, board_y or self.nn_y,
+                                           policy.ctypes.data if policy is not None else None, ctypes.byref(secs), err,
+                                           len(err))
+        if rc != 0:
+            _raise(err)
+        return secs.value, policy
+
+    def close(self):
+        if getattr(self, "_ptr", None):
+            host_library().kgn_evaluator_free(self._ptr)
             self._ptr = None
 
     def __del__(self):
