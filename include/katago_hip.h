@@ -136,6 +136,51 @@ int kgh_handle_staging(kgh_handle* handle, float** spatial, float** global_in, i
  * land in the staging output buffer. Synchronous. */
 int kgh_forward_staged(kgh_handle* handle, int32_t n);
 
+/* Post-processing on the device of what NNEvaluator::evaluate does on the
+ * host after getOutput (nneval.cpp:946-1240): policy softmax over legal moves
+ * with the policy temperature (illegal entries -1) and the optional pass cap,
+ * win/loss/noResult softmax, score, lead and error transforms, ownership tanh,
+ * all from the white player's perspective. Needs model version >= 4. The
+ * multipliers are ModelPostProcessParams (desc.h:468-481). No counterpart in
+ * the reference's backend interface: the row's legal moves, side to move and
+ * rules are inputs the evaluator holds. */
+typedef struct kgh_post_params {
+  float output_scale_multiplier;
+  double score_mean_multiplier;
+  double score_stdev_multiplier;
+  double lead_multiplier;
+  double variance_time_multiplier;
+  double shortterm_value_error_multiplier;
+  double shortterm_score_error_multiplier;
+} kgh_post_params;
+
+/* Per-row info word: flags | board_x << 8 | board_y << 16. */
+#define KGH_POST_ENABLED 1
+#define KGH_POST_WHITE_TO_MOVE 2
+#define KGH_POST_NO_RESULT_DISABLED 4 /* koRule != KO_SIMPLE && scoringRule != SCORING_TERRITORY */
+#define KGH_POST_PASSING_HACKS 8
+
+/* Post-processed row: policy[nn_x*nn_y + 1] (probabilities, -1 illegal),
+ * whiteWinProb, whiteLossProb, whiteNoResultProb, whiteScoreMean,
+ * whiteScoreMeanSq, whiteLead, varTimeLeft, shorttermWinlossError,
+ * shorttermScoreError, whiteOwnerMap[nn_x*nn_y]. */
+int32_t kgh_post_row_floats(int32_t nn_x, int32_t nn_y);
+
+/* Pinned staging for kgh_forward_staged_post: legal[max_batch][nn_x*nn_y+1]
+ * (1 = legal, pass last), info[max_batch], temperature[max_batch]
+ * (nnPolicyTemperature), and the post-processed rows. */
+int kgh_handle_post_staging(kgh_handle* handle, uint8_t** legal, int32_t** info, float** temperature, float** post_out);
+/* kgh_forward_staged plus post-processing of the rows whose info has
+ * KGH_POST_ENABLED: raw rows land in the staging output as before,
+ * post-processed rows in the post staging. Synchronous; a non-finite sum or
+ * a row without legal moves is an error (as in the reference). */
+int kgh_forward_staged_post(kgh_handle* handle, int32_t n, const kgh_post_params* params);
+/* The post-processing alone on raw rows already on the device (layout of
+ * kgh_forward_device's output). Synchronous. */
+int kgh_postprocess_device(kgh_handle* handle, int32_t n, const float* d_raw, const uint8_t* d_legal,
+                           const int32_t* d_info, const float* d_temperature, const kgh_post_params* params,
+                           float* d_post);
+
 /* Device-memory forward on the handle's stream: every pointer is a device
  * pointer with the same layout as kgh_forward. Asynchronous; call
  * kgh_handle_synchronize before reading out. */

@@ -59,6 +59,21 @@ int32_t kgn_get_output(void* handle, void* loaded_model, int32_t nn_x, int32_t n
                        const int32_t* symmetry, const float* policy_optimism, float* policy, float* value, float* score,
                        float* ownership, char* err, int32_t errlen);
 
+/* kgn_get_output with device post-processing (NNResultBuf's
+ * postProcessOnDevice extension): per row legal[nn_x*nn_y+1] (1 = legal),
+ * row_info (KGH_POST_* flags | board_x << 8 | board_y << 16, katago_hip.h),
+ * temperature. Rows with KGH_POST_ENABLED come back post-processed as
+ * NNEvaluator::evaluate leaves them (nneval.cpp:946-1240): policy
+ * probabilities (-1 illegal), values[9] = whiteWinProb, whiteLossProb,
+ * whiteNoResultProb, whiteScoreMean, whiteScoreMeanSq, whiteLead,
+ * varTimeLeft, shorttermWinlossError, shorttermScoreError, and the white
+ * ownership map; other rows raw (values[0..2] logits, [3..8] the raw score
+ * fields). */
+int32_t kgn_get_output_post(void* handle, void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t n, const float* spatial,
+                            const float* global_in, const int32_t* symmetry, const float* policy_optimism,
+                            const uint8_t* legal, const int32_t* row_info, const float* temperature, float* policy,
+                            float* values, float* ownership, char* err, int32_t errlen);
+
 /* NeuralNet::testEvaluate{Conv,BatchNorm,ResidualBlock,GlobalPoolingResidualBlock}
  * (nninterface.h:134-180). kind: 0 conv, 1 batch norm, 2 residual block,
  * 3 global pooling residual block; desc_text is the descriptor in the model

@@ -510,6 +510,17 @@ struct kgh_handle {
   int* hSym = nullptr;
   float* hOpt = nullptr;
   float* hOut = nullptr;
+  // post-processing staging (kgh_forward_staged_post)
+  unsigned char* hLegal = nullptr;
+  int* hInfo = nullptr;
+  float* hTemp = nullptr;
+  float* hPost = nullptr;
+  int* hErr = nullptr;
+  unsigned char* dLegal = nullptr;
+  int* dInfo = nullptr;
+  float* dTemp = nullptr;
+  float* dPost = nullptr;
+  int* dErr = nullptr;
 
   std::vector<const float*> ropeCos, ropeSin;  // per RopeSpec of the model: [table][pair][H*W]
 
@@ -541,6 +552,11 @@ struct kgh_handle {
     if(hSym) (void)hipHostFree(hSym);
     if(hOpt) (void)hipHostFree(hOpt);
     if(hOut) (void)hipHostFree(hOut);
+    if(hLegal) (void)hipHostFree(hLegal);
+    if(hInfo) (void)hipHostFree(hInfo);
+    if(hTemp) (void)hipHostFree(hTemp);
+    if(hPost) (void)hipHostFree(hPost);
+    if(hErr) (void)hipHostFree(hErr);
     if(stream) (void)hipStreamDestroy(stream);
   }
 };
@@ -1252,6 +1268,18 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     KGH_HIP_CHECK(hipHostMalloc((void**)&h->hSym, (size_t)max_batch * sizeof(int), hipHostMallocDefault));
     KGH_HIP_CHECK(hipHostMalloc((void**)&h->hOpt, (size_t)max_batch * sizeof(float), hipHostMallocDefault));
     KGH_HIP_CHECK(hipHostMalloc((void**)&h->hOut, (size_t)max_batch * h->rowFloats * sizeof(float), hipHostMallocDefault));
+    const size_t policySize = (size_t)nn_x * nn_y + 1;
+    const size_t postFloats = (size_t)kgh_post_row_floats(nn_x, nn_y);
+    h->dLegal = a.allocN<unsigned char>((size_t)max_batch * policySize);
+    h->dInfo = a.allocN<int>(max_batch);
+    h->dTemp = a.allocN<float>(max_batch);
+    h->dPost = a.allocN<float>((size_t)max_batch * postFloats);
+    h->dErr = a.allocN<int>(1);
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hLegal, (size_t)max_batch * policySize, hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hInfo, (size_t)max_batch * sizeof(int), hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hTemp, (size_t)max_batch * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hPost, (size_t)max_batch * postFloats * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hErr, sizeof(int), hipHostMallocDefault));
     *out = h.release();
   });
 }
@@ -1279,7 +1307,7 @@ int kgh_forward_device(kgh_handle* handle, int32_t n, const float* d_spatial, co
 namespace {
 // The rows already in the handle's pinned staging buffers: H2D, forward, D2H
 // into the staging output, all on the handle's stream, then wait.
-void forwardStaged(kgh_handle* handle, int n) {
+void forwardStagedAsync(kgh_handle* handle, int n) {
   if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
   for(int i = 0; i < n; i++)
     if(handle->hSym[i] < 0 || handle->hSym[i] > 7) invalid("symmetry must be in 0..7");
@@ -1296,7 +1324,11 @@ void forwardStaged(kgh_handle* handle, int n) {
   runForward(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut);
   const size_t outBytes = (size_t)n * handle->rowFloats * sizeof(float);
   KGH_HIP_CHECK(hipMemcpyAsync(handle->hOut, handle->dOut, outBytes, hipMemcpyDeviceToHost, s));
-  KGH_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+void forwardStaged(kgh_handle* handle, int n) {
+  forwardStagedAsync(handle, n);
+  KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
 }
 }  // namespace
 
@@ -1314,6 +1346,93 @@ int kgh_forward(kgh_handle* handle, int32_t n, const float* spatial, const float
     memcpy(handle->hOpt, policy_optimism, (size_t)n * sizeof(float));
     forwardStaged(handle, n);
     memcpy(out, handle->hOut, (size_t)n * handle->rowFloats * sizeof(float));
+  });
+}
+
+namespace {
+// Post-processing of n raw rows already on the device (d_raw) into d_post,
+// then the error bits back to host memory; on the handle's stream, no wait.
+void postprocessAsync(kgh_handle* handle, int n, const float* d_raw, const unsigned char* d_legal, const int* d_info,
+                      const float* d_temp, const kgh_post_params* params, float* d_post) {
+  if(params == nullptr) invalid("null post-processing parameters");
+  const Net& net = handle->model->net;
+  if(net.modelVersion < 4) invalid("post-processing needs model version 4 or later");
+  PostArgs pa;
+  pa.raw = d_raw;
+  pa.rowFloats = handle->rowFloats;
+  pa.scoreC = net.scoreC;
+  pa.modelVersion = net.modelVersion;
+  pa.nnX = handle->W;
+  pa.nnY = handle->H;
+  pa.legal = d_legal;
+  pa.info = d_info;
+  pa.temperature = d_temp;
+  pa.outputScaleMultiplier = params->output_scale_multiplier;
+  pa.scoreMeanMultiplier = params->score_mean_multiplier;
+  pa.scoreStdevMultiplier = params->score_stdev_multiplier;
+  pa.leadMultiplier = params->lead_multiplier;
+  pa.varianceTimeMultiplier = params->variance_time_multiplier;
+  pa.shorttermValueErrorMultiplier = params->shortterm_value_error_multiplier;
+  pa.shorttermScoreErrorMultiplier = params->shortterm_score_error_multiplier;
+  pa.out = d_post;
+  pa.err = handle->dErr;
+  pa.batch = n;
+  hipStream_t s = handle->stream;
+  KGH_HIP_CHECK(hipMemsetAsync(handle->dErr, 0, sizeof(int), s));
+  kgh::launchPostprocess(pa, s);
+  KGH_HIP_CHECK(hipMemcpyAsync(handle->hErr, handle->dErr, sizeof(int), hipMemcpyDeviceToHost, s));
+}
+
+void checkPostErrors(const kgh_handle* handle) {
+  const int e = *handle->hErr;
+  if(e & POST_ERR_NO_LEGAL_MOVE) invalid("post-processing: a row has no legal move");
+  if(e & POST_ERR_POLICY_NONFINITE) throw KghError(KGH_ERR_INTERNAL, "Got nonfinite for policy sum");
+  if(e & POST_ERR_VALUE_NONFINITE) throw KghError(KGH_ERR_INTERNAL, "Got nonfinite for nneval value");
+}
+}  // namespace
+
+int32_t kgh_post_row_floats(int32_t nn_x, int32_t nn_y) { return 2 * nn_x * nn_y + 10; }
+
+int kgh_handle_post_staging(kgh_handle* handle, uint8_t** legal, int32_t** info, float** temperature, float** post_out) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(!legal || !info || !temperature || !post_out) invalid("null pointer");
+    *legal = handle->hLegal;
+    *info = handle->hInfo;
+    *temperature = handle->hTemp;
+    *post_out = handle->hPost;
+  });
+}
+
+int kgh_forward_staged_post(kgh_handle* handle, int32_t n, const kgh_post_params* params) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
+    KGH_HIP_CHECK(hipSetDevice(handle->model->device));
+    hipStream_t s = handle->stream;
+    const size_t policySize = (size_t)handle->H * handle->W + 1;
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->dLegal, handle->hLegal, (size_t)n * policySize, hipMemcpyHostToDevice, s));
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->dInfo, handle->hInfo, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s));
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->dTemp, handle->hTemp, (size_t)n * sizeof(float), hipMemcpyHostToDevice, s));
+    forwardStagedAsync(handle, n);
+    postprocessAsync(handle, n, handle->dOut, handle->dLegal, handle->dInfo, handle->dTemp, params, handle->dPost);
+    const size_t postBytes = (size_t)n * kgh_post_row_floats(handle->W, handle->H) * sizeof(float);
+    KGH_HIP_CHECK(hipMemcpyAsync(handle->hPost, handle->dPost, postBytes, hipMemcpyDeviceToHost, s));
+    KGH_HIP_CHECK(hipStreamSynchronize(s));
+    checkPostErrors(handle);
+  });
+}
+
+int kgh_postprocess_device(kgh_handle* handle, int32_t n, const float* d_raw, const uint8_t* d_legal, const int32_t* d_info,
+                           const float* d_temperature, const kgh_post_params* params, float* d_post) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(n <= 0 || n > handle->maxBatch) invalid("batch size " + std::to_string(n) + " outside 1.." + std::to_string(handle->maxBatch));
+    if(!d_raw || !d_legal || !d_info || !d_temperature || !d_post) invalid("null device pointer");
+    KGH_HIP_CHECK(hipSetDevice(handle->model->device));
+    postprocessAsync(handle, n, d_raw, d_legal, d_info, d_temperature, params, d_post);
+    KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
+    checkPostErrors(handle);
   });
 }
 

@@ -35,6 +35,33 @@ struct UnpackArgs {
   float* out;
 };
 
+// Post-processing of raw outputs into what NNEvaluator::evaluate returns
+// (nneval.cpp:946-1240). Per row: legal[policySize] (1 = legal),
+// info = POST_* flags | boardX << 8 | boardY << 16, temperature.
+constexpr int POST_ENABLED = 1;
+constexpr int POST_WHITE_TO_MOVE = 2;
+constexpr int POST_NO_RESULT_DISABLED = 4;  // koRule != KO_SIMPLE && scoringRule != SCORING_TERRITORY
+constexpr int POST_PASSING_HACKS = 8;
+constexpr int POST_ERR_POLICY_NONFINITE = 1;
+constexpr int POST_ERR_NO_LEGAL_MOVE = 2;
+constexpr int POST_ERR_VALUE_NONFINITE = 4;
+struct PostArgs {
+  const float* raw;  // packed raw rows (kgh_output_row_floats)
+  int rowFloats;
+  int scoreC;
+  int modelVersion;
+  int nnX, nnY;
+  const unsigned char* legal;  // [batch][nnX*nnY + 1]
+  const int* info;
+  const float* temperature;
+  float outputScaleMultiplier;
+  double scoreMeanMultiplier, scoreStdevMultiplier, leadMultiplier, varianceTimeMultiplier;
+  double shorttermValueErrorMultiplier, shorttermScoreErrorMultiplier;
+  float* out;  // [batch][2*nnX*nnY + 10]: policy+pass, win/loss/noResult, 6 score fields, ownership
+  int* err;    // POST_ERR_* bits, or-ed per call
+  int batch;
+};
+
 namespace kgh {
 
 template<typename T>
@@ -56,6 +83,7 @@ template<typename T>
 void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream);
 
 void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream);
+void launchPostprocess(const PostArgs& a, hipStream_t stream);
 
 // Transformer trunk (kgh_transformer.hip).
 // Per-row RMSNorm: y = act(x * rsqrt(mean(x^2) + eps) * gamma + beta) * (mask != 0); beta may be null.

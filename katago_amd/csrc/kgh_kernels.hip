@@ -371,6 +371,178 @@ __global__ void unpackOutputsKernel(UnpackArgs a) {
   }
 }
 
+constexpr int NN_MAX_POLICY = 19 * 19 + 1;
+
+// NNEvaluator's post-processing of one row per workgroup
+// (nneval.cpp:946-1240): the policy softmax over legal moves with the
+// temperature and the optional pass cap, the value softmax and score
+// transforms in double precision, and the ownership tanh, all turned to the
+// white player's perspective. Rows without POST_ENABLED are skipped.
+__device__ double postSoftPlus(double x) { return x > 40.0 ? x : log(1.0 + exp(x)); }
+
+__global__ __launch_bounds__(256) void postprocessKernel(PostArgs a) {
+  const int n = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int info = a.info[n];
+  if(!(info & POST_ENABLED)) return;
+  const int HW = a.nnX * a.nnY;
+  const int policySize = HW + 1;
+  const float* raw = a.raw + (size_t)n * a.rowFloats;
+  const unsigned char* legal = a.legal + (size_t)n * policySize;
+  float* out = a.out + (size_t)n * (2 * HW + 10);
+  __shared__ float redF[8];
+  __shared__ int redI[8];
+  const int lane = tid & 63, wave = tid >> 6;
+
+  // Policy (nneval.cpp:946-1024).
+  const float scaling = a.outputScaleMultiplier / a.temperature[n];
+  constexpr int PER = (NN_MAX_POLICY + 255) / 256;
+  float v[PER];
+  float mx = -1e25f;
+  int legalCount = 0;
+#pragma unroll
+  for(int k = 0; k < PER; k++) {
+    const int i = tid + 256 * k;
+    v[k] = -1e30f;
+    if(i < policySize) {
+      if(legal[i]) {
+        legalCount++;
+        v[k] = raw[i] * scaling;
+      }
+      mx = fmaxf(mx, v[k]);
+    }
+  }
+  for(int o = 32; o > 0; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    legalCount += __shfl_xor(legalCount, o);
+  }
+  if(lane == 0) {
+    redF[wave] = mx;
+    redI[wave] = legalCount;
+  }
+  __syncthreads();
+  mx = fmaxf(fmaxf(redF[0], redF[1]), fmaxf(redF[2], redF[3]));
+  legalCount = redI[0] + redI[1] + redI[2] + redI[3];
+  __syncthreads();
+  const bool passHacks = (info & POST_PASSING_HACKS) != 0;
+  float e[PER];
+  float sum = 0.0f;
+#pragma unroll
+  for(int k = 0; k < PER; k++) {
+    const int i = tid + 256 * k;
+    e[k] = 0.0f;
+    if(i < policySize) {
+      e[k] = expf(v[k] - mx);
+      if(!(passHacks && i == HW)) sum += e[k];
+    }
+  }
+  for(int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  if(lane == 0) redF[wave] = sum;
+  __syncthreads();
+  sum = (redF[0] + redF[1]) + (redF[2] + redF[3]);
+  if(passHacks) {
+    // Pass prior capped at 19 times the other moves' total (95%).
+    const float ePass = expf((legal[HW] ? raw[HW] * scaling : -1e30f) - mx);
+    const float pass = fmaxf(1e-20f, fminf(ePass, sum * 19.0f));
+#pragma unroll
+    for(int k = 0; k < PER; k++)
+      if(tid + 256 * k == HW) e[k] = pass;
+    sum += pass;
+  }
+  if(tid == 0) {
+    if(legalCount <= 0) atomicOr(a.err, POST_ERR_NO_LEGAL_MOVE);
+    if(!isfinite(sum)) atomicOr(a.err, POST_ERR_POLICY_NONFINITE);
+  }
+  const float uniform = legalCount > 0 ? 1.0f / legalCount : 0.0f;
+#pragma unroll
+  for(int k = 0; k < PER; k++) {
+    const int i = tid + 256 * k;
+    if(i < policySize) out[i] = legal[i] ? (sum > 0.0f ? e[k] / sum : uniform) : -1.0f;
+  }
+
+  // Ownership (nneval.cpp:1222-1241): tanh, white's perspective, zero off the board.
+  const int bx = (info >> 8) & 0xff, by = (info >> 16) & 0xff;
+  const bool white = (info & POST_WHITE_TO_MOVE) != 0;
+  const float* own = raw + HW + 1 + 3 + a.scoreC;
+  for(int p = tid; p < HW; p += 256) {
+    const int y = p / a.nnX, x = p - y * a.nnX;
+    float o = 0.0f;
+    if(y < by && x < bx) {
+      const float t = tanhf(own[p] * a.outputScaleMultiplier);
+      o = white ? t : -t;
+    }
+    out[policySize + 9 + p] = o;
+  }
+
+  // Value and score (nneval.cpp:1097-1216), model version >= 4.
+  if(tid == 0) {
+    const float* val = raw + policySize;
+    const float* sc = val + 3;
+    double sm = 0, smsq = 0, lead = 0, vtl = 0, stw = 0, sts = 0;
+    if(a.modelVersion >= 9) {
+      sm = sc[0], smsq = sc[1], lead = sc[2], vtl = sc[3], stw = sc[4], sts = sc[5];
+    }
+    else if(a.modelVersion >= 8) {
+      sm = sc[0], smsq = sc[1], lead = sc[2], vtl = sc[3];
+    }
+    else {
+      sm = sc[0], smsq = sc[1], lead = sc[0];
+    }
+    const double osm = a.outputScaleMultiplier;
+    const double winLogits = val[0] * osm;
+    const double lossLogits = val[1] * osm;
+    double noResultLogits = val[2] * osm;
+    const bool noResultDisabled = (info & POST_NO_RESULT_DISABLED) != 0;
+    if(noResultDisabled) noResultLogits -= 100000.0;
+    const double maxLogits = fmax(fmax(winLogits, lossLogits), noResultLogits);
+    double winProb = exp(winLogits - maxLogits);
+    double lossProb = exp(lossLogits - maxLogits);
+    double noResultProb = exp(noResultLogits - maxLogits);
+    if(noResultDisabled) noResultProb = 0.0;
+    const double probSum = winProb + lossProb + noResultProb;
+    winProb /= probSum;
+    lossProb /= probSum;
+    noResultProb /= probSum;
+    double scoreMean = sm * osm * a.scoreMeanMultiplier;
+    const double scoreStdev = postSoftPlus(smsq * osm) * a.scoreStdevMultiplier;
+    double scoreMeanSq = scoreMean * scoreMean + scoreStdev * scoreStdev;
+    double ld = lead * osm * a.leadMultiplier;
+    const double varTimeLeft = postSoftPlus(vtl * osm) * a.varianceTimeMultiplier;
+    scoreMean *= 1.0 - noResultProb;
+    scoreMeanSq *= 1.0 - noResultProb;
+    ld *= 1.0 - noResultProb;
+    double stWinloss, stScore;
+    if(a.modelVersion >= 14) {
+      const double s1 = postSoftPlus(stw * osm * 0.5);
+      stWinloss = sqrt(s1 * s1 * a.shorttermValueErrorMultiplier);
+      const double s2 = postSoftPlus(sts * osm * 0.5);
+      stScore = sqrt(s2 * s2 * a.shorttermScoreErrorMultiplier);
+    }
+    else if(a.modelVersion >= 10) {
+      stWinloss = sqrt(postSoftPlus(stw * osm) * a.shorttermValueErrorMultiplier);
+      stScore = sqrt(postSoftPlus(sts * osm) * a.shorttermScoreErrorMultiplier);
+    }
+    else {
+      stWinloss = postSoftPlus(stw * osm);
+      stScore = postSoftPlus(sts * osm) * 10.0;
+    }
+    if(!isfinite(probSum) || !isfinite(scoreMean) || !isfinite(scoreMeanSq) || !isfinite(ld) || !isfinite(varTimeLeft) ||
+       !isfinite(stWinloss) || !isfinite(stScore))
+      atomicOr(a.err, POST_ERR_VALUE_NONFINITE);
+    float* o = out + policySize;
+    o[0] = (float)(white ? winProb : lossProb);
+    o[1] = (float)(white ? lossProb : winProb);
+    o[2] = (float)noResultProb;
+    o[3] = (float)(white ? scoreMean : -scoreMean);
+    o[4] = (float)scoreMeanSq;
+    o[5] = (float)(white ? ld : -ld);
+    const bool v9 = a.modelVersion >= 9;
+    o[6] = v9 ? (float)varTimeLeft : -1.0f;
+    o[7] = v9 ? (float)stWinloss : -1.0f;
+    o[8] = v9 ? (float)stScore : -1.0f;
+  }
+}
+
 }  // namespace
 
 namespace kgh {
@@ -472,6 +644,12 @@ void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream) {
 void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream) {
   int total = a.batch * a.H * a.W;
   hipLaunchKernelGGL(unpackOutputsKernel, dim3((total + 255) / 256), dim3(256), 0, stream, a);
+  KGH_CHECK_LAUNCH();
+}
+
+void launchPostprocess(const PostArgs& a, hipStream_t stream) {
+  if(a.nnX * a.nnY + 1 > NN_MAX_POLICY) throw KghError(3, "post-processing: board larger than 19x19");
+  hipLaunchKernelGGL(postprocessKernel, dim3(a.batch), dim3(256), 0, stream, a);
   KGH_CHECK_LAUNCH();
 }
 

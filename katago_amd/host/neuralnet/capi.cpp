@@ -158,6 +158,68 @@ int32_t kgn_get_output(void* h, void* m, int32_t nn_x, int32_t nn_y, int32_t n, 
   }
 }
 
+int32_t kgn_get_output_post(void* h, void* m, int32_t nn_x, int32_t nn_y, int32_t n, const float* spatial, const float* global_in,
+                            const int32_t* symmetry, const float* policy_optimism, const uint8_t* legal, const int32_t* row_info,
+                            const float* temperature, float* policy, float* values, float* ownership, char* err, int32_t errlen) {
+  try {
+    const LoadedModel* lm = (const LoadedModel*)m;
+    const ModelDesc& d = NeuralNet::getModelDesc(lm);
+    const int HW = nn_x * nn_y;
+    const size_t spatialElts = (size_t)d.numInputChannels * HW;
+    std::unique_ptr<InputBuffers, void (*)(InputBuffers*)> bufs(NeuralNet::createInputBuffers(lm, n, nn_x, nn_y),
+                                                                 NeuralNet::freeInputBuffers);
+    vector<std::unique_ptr<NNResultBuf>> rows;
+    vector<NNResultBuf*> rowPtrs;
+    vector<std::unique_ptr<NNOutput>> outs;
+    vector<NNOutput*> outPtrs;
+    for(int i = 0; i < n; i++) {
+      rows.emplace_back(new NNResultBuf());
+      NNResultBuf& r = *rows.back();
+      r.rowSpatialBuf.assign(spatial + spatialElts * i, spatial + spatialElts * (i + 1));
+      r.rowGlobalBuf.assign(global_in + (size_t)d.numInputGlobalChannels * i, global_in + (size_t)d.numInputGlobalChannels * (i + 1));
+      r.symmetry = symmetry[i];
+      r.policyOptimism = policy_optimism[i];
+      const int info = row_info[i];
+      r.postProcessOnDevice = (info & KGH_POST_ENABLED) != 0;
+      r.nextPlayerIsWhite = (info & KGH_POST_WHITE_TO_MOVE) != 0;
+      r.noResultDisabled = (info & KGH_POST_NO_RESULT_DISABLED) != 0;
+      r.enablePassingHacks = (info & KGH_POST_PASSING_HACKS) != 0;
+      r.boardXSizeForServer = (info >> 8) & 0xff;
+      r.boardYSizeForServer = (info >> 16) & 0xff;
+      r.nnPolicyTemperature = temperature[i];
+      r.rowLegalBuf.assign(legal + (size_t)(HW + 1) * i, legal + (size_t)(HW + 1) * (i + 1));
+      rowPtrs.push_back(&r);
+      outs.emplace_back(new NNOutput());
+      NNOutput& o = *outs.back();
+      memset(&o, 0, sizeof(o));
+      o.nnXLen = nn_x;
+      o.nnYLen = nn_y;
+      o.whiteOwnerMap = ownership + (size_t)HW * i;
+      outPtrs.push_back(&o);
+    }
+    NeuralNet::getOutput((ComputeHandle*)h, bufs.get(), n, rowPtrs.data(), outPtrs);
+    for(int i = 0; i < n; i++) {
+      const NNOutput& o = *outPtrs[i];
+      memcpy(policy + (size_t)(HW + 1) * i, o.policyProbs, (size_t)(HW + 1) * sizeof(float));
+      float* v = values + 9 * i;
+      v[0] = o.whiteWinProb;
+      v[1] = o.whiteLossProb;
+      v[2] = o.whiteNoResultProb;
+      v[3] = o.whiteScoreMean;
+      v[4] = o.whiteScoreMeanSq;
+      v[5] = o.whiteLead;
+      v[6] = o.varTimeLeft;
+      v[7] = o.shorttermWinlossError;
+      v[8] = o.shorttermScoreError;
+    }
+    return 0;
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return -1;
+  }
+}
+
 int32_t kgn_test_evaluate(int32_t kind, const char* desc_text, int32_t batch, int32_t nn_x, int32_t nn_y, int32_t use_fp16,
                           int32_t use_nhwc, const float* input, const float* mask, float* output, int64_t output_len, char* err,
                           int32_t errlen) {

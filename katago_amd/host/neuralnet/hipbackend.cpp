@@ -320,6 +320,11 @@ struct ComputeHandle {
   int32_t* stSymmetry = nullptr;
   float* stOptimism = nullptr;
   float* stOutput = nullptr;
+  uint8_t* stLegal = nullptr;
+  int32_t* stInfo = nullptr;
+  float* stTemperature = nullptr;
+  float* stPost = nullptr;
+  kgh_post_params postParams = {};
   ~ComputeHandle() {
     if(handle != nullptr) kgh_handle_free(handle);
     if(context != nullptr && model != nullptr) {
@@ -413,6 +418,15 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
            "kgh_handle_create");
   checkKgh(kgh_handle_staging(h->handle, &h->stSpatial, &h->stGlobal, &h->stSymmetry, &h->stOptimism, &h->stOutput),
            "kgh_handle_staging");
+  checkKgh(kgh_handle_post_staging(h->handle, &h->stLegal, &h->stInfo, &h->stTemperature, &h->stPost), "kgh_handle_post_staging");
+  const ModelPostProcessParams& pp = desc.postProcessParams;
+  h->postParams.output_scale_multiplier = pp.outputScaleMultiplier;
+  h->postParams.score_mean_multiplier = pp.scoreMeanMultiplier;
+  h->postParams.score_stdev_multiplier = pp.scoreStdevMultiplier;
+  h->postParams.lead_multiplier = pp.leadMultiplier;
+  h->postParams.variance_time_multiplier = pp.varianceTimeMultiplier;
+  h->postParams.shortterm_value_error_multiplier = pp.shorttermValueErrorMultiplier;
+  h->postParams.shortterm_score_error_multiplier = pp.shorttermScoreErrorMultiplier;
 
   if(logger != nullptr) {
     char buf[512] = {0};
@@ -474,11 +488,56 @@ void NeuralNet::getOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFil
     h->stSymmetry[i] = row.symmetry;
     h->stOptimism[i] = (float)row.policyOptimism;
   }
-  checkKgh(kgh_forward_staged(h->handle, n), "kgh_forward_staged");
+  // Rows asking for device post-processing (an extension of the reference's
+  // NNResultBuf) carry their legal moves, side to move and rules.
+  bool anyPost = false;
+  for(int i = 0; i < n; i++) anyPost = anyPost || inputBufs[i]->postProcessOnDevice;
+  if(anyPost) {
+    const size_t policySize = (size_t)HW + 1;
+    for(int i = 0; i < n; i++) {
+      const NNResultBuf& row = *inputBufs[i];
+      int32_t info = 0;
+      if(row.postProcessOnDevice) {
+        if(row.rowLegalBuf.size() < policySize) throw StringError("HIP backend: rowLegalBuf smaller than the policy size");
+        memcpy(h->stLegal + policySize * i, row.rowLegalBuf.data(), policySize);
+        info = KGH_POST_ENABLED | (row.nextPlayerIsWhite ? KGH_POST_WHITE_TO_MOVE : 0) |
+               (row.noResultDisabled ? KGH_POST_NO_RESULT_DISABLED : 0) | (row.enablePassingHacks ? KGH_POST_PASSING_HACKS : 0) |
+               (row.boardXSizeForServer << 8) | (row.boardYSizeForServer << 16);
+        if(row.boardXSizeForServer <= 0 || row.boardXSizeForServer > nnX || row.boardYSizeForServer <= 0 ||
+           row.boardYSizeForServer > nnY)
+          throw StringError("HIP backend: post-processed row with a board size outside the net's");
+      }
+      h->stInfo[i] = info;
+      h->stTemperature[i] = row.nnPolicyTemperature;
+    }
+    checkKgh(kgh_forward_staged_post(h->handle, n, &h->postParams), "kgh_forward_staged_post");
+  }
+  else {
+    checkKgh(kgh_forward_staged(h->handle, n), "kgh_forward_staged");
+  }
 
+  const size_t postFloats = (size_t)kgh_post_row_floats(nnX, nnY);
   for(int i = 0; i < n; i++) {
     NNOutput* out = outputs[i];
     if(out->nnXLen != nnX || out->nnYLen != nnY) throw StringError("HIP backend: NNOutput board size mismatch");
+    out->policyOptimismUsed = (float)inputBufs[i]->policyOptimism;
+    if(inputBufs[i]->postProcessOnDevice) {
+      const float* r = h->stPost + postFloats * i;
+      memcpy(out->policyProbs, r, (size_t)(HW + 1) * sizeof(float));
+      for(int k = HW + 1; k < NNPos::MAX_NN_POLICY_SIZE; k++) out->policyProbs[k] = -1.0f;
+      const float* v = r + HW + 1;
+      out->whiteWinProb = v[0];
+      out->whiteLossProb = v[1];
+      out->whiteNoResultProb = v[2];
+      out->whiteScoreMean = v[3];
+      out->whiteScoreMeanSq = v[4];
+      out->whiteLead = v[5];
+      out->varTimeLeft = v[6];
+      out->shorttermWinlossError = v[7];
+      out->shorttermScoreError = v[8];
+      if(out->whiteOwnerMap != nullptr) memcpy(out->whiteOwnerMap, v + 9, (size_t)HW * sizeof(float));
+      continue;
+    }
     const float* r = h->stOutput + b->singleOutputElts * i;
     memcpy(out->policyProbs, r, (size_t)(HW + 1) * sizeof(float));
     out->whiteWinProb = r[HW + 1];

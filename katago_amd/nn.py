@@ -81,6 +81,8 @@ def host_library() -> ctypes.CDLL:
             c.c_char_p, c.c_int32]
         lib.kgn_test_evaluate.argtypes = [c.c_int32, c.c_char_p, c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_int32,
                                           c.c_void_p, c.c_void_p, c.c_void_p, c.c_int64, c.c_char_p, c.c_int32]
+        lib.kgn_get_output_post.argtypes = [c.c_void_p, c.c_void_p, c.c_int32, c.c_int32, c.c_int32] + [c.c_void_p] * 10 + [
+            c.c_char_p, c.c_int32]
         lib.kgn_evaluator_create.restype = c.c_void_p
         lib.kgn_evaluator_create.argtypes = [c.c_void_p] + [c.c_int32] * 7 + [c.c_char_p, c.c_int32]
         lib.kgn_evaluator_free.argtypes = [c.c_void_p]
@@ -206,6 +208,32 @@ class ComputeHandle:
         if rc != 0:
             _raise(err)
         return {"policy": policy, "value": value, "score": score, "ownership": own}
+
+    def get_output_post(self, spatial, global_in, legal, row_info, temperature=None, symmetry=None, policy_optimism=None):
+        """getOutput with device post-processing of the rows whose row_info
+        has POST_ENABLED: returns policy [n, HW+1], values [n, 9], ownership
+        [n, HW] (see kgn_get_output_post)."""
+        lib = host_library()
+        n = int(np.asarray(global_in).shape[0])
+        hw = self.context.nn_x * self.context.nn_y
+        spatial = np.ascontiguousarray(spatial, dtype=np.float32).reshape(n, -1)
+        global_in = np.ascontiguousarray(global_in, dtype=np.float32).reshape(n, -1)
+        legal = np.ascontiguousarray(legal, dtype=np.uint8).reshape(n, hw + 1)
+        info = np.ascontiguousarray(row_info, dtype=np.int32)
+        temp = np.ascontiguousarray(np.ones(n) if temperature is None else temperature, dtype=np.float32)
+        sym = np.ascontiguousarray(np.zeros(n) if symmetry is None else symmetry, dtype=np.int32)
+        opt = np.ascontiguousarray(np.zeros(n) if policy_optimism is None else policy_optimism, dtype=np.float32)
+        policy = np.zeros((n, hw + 1), np.float32)
+        values = np.zeros((n, 9), np.float32)
+        own = np.zeros((n, hw), np.float32)
+        err = _errbuf()
+        rc = lib.kgn_get_output_post(self._ptr, self.model._ptr, self.context.nn_x, self.context.nn_y, n, spatial.ctypes.data,
+                                     global_in.ctypes.data, sym.ctypes.data, opt.ctypes.data, legal.ctypes.data,
+                                     info.ctypes.data, temp.ctypes.data, policy.ctypes.data, values.ctypes.data,
+                                     own.ctypes.data, err, len(err))
+        if rc != 0:
+            _raise(err)
+        return {"policy": policy, "values": values, "ownership": own}
 
     def close(self):
         if getattr(self, "_ptr", None):
@@ -406,6 +434,12 @@ class DeviceHandle:
     def forward_device(self, n, d_spatial, d_global, d_sym, d_opt, d_out):
         hip_check(hip_library().kgh_forward_device(self._ptr, n, d_spatial, d_global, d_sym, d_opt, d_out))
 
+    def postprocess_device(self, n, d_raw, d_legal, d_info, d_temp, params: "PostParams", d_post):
+        lib = hip_library()
+        lib.kgh_postprocess_device.argtypes = [ctypes.c_void_p, ctypes.c_int32] + [ctypes.c_void_p] * 4 + [
+            ctypes.POINTER(PostParams), ctypes.c_void_p]
+        hip_check(lib.kgh_postprocess_device(self._ptr, n, d_raw, d_legal, d_info, d_temp, ctypes.byref(params), d_post))
+
     def synchronize(self):
         hip_check(hip_library().kgh_handle_synchronize(self._ptr))
 
@@ -430,6 +464,24 @@ class DeviceHandle:
 
     def __del__(self):
         self.close()
+
+
+POST_ENABLED, POST_WHITE_TO_MOVE, POST_NO_RESULT_DISABLED, POST_PASSING_HACKS = 1, 2, 4, 8
+
+
+def post_info(enabled=True, white_to_move=False, no_result_disabled=False, passing_hacks=False, board_x=19, board_y=19):
+    """The per-row info word of the device post-processing (katago_hip.h)."""
+    return ((POST_ENABLED if enabled else 0) | (POST_WHITE_TO_MOVE if white_to_move else 0) |
+            (POST_NO_RESULT_DISABLED if no_result_disabled else 0) | (POST_PASSING_HACKS if passing_hacks else 0) |
+            (board_x << 8) | (board_y << 16))
+
+
+class PostParams(ctypes.Structure):
+    """kgh_post_params (ModelPostProcessParams, desc.h:468-481)."""
+    _fields_ = [("output_scale_multiplier", ctypes.c_float), ("score_mean_multiplier", ctypes.c_double),
+                ("score_stdev_multiplier", ctypes.c_double), ("lead_multiplier", ctypes.c_double),
+                ("variance_time_multiplier", ctypes.c_double), ("shortterm_value_error_multiplier", ctypes.c_double),
+                ("shortterm_score_error_multiplier", ctypes.c_double)]
 
 
 class DeviceBuffer:
