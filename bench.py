@@ -141,6 +141,7 @@ def main():
     ap.add_argument("--model-dir", default=None)
     ap.add_argument("--config", type=int, default=CFG_INDEX,
                     help="BASELINE.json config index; 2 (default) is the headline, 4 the transformer trunk")
+    ap.add_argument("--no-autotune", action="store_true", help="keep the built-in kernel choices")
     ap.add_argument("--no-serve", action="store_true",
                     help="skip the PCIe-inclusive measurement through the batching evaluator")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -175,6 +176,11 @@ def main():
     lm = nn.LoadedModel(path)
     dm = nn.DeviceModel(lm, use_fp16=cfg.fp16)
     h = nn.DeviceHandle(dm, batch)
+    # Tile choices as a backend handle makes them at creation (the on-device
+    # autotuner); the table goes to stderr.
+    tuning = "" if args.no_autotune else h.autotune()
+    print("bench: autotuned conv shapes (ky kx cinPad cout M gated residual maskedResidual variant name best_us "
+          "heuristic_us):\n" + tuning, file=sys.stderr, flush=True)
     f3, f1, fother = conv_flops(dm.layers, hw)
     flops_per_eval = f3 + f1 + fother
 
@@ -243,7 +249,8 @@ def main():
         "data": f"synthetic (seeded random-weight {name}, seeded synthetic positions)",
         "config": {"workload": f"C{args.config}: {name} {'fp16' if cfg.fp16 else 'fp32'} boards {boards} in 19x19, batch {batch}, "
                                f"symmetry 0, inputs resident in HBM",
-                   "global_batch": batch, "board": "19x19", "parallelism": "none (1 GPU)"},
+                   "global_batch": batch, "board": "19x19", "parallelism": "none (1 GPU)",
+                   "autotuned_shapes": len([l for l in tuning.splitlines() if l.strip()])},
         "mfma_frac_end_to_end": round(value * flops_per_eval / (PEAK_FP16_TFLOPS * 1e12), 4),
         "gflop_per_eval": round(flops_per_eval / 1e9, 3),
         "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2),

@@ -211,6 +211,28 @@ int kgh_evaluate_layers(int32_t device, const kgh_layer* layers, int32_t num_lay
  * launches. Forwards while profiling is on always run eagerly. */
 int kgh_handle_set_graphs(kgh_handle* handle, int32_t enabled);
 
+/* On-device autotuner (no counterpart in the reference's HIP-less backends;
+ * the OpenCL backend's tuner, opencltuner.cpp, plays this role there). For
+ * every distinct conv shape of the model at the handle's max batch it times
+ * each applicable kernel variant (tap-window / 1x1 DMA / 128-row tile
+ * kernels and their tile widths) inside whole forwards on the handle's own
+ * buffers (HIP events around every conv launch; forward k runs each shape's
+ * k-th candidate, repeated reps times). The fastest on average replaces the
+ * built-in choice only if whole forwards replayed from graphs get at least
+ * 0.5% faster with it. Choices hold for later forwards of the handle's max
+ * batch size; other batch sizes keep the built-in choices. All variants sum in the same order, so results
+ * are bitwise unchanged. report (may be NULL) receives one line per shape:
+ * "ky kx cinPad cout M gated residual maskedResidual variant name
+ * [best_us heuristic_us]", variant 0 ("auto") where the built-in choice
+ * stays. */
+int kgh_handle_autotune(kgh_handle* handle, int32_t reps, char* report, int32_t report_len);
+/* Installs a tuning table (lines "ky kx cinPad cout M gated residual
+ * maskedResidual variant ...", '#' comments) as saved from
+ * kgh_handle_autotune or kgh_handle_get_tuning. A variant that does not apply
+ * to its shape at launch time falls back to the built-in choice. */
+int kgh_handle_set_tuning(kgh_handle* handle, const char* table);
+int kgh_handle_get_tuning(kgh_handle* handle, char* buf, int32_t buflen);
+
 /* Per-launch timing of the convolution kernels, measured with HIP events on
  * the handle's stream. kgh_handle_set_profiling(h, 1) clears the records and
  * starts recording every conv launch of the following forwards;

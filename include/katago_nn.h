@@ -40,6 +40,21 @@ int32_t kgn_model_flatten(void* loaded_model, int32_t* num_layers, int64_t* num_
 void* kgn_create_context(void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t use_fp16, char* err, int32_t errlen);
 /* NeuralNet::freeComputeContext (nninterface.h:64). */
 void kgn_free_context(void* context);
+
+/* createComputeContext with the backend's config keys: home_data_dir is
+ * homeDataDirOverride (tuning tables go to <dir>/hiptuning; "" = $HOME/.katago),
+ * auto_tune sets hipAutoTune (-1 keeps the default, on), tuner_file sets
+ * hipTunerFile (NULL or "" = a name per gpu, board, batch, dtype and
+ * architecture). */
+void* kgn_create_context_ex(void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t use_fp16, const char* home_data_dir,
+                            int32_t auto_tune, const char* tuner_file, char* err, int32_t errlen);
+
+/* The handle's tuning table (text, as saved) into buf; returns where it came
+ * from: 0 built-in choices, 1 a tuning file, 2 tuned at handle creation;
+ * -1 on error (message in buf). */
+int32_t kgn_handle_tuning(void* handle, char* buf, int32_t buflen);
+/* Installs a tuning table on the handle (kgh_handle_set_tuning). */
+int32_t kgn_handle_set_tuning(void* handle, const char* table, char* err, int32_t errlen);
 /* NeuralNet::createComputeHandle (nninterface.h:74-83). */
 void* kgn_create_handle(void* context, void* loaded_model, int32_t max_batch, int32_t require_exact_nn_len,
                         int32_t inputs_use_nhwc, int32_t gpu_idx, char* err, int32_t errlen);

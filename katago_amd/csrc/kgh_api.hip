@@ -12,7 +12,10 @@
 #include "kgh_kernels.h"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
+#include <map>
+#include <sstream>
 #include <climits>
 #include <cstring>
 #include <memory>
@@ -537,6 +540,28 @@ struct kgh_handle {
   };
   bool graphsEnabled = true;
   std::vector<GraphEntry> graphs;
+
+  // Autotuned kernel variant per conv shape, keyed by (ky, kx, cinPad, cout,
+  // M, gated epilogue, residual, masked residual); every conv launch of a
+  // forward looks its shape up here (kgh_handle_autotune, kgh_handle_set_tuning).
+  typedef std::array<int, 8> TuneKey;
+  std::map<TuneKey, int> tuned;
+  std::vector<TuneKey> tuneShapes;  // every shape the last autotune looked at
+  // While autotuning: the shapes seen in a forward with the variants that
+  // apply to each (collect), then the timing of every conv launch of the
+  // timed forwards (timing; events reused across forwards).
+  struct ConvCall {
+    TuneKey key;
+    std::vector<int> variants;
+  };
+  std::vector<ConvCall>* collect = nullptr;
+  struct TuneRec {
+    TuneKey key;
+    int variant;
+    hipEvent_t start, stop;
+  };
+  std::vector<TuneRec>* timing = nullptr;
+  size_t timingUsed = 0;
   int lastN = -1;
   const void* lastPtr[5] = {};
   uint64_t useCounter = 0;
@@ -606,6 +631,36 @@ struct Runner {
   }
 
   void conv(const ConvW& c, const T* x, int ldx, const ConvEpilogue<T>& e) {
+    int variant = CONV_AUTO;
+    if(h != nullptr) {
+      const kgh_handle::TuneKey key = {c.ky, c.kx, c.cinPad, c.cout, M, e.glu, e.residual != nullptr ? 1 : 0, e.maskResidualAdd};
+      if(!h->tuned.empty()) {
+        auto it = h->tuned.find(key);
+        if(it != h->tuned.end()) variant = it->second;
+      }
+      if(h->collect != nullptr) {
+        kgh_handle::ConvCall call;
+        call.key = key;
+        for(int v = 1; v < CONV_VARIANT_COUNT; v++)
+          if(kgh::convVariantApplies<T>(v, x, ldx, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, g, e)) call.variants.push_back(v);
+        h->collect->push_back(call);
+      }
+      if(h->timing != nullptr) {
+        if(h->timingUsed == h->timing->size()) {
+          kgh_handle::TuneRec r;
+          KGH_HIP_CHECK(hipEventCreate(&r.start));
+          KGH_HIP_CHECK(hipEventCreate(&r.stop));
+          h->timing->push_back(r);
+        }
+        kgh_handle::TuneRec& r = (*h->timing)[h->timingUsed++];
+        r.key = key;
+        r.variant = variant;
+        KGH_HIP_CHECK(hipEventRecord(r.start, s));
+        kgh::launchConv<T>(x, ldx, c.cin, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, c.wDirect, g, e, s, nullptr, variant);
+        KGH_HIP_CHECK(hipEventRecord(r.stop, s));
+        return;
+      }
+    }
     ProfRec* rec = nullptr;
     if(h != nullptr && h->profiling) {
       if(h->profUsed == h->prof.size()) {
@@ -619,7 +674,7 @@ struct Runner {
       rec->flops = 2.0 * M * (double)c.cin * c.cout * c.ky * c.kx;
       KGH_HIP_CHECK(hipEventRecord(rec->start, s));
     }
-    kgh::launchConv<T>(x, ldx, c.cin, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, c.wDirect, g, e, s, nullptr);
+    kgh::launchConv<T>(x, ldx, c.cin, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, c.wDirect, g, e, s, nullptr, variant);
     if(rec != nullptr) KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
   }
 
@@ -914,6 +969,29 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
 // kernels of a forward. Profiling runs eagerly.
 constexpr size_t KGH_MAX_GRAPHS = 8;
 
+// The eager forward captured into an executable graph (graph replay is how
+// repeated forwards run, and how the autotuner judges a choice end to end).
+hipGraphExec_t captureForward(kgh_handle* h, int n, const float* sp, const float* gl, const int* sym, const float* opt, float* out) {
+  hipGraph_t graph = nullptr;
+  KGH_HIP_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+  try {
+    if(h->model->net.fp16) forwardImpl<half_t>(h, n, sp, gl, sym, opt, out);
+    else forwardImpl<float>(h, n, sp, gl, sym, opt, out);
+  }
+  catch(...) {
+    hipGraph_t partial = nullptr;
+    (void)hipStreamEndCapture(h->stream, &partial);
+    if(partial) (void)hipGraphDestroy(partial);
+    throw;
+  }
+  KGH_HIP_CHECK(hipStreamEndCapture(h->stream, &graph));
+  hipGraphExec_t exec = nullptr;
+  hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  KGH_HIP_CHECK(e);
+  return exec;
+}
+
 void runForward(kgh_handle* h, int n, const float* sp, const float* gl, const int* sym, const float* opt, float* out) {
   auto eager = [&] {
     if(h->model->net.fp16) forwardImpl<half_t>(h, n, sp, gl, sym, opt, out);
@@ -943,22 +1021,7 @@ void runForward(kgh_handle* h, int n, const float* sp, const float* gl, const in
     eager();
     return;
   }
-  hipGraph_t graph = nullptr;
-  KGH_HIP_CHECK(hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
-  try {
-    eager();
-  }
-  catch(...) {
-    hipGraph_t partial = nullptr;
-    (void)hipStreamEndCapture(h->stream, &partial);
-    if(partial) (void)hipGraphDestroy(partial);
-    throw;
-  }
-  KGH_HIP_CHECK(hipStreamEndCapture(h->stream, &graph));
-  hipGraphExec_t exec = nullptr;
-  hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  (void)hipGraphDestroy(graph);
-  KGH_HIP_CHECK(e);
+  hipGraphExec_t exec = captureForward(h, n, sp, gl, sym, opt, out);
   if(h->graphs.size() >= KGH_MAX_GRAPHS) {
     size_t lru = 0;
     for(size_t i = 1; i < h->graphs.size(); i++)
@@ -1480,6 +1543,220 @@ int kgh_memcpy_htod(void* dst, const void* src, size_t bytes) {
 }
 int kgh_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
   return guarded([&] { KGH_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost)); });
+}
+
+namespace {
+void dropGraphs(kgh_handle* h) {
+  for(auto& g : h->graphs) (void)hipGraphExecDestroy(g.exec);
+  h->graphs.clear();
+  h->lastN = -1;
+}
+
+// One line per shape: the tuned variant, or 0 (the built-in choice) for
+// shapes the tuner looked at and left alone.
+std::string tuningText(const kgh_handle* h, const std::map<kgh_handle::TuneKey, std::pair<float, float>>* times) {
+  std::map<kgh_handle::TuneKey, int> all;
+  for(const auto& k : h->tuneShapes) all[k] = CONV_AUTO;
+  for(const auto& kv : h->tuned) all[kv.first] = kv.second;
+  std::ostringstream o;
+  for(const auto& kv : all) {
+    for(int k : kv.first) o << k << ' ';
+    o << kv.second << ' ' << kgh::convVariantName(kv.second);
+    if(times != nullptr) {
+      auto it = times->find(kv.first);
+      if(it != times->end()) o << ' ' << it->second.first << ' ' << it->second.second;
+    }
+    o << '\n';
+  }
+  return o.str();
+}
+
+void writeText(const std::string& text, char* buf, int32_t buflen) {
+  if(buf == nullptr || buflen <= 0) return;
+  if((int64_t)text.size() + 1 > buflen) invalid("tuning text needs " + std::to_string(text.size() + 1) + " bytes");
+  memcpy(buf, text.c_str(), text.size() + 1);
+}
+}  // namespace
+
+int kgh_handle_autotune(kgh_handle* handle, int32_t reps, char* report, int32_t report_len) {
+  return guarded([&] {
+    requireHandle(handle);
+    KGH_HIP_CHECK(hipSetDevice(handle->model->device));
+    if(handle->profiling) invalid("autotune while profiling");
+    reps = reps > 0 ? reps : 3;
+    const int n = handle->maxBatch;
+    const Net& net = handle->model->net;
+    const size_t HW = (size_t)handle->H * handle->W;
+    hipStream_t s = handle->stream;
+    // Any inputs do: the launches are timed, not checked.
+    KGH_HIP_CHECK(hipMemsetAsync(handle->dSpatial, 0, (size_t)n * HW * net.inputC * sizeof(float), s));
+    KGH_HIP_CHECK(hipMemsetAsync(handle->dGlobal, 0, (size_t)n * net.globalC * sizeof(float), s));
+    KGH_HIP_CHECK(hipMemsetAsync(handle->dSym, 0, (size_t)n * sizeof(int), s));
+    KGH_HIP_CHECK(hipMemsetAsync(handle->dOpt, 0, (size_t)n * sizeof(float), s));
+    const bool graphs = handle->graphsEnabled;
+    handle->graphsEnabled = false;
+    dropGraphs(handle);
+    handle->tuned.clear();
+    std::vector<kgh_handle::ConvCall> calls;
+    std::vector<kgh_handle::TuneRec> recs;
+    std::map<kgh_handle::TuneKey, std::pair<float, float>> times;  // chosen variant's us, built-in choice's us
+    auto forward = [&] { runForward(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut); };
+    try {
+      // The shapes of the model and the variants each can take.
+      handle->collect = &calls;
+      forward();
+      handle->collect = nullptr;
+      std::map<kgh_handle::TuneKey, std::vector<int>> cands;  // CONV_AUTO first
+      for(const auto& c : calls)
+        if(!cands.count(c.key) && !c.variants.empty()) {
+          std::vector<int> v = {CONV_AUTO};
+          v.insert(v.end(), c.variants.begin(), c.variants.end());
+          cands[c.key] = v;
+        }
+      handle->tuneShapes.clear();
+      for(const auto& kv : cands) handle->tuneShapes.push_back(kv.first);
+      size_t rounds = 0;
+      for(const auto& kv : cands) rounds = std::max(rounds, kv.second.size());
+      // Timed forwards: in forward k every shape runs its (k mod count)-th
+      // candidate, so each variant is timed in place (inputs as the previous
+      // kernel left them), reps times over.
+      for(int i = 0; i < 2; i++) forward();  // clocks up
+      std::map<std::pair<kgh_handle::TuneKey, int>, std::pair<double, int>> acc;
+      handle->timing = &recs;
+      for(int r = 0; r < reps; r++)
+        for(size_t k = 0; k < rounds; k++) {
+          for(const auto& kv : cands) handle->tuned[kv.first] = kv.second[k % kv.second.size()];
+          handle->timingUsed = 0;
+          forward();
+          KGH_HIP_CHECK(hipStreamSynchronize(s));
+          for(size_t i = 0; i < handle->timingUsed; i++) {
+            float ms = 0.0f;
+            KGH_HIP_CHECK(hipEventElapsedTime(&ms, recs[i].start, recs[i].stop));
+            auto& a = acc[{recs[i].key, recs[i].variant}];
+            a.first += ms * 1000.0;
+            a.second++;
+          }
+        }
+      handle->timing = nullptr;
+      handle->tuned.clear();
+      // Per shape, the fastest variant in place is the challenger of the
+      // built-in choice; it is kept only if whole forwards, replayed from
+      // graphs as they run in production, get faster with it (alternating
+      // A/B replays, at least 0.5% less time).
+      hipEvent_t e0, e1;
+      KGH_HIP_CHECK(hipEventCreate(&e0));
+      KGH_HIP_CHECK(hipEventCreate(&e1));
+      auto replayMs = [&](hipGraphExec_t g, int times) {
+        KGH_HIP_CHECK(hipEventRecord(e0, s));
+        for(int i = 0; i < times; i++) KGH_HIP_CHECK(hipGraphLaunch(g, s));
+        KGH_HIP_CHECK(hipEventRecord(e1, s));
+        KGH_HIP_CHECK(hipEventSynchronize(e1));
+        float ms = 0.0f;
+        KGH_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        return (double)ms;
+      };
+      auto capture = [&] { return captureForward(handle, n, handle->dSpatial, handle->dGlobal, handle->dSym, handle->dOpt, handle->dOut); };
+      std::map<kgh_handle::TuneKey, int> chosen;
+      try {
+        for(const auto& kv : cands) {
+          int best = CONV_AUTO;
+          double bestUs = 1e30, autoUs = 0;
+          for(int v : kv.second) {
+            auto it = acc.find({kv.first, v});
+            if(it == acc.end() || it->second.second == 0) continue;
+            const double us = it->second.first / it->second.second;
+            if(v == CONV_AUTO) autoUs = us;
+            else if(us < bestUs) {
+              bestUs = us;
+              best = v;
+            }
+          }
+          if(best == CONV_AUTO || bestUs >= autoUs) continue;
+          handle->tuned = chosen;
+          hipGraphExec_t ga = capture();
+          handle->tuned[kv.first] = best;
+          hipGraphExec_t gb = nullptr;
+          try {
+            gb = capture();
+          }
+          catch(...) {
+            (void)hipGraphExecDestroy(ga);
+            throw;
+          }
+          double ta = 0, tb = 0;
+          replayMs(ga, 2);
+          replayMs(gb, 2);
+          for(int r = 0; r < 3; r++) {
+            ta += replayMs(ga, 4);
+            tb += replayMs(gb, 4);
+          }
+          (void)hipGraphExecDestroy(ga);
+          (void)hipGraphExecDestroy(gb);
+          if(tb < 0.995 * ta) {
+            chosen[kv.first] = best;
+            times[kv.first] = {(float)bestUs, (float)autoUs};
+          }
+        }
+      }
+      catch(...) {
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        throw;
+      }
+      (void)hipEventDestroy(e0);
+      (void)hipEventDestroy(e1);
+      handle->tuned = chosen;
+    }
+    catch(...) {
+      handle->collect = nullptr;
+      handle->timing = nullptr;
+      handle->graphsEnabled = graphs;
+      for(auto& r : recs) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+      }
+      throw;
+    }
+    for(auto& r : recs) {
+      (void)hipEventDestroy(r.start);
+      (void)hipEventDestroy(r.stop);
+    }
+    handle->graphsEnabled = graphs;
+    dropGraphs(handle);
+    writeText(tuningText(handle, &times), report, report_len);
+  });
+}
+
+int kgh_handle_set_tuning(kgh_handle* handle, const char* table) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(table == nullptr) invalid("null tuning table");
+    std::map<kgh_handle::TuneKey, int> t;
+    std::vector<kgh_handle::TuneKey> shapes;
+    std::istringstream in(table);
+    std::string line;
+    while(std::getline(in, line)) {
+      if(line.empty() || line[0] == '#') continue;
+      std::istringstream ls(line);
+      kgh_handle::TuneKey key;
+      int v = 0;
+      for(int& k : key) ls >> k;
+      ls >> v;
+      if(!ls || v < CONV_AUTO || v >= CONV_VARIANT_COUNT) invalid("bad tuning line: " + line);
+      shapes.push_back(key);
+      if(v != CONV_AUTO) t[key] = v;
+    }
+    handle->tuned = t;
+    handle->tuneShapes = shapes;
+    dropGraphs(handle);
+  });
+}
+
+int kgh_handle_get_tuning(kgh_handle* handle, char* buf, int32_t buflen) {
+  return guarded([&] {
+    requireHandle(handle);
+    writeText(tuningText(handle, nullptr), buf, buflen);
+  });
 }
 
 int kgh_handle_set_graphs(kgh_handle* handle, int32_t enabled) {

@@ -142,15 +142,45 @@ struct BoardGeom {
   int W;
 };
 
+// Kernel choices for one conv launch: the autotuner's search space. All of
+// them sum the K dimension in the same order, so they give bitwise the same
+// results. CONV_AUTO is the built-in heuristic.
+enum ConvVariant {
+  CONV_AUTO = 0,
+  CONV_TW_192,    // 3x3 fp16 tap-window DMA kernel, 12 waves, 192 output channels per tile
+  CONV_TW_128,
+  CONV_TW_64,
+  CONV_TW8_192,   // the same with 8 waves
+  CONV_DMA1_192,  // 1x1 fp16 DMA kernel
+  CONV_DMA1_128,
+  CONV_DMA1_64,
+  CONV_TILE_192,  // 128-row tile kernel (fp16 and fp32, 1x1 and 3x3)
+  CONV_TILE_128,
+  CONV_TILE_96,
+  CONV_TILE_64,
+  CONV_TILE_32,
+  CONV_VARIANT_COUNT
+};
+
 // Host-side launchers (definitions in kgh_conv.hip / kgh_kernels.hip).
 namespace kgh {
 
 // Conv of x[M, cinStride] (first cin channels used) with weights prepared by
 // prepareConvWeights into layout [tap][cout][cinPad]; dispatches to the
 // matrix-core kernel when the shape allows, else to the direct kernel.
+const char* convVariantName(int variant);
+
+// variant pins the kernel when it applies to the shape; otherwise (or with
+// CONV_AUTO) the heuristic picks.
 template<typename T>
 void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky, int kx, const void* wPrepared,
-                const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma);
+                const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma,
+                int variant = CONV_AUTO);
+
+// Whether launchConv would take variant for this shape.
+template<typename T>
+bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared,
+                        BoardGeom g, const ConvEpilogue<T>& epi);
 
 template<typename T>
 bool convMfmaSupported(int cinPad, int cout);

@@ -1021,14 +1021,20 @@ void launchMfma(const T* x, int cinStride, int cinPad, int cout, const T* w, Boa
 
 constexpr int TW_ROW_WAVES = 6;  // 12 wave64s, three per SIMD: ~5% faster than 8 (sustained-clock measurement)
 
-template<int BN>
+template<int BN, int RW = TW_ROW_WAVES>
 void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                      const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   int M = g.batch * g.H * g.W;
   dim3 grid((M + TW_BM - 1) / TW_BM * (cout / BN));
-  hipLaunchKernelGGL((convTapWindowKernel<BN, TW_ROW_WAVES>), grid, dim3(TW_ROW_WAVES * 2 * 64), 0, stream, x, cinStride, cinPad, cout,
-                     w, g, epi);
+  hipLaunchKernelGGL((convTapWindowKernel<BN, RW>), grid, dim3(RW * 2 * 64), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
   KGH_CHECK_LAUNCH();
+}
+
+// Shape conditions of the window kernel apart from batch size.
+bool tapWindowFits(int cinStride, int cinPad, int cout, int bn, BoardGeom g, const ConvEpilogue<half_t>& epi) {
+  const long M = (long)g.batch * g.H * g.W;
+  return g.W + 1 <= TW_PAD_MAX && cinPad % 32 == 0 && cinStride % 8 == 0 && !epi.maskResidualAdd && !epi.glu &&
+         cout % bn == 0 && M * cinStride < (1L << 31) && 9L * cout * cinPad < (1L << 31);
 }
 
 // The window kernel: fp16, 3x3, plain residual adds (it starts the
@@ -1063,6 +1069,12 @@ void launch1x1Dma(const half_t* x, int cinStride, int cinPad, int cout, const ha
   KGH_CHECK_LAUNCH();
 }
 
+// Shape conditions of the 1x1 DMA kernel apart from batch size.
+bool dma1x1Fits(int cinStride, int cinPad, int cout, int bn, BoardGeom g) {
+  const long M = (long)g.batch * g.H * g.W;
+  return cinPad % 32 == 0 && cinStride % 8 == 0 && cout % bn == 0 && M * cinStride < (1L << 31) && (long)cout * cinPad < (1L << 31);
+}
+
 // The 1x1 DMA kernel: fp16, 32-channel steps, enough 384-row x BN tiles
 // (about 128 or more), 32-bit element offsets.
 template<typename T>
@@ -1081,6 +1093,67 @@ bool dispatch1x1Dma<half_t>(const half_t* x, int cinStride, int cinPad, int cout
   else if(cout % 64 == 0) launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
   else return false;
   return true;
+}
+
+// The explicitly chosen variants. variantFits() says whether the variant
+// takes the shape; launchVariant() runs it (only after variantFits()).
+template<typename T>
+bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g, const ConvEpilogue<T>& epi) {
+  if(v >= CONV_TILE_192 && v <= CONV_TILE_32) {
+    static const int bn[] = {192, 128, 96, 64, 32};
+    return cout % bn[v - CONV_TILE_192] == 0;
+  }
+  if constexpr(std::is_same<T, half_t>::value) {
+    if(ky == 3) {
+      if(v == CONV_TW_192 || v == CONV_TW8_192) return tapWindowFits(cinStride, cinPad, cout, 192, g, epi);
+      if(v == CONV_TW_128) return tapWindowFits(cinStride, cinPad, cout, 128, g, epi);
+      if(v == CONV_TW_64) return tapWindowFits(cinStride, cinPad, cout, 64, g, epi);
+    }
+    else {
+      if(v == CONV_DMA1_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
+      if(v == CONV_DMA1_128) return dma1x1Fits(cinStride, cinPad, cout, 128, g);
+      if(v == CONV_DMA1_64) return dma1x1Fits(cinStride, cinPad, cout, 64, g);
+    }
+  }
+  else {
+    (void)ky, (void)cinStride, (void)cinPad, (void)g, (void)epi;
+  }
+  return false;
+}
+
+template<typename T, int KS>
+void launchTileVariant(int v, const T* x, int cinStride, int cinPad, int cout, const T* w, BoardGeom g, const ConvEpilogue<T>& epi,
+                       hipStream_t stream) {
+  switch(v) {
+    case CONV_TILE_192: launchMfma<T, KS, 192, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); break;
+    case CONV_TILE_128: launchMfma<T, KS, 128, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); break;
+    case CONV_TILE_96: launchMfma<T, KS, 96, 4>(x, cinStride, cinPad, cout, w, g, epi, stream); break;
+    case CONV_TILE_64: launchMfma<T, KS, 64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); break;
+    default: launchMfma<T, KS, 32, 4>(x, cinStride, cinPad, cout, w, g, epi, stream); break;
+  }
+}
+
+template<typename T>
+void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cout, const T* w, BoardGeom g,
+                   const ConvEpilogue<T>& epi, hipStream_t stream) {
+  if(v >= CONV_TILE_192) {
+    if(ky == 3) launchTileVariant<T, 3>(v, x, cinStride, cinPad, cout, w, g, epi, stream);
+    else launchTileVariant<T, 1>(v, x, cinStride, cinPad, cout, w, g, epi, stream);
+    return;
+  }
+  if constexpr(std::is_same<T, half_t>::value) {
+    switch(v) {
+      case CONV_TW_192: launchTapWindow<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_TW_128: launchTapWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_TW_64: launchTapWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_TW8_192: launchTapWindow<192, 4>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_DMA1_192: launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_DMA1_128: launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_DMA1_64: launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      default: break;
+    }
+  }
+  throw KghError(5, "conv: variant does not apply");
 }
 
 template<typename T, int KS>
@@ -1104,13 +1177,17 @@ bool convMfmaSupported(int cinPad, int cout) {
   return cinPad % MfmaCfg<T>::BK == 0 && cout % 32 == 0 && cinPad > 0;
 }
 
+const char* convVariantName(int variant) {
+  static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
+                                "tile192", "tile128", "tile96", "tile64", "tile32"};
+  return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
+}
+
+// Conditions every matrix-core kernel needs: the epilogue moves 16 channels
+// per lane with 16-byte accesses, so split points fall on 16-channel
+// boundaries and every row start is 16-byte aligned.
 template<typename T>
-void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky, int kx, const void* wPrepared,
-                const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma) {
-  bool done = false;
-  // The matrix-core kernel's epilogue moves 16 channels per lane with 16-byte
-  // accesses: split points must fall on 16-channel boundaries and every row
-  // start must be 16-byte aligned.
+static bool mfmaPathOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi) {
   const int vec = 16 / (int)sizeof(T);
   auto on16 = [](int v) { return v == INT_MAX || v % 16 == 0; };
   auto aligned = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
@@ -1118,7 +1195,27 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
                      (epi.outRaw == nullptr || (epi.ldRaw % vec == 0 && aligned(epi.outRaw))) &&
                      (epi.outAct == nullptr || (epi.ldAct % vec == 0 && aligned(epi.outAct))) &&
                      (epi.residual == nullptr || (epi.ldRes % vec == 0 && aligned(epi.residual)));
-  if(wPrepared != nullptr && epiOk && convMfmaSupported<T>(cinPad, cout) && cinStride % vec == 0) {
+  return wPrepared != nullptr && epiOk && convMfmaSupported<T>(cinPad, cout) && cinStride % vec == 0 &&
+         ((ky == 3 && kx == 3) || (ky == 1 && kx == 1));
+}
+
+template<typename T>
+bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared,
+                        BoardGeom g, const ConvEpilogue<T>& epi) {
+  (void)x;
+  return variant > CONV_AUTO && variant < CONV_VARIANT_COUNT && mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
+         variantFits<T>(variant, ky, cinStride, cinPad, cout, g, epi);
+}
+
+template<typename T>
+void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky, int kx, const void* wPrepared,
+                const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma, int variant) {
+  bool done = false;
+  if(variant != CONV_AUTO && convVariantApplies<T>(variant, x, cinStride, cinPad, cout, ky, kx, wPrepared, g, epi)) {
+    launchVariant<T>(variant, ky, x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
+    done = true;
+  }
+  else if(mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi)) {
     if(ky == 3 && kx == 3) {
       done = dispatchTapWindow<T>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
       if(!done) done = dispatchMfmaTile<T, 3>(x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
@@ -1165,9 +1262,13 @@ void launchConvertToFloat(const T* src, float* dst, size_t n, hipStream_t stream
 template bool convMfmaSupported<float>(int, int);
 template bool convMfmaSupported<half_t>(int, int);
 template void launchConv<float>(const float*, int, int, int, int, int, int, const void*, const float*, BoardGeom,
-                                const ConvEpilogue<float>&, hipStream_t, bool*);
+                                const ConvEpilogue<float>&, hipStream_t, bool*, int);
+template bool convVariantApplies<float>(int, const float*, int, int, int, int, int, const void*, BoardGeom,
+                                        const ConvEpilogue<float>&);
+template bool convVariantApplies<half_t>(int, const half_t*, int, int, int, int, int, const void*, BoardGeom,
+                                         const ConvEpilogue<half_t>&);
 template void launchConv<half_t>(const half_t*, int, int, int, int, int, int, const void*, const float*, BoardGeom,
-                                 const ConvEpilogue<half_t>&, hipStream_t, bool*);
+                                 const ConvEpilogue<half_t>&, hipStream_t, bool*, int);
 template void prepareConvWeights<float>(const float*, float*, int, int, int, int, int, hipStream_t);
 template void prepareConvWeights<half_t>(const float*, half_t*, int, int, int, int, int, hipStream_t);
 template void launchConvertFromFloat<float>(const float*, float*, size_t, hipStream_t);

@@ -10,6 +10,8 @@
 #include "katago_nn.h"
 
 void hipBackendFlattenModel(const ModelDesc& desc, std::vector<kgh_layer>& layers, std::vector<float>& weights);
+int hipBackendTuning(const ComputeHandle* h, std::string& table);
+int32_t hipBackendSetTuning(ComputeHandle* h, const std::string& table);
 
 using std::string;
 using std::vector;
@@ -82,6 +84,45 @@ void* kgn_create_context(void* m, int32_t nn_x, int32_t nn_y, int32_t use_fp16, 
   catch(const std::exception& e) {
     setErr(err, errlen, e.what());
     return nullptr;
+  }
+}
+
+void* kgn_create_context_ex(void* m, int32_t nn_x, int32_t nn_y, int32_t use_fp16, const char* home_data_dir, int32_t auto_tune,
+                            const char* tuner_file, char* err, int32_t errlen) {
+  try {
+    ConfigParser cfg;
+    if(auto_tune >= 0) cfg.overrideKey("hipAutoTune", auto_tune ? "true" : "false");
+    if(tuner_file != nullptr && tuner_file[0] != 0) cfg.overrideKey("hipTunerFile", tuner_file);
+    enabled_t mode = use_fp16 == 0 ? enabled_t::False : use_fp16 == 1 ? enabled_t::True : enabled_t::Auto;
+    return NeuralNet::createComputeContext({0}, nullptr, nn_x, nn_y, home_data_dir != nullptr ? home_data_dir : "", mode,
+                                           (const LoadedModel*)m, cfg);
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return nullptr;
+  }
+}
+
+int32_t kgn_handle_set_tuning(void* h, const char* table, char* err, int32_t errlen) {
+  try {
+    return hipBackendSetTuning((ComputeHandle*)h, table != nullptr ? table : "");
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return -1;
+  }
+}
+
+int32_t kgn_handle_tuning(void* h, char* buf, int32_t buflen) {
+  try {
+    std::string table;
+    const int source = hipBackendTuning((const ComputeHandle*)h, table);
+    setErr(buf, buflen, table);
+    return source;
+  }
+  catch(const std::exception& e) {
+    setErr(buf, buflen, e.what());
+    return -1;
   }
 }
 

@@ -9,15 +9,25 @@
 // into cpp/neuralnet/ of a KataGo checkout next to the other backends.
 #include "../neuralnet/nninterface.h"
 
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cctype>
+#include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <iostream>
 #include <map>
 #include <memory>
 #include <mutex>
+#include <sstream>
 
 #include "../neuralnet/modelversion.h"
 #include "../neuralnet/nneval.h"
 #include "katago_hip.h"
+
+static const int HIP_TUNER_VERSION = 1;
+static const char* HIP_TUNER_VERSION_LINE = "VERSION=1";
 
 using std::string;
 using std::vector;
@@ -295,6 +305,13 @@ struct ComputeContext {
   // One uploaded copy of the weights per (device, precision), shared by handles.
   std::map<std::pair<int, bool>, std::pair<kgh_model*, int>> models;
 
+  // Autotuning (config keys hipAutoTune, hipTunerFile; the OpenCL backend's
+  // openCLTunerFile is the model): tables live in <home data dir>/hiptuning.
+  bool autoTune = true;
+  std::string tunerFile;  // explicit tuning file, else a per-(gpu, board, batch, dtype, architecture) name
+  std::string tunerDir;
+  uint64_t archHash = 0;  // of the flattened layer table (shapes, not weights)
+
   ComputeContext(int x, int y, enabled_t fp16) : nnXLen(x), nnYLen(y), useFP16Mode(fp16) {}
   ~ComputeContext() {
     for(auto& kv : models) kgh_model_free(kv.second.first);
@@ -325,6 +342,7 @@ struct ComputeHandle {
   float* stTemperature = nullptr;
   float* stPost = nullptr;
   kgh_post_params postParams = {};
+  int tuningSource = 0;  // 0 built-in choices, 1 loaded from a tuning file, 2 tuned at creation
   ~ComputeHandle() {
     if(handle != nullptr) kgh_handle_free(handle);
     if(context != nullptr && model != nullptr) {
@@ -367,17 +385,94 @@ LoadedModel* NeuralNet::loadModelFile(const string& file, const string& expected
 void NeuralNet::freeLoadedModel(LoadedModel* loadedModel) { delete loadedModel; }
 const ModelDesc& NeuralNet::getModelDesc(const LoadedModel* loadedModel) { return loadedModel->modelDesc; }
 
+// Tile choices for the handle's batch size: read from the tuning file when
+// one exists, else measured on the device (kgh_handle_autotune) and saved.
+// Batches of 8 boards or fewer keep the built-in choices.
+static void maybeAutoTune(ComputeHandle& h, Logger* logger, int serverThreadIdx) {
+  ComputeContext& c = *h.context;
+  h.tuningSource = 0;
+  if(!c.autoTune || h.maxBatchSize <= 8) return;
+  string path = c.tunerFile;
+  if(path.empty()) {
+    char dev[512] = {0};
+    kgh_device_info(h.device, dev, sizeof(dev));
+    string gpu;
+    for(const char* p = dev; *p != 0 && *p != ','; p++)
+      if(isalnum((unsigned char)*p)) gpu += *p;
+    path = c.tunerDir + "/" +
+           Global::strprintf("tune%d_gpu%s_x%d_y%d_b%d_%s_arch%016llx.txt", HIP_TUNER_VERSION, gpu.c_str(), c.nnXLen, c.nnYLen,
+                             h.maxBatchSize, h.useFP16 ? "fp16" : "fp32", (unsigned long long)c.archHash);
+  }
+  const string prefix = "HIP backend thread " + Global::intToString(serverThreadIdx) + ": ";
+  {
+    std::ifstream in(path);
+    if(in) {
+      std::stringstream ss;
+      ss << in.rdbuf();
+      string text = ss.str();
+      if(text.rfind(HIP_TUNER_VERSION_LINE, 0) == 0) {
+        const size_t eol = text.find('\n');
+        const string table = eol == string::npos ? string() : text.substr(eol + 1);
+        checkKgh(kgh_handle_set_tuning(h.handle, table.c_str()), "kgh_handle_set_tuning");
+        h.tuningSource = 1;
+        if(logger != nullptr) logger->write(prefix + "Loaded tuning parameters from: " + path);
+        return;
+      }
+    }
+  }
+  vector<char> report(1 << 16);
+  checkKgh(kgh_handle_autotune(h.handle, 3, report.data(), (int32_t)report.size()), "kgh_handle_autotune");
+  h.tuningSource = 2;
+  string text = string(HIP_TUNER_VERSION_LINE) + "\n# ky kx cinPad cout M gated residual maskedResidual variant name best_us heuristic_us\n" +
+                report.data();
+  // Save atomically; a directory that cannot be written only costs re-tuning.
+  mkdir(c.tunerDir.c_str(), 0755);
+  const string tmp = path + ".tmp" + Global::intToString((int)getpid()) + "_" + Global::intToString(serverThreadIdx);
+  {
+    std::ofstream out(tmp);
+    out << text;
+  }
+  if(rename(tmp.c_str(), path.c_str()) != 0) {
+    remove(tmp.c_str());
+    if(logger != nullptr) logger->write(prefix + "Could not save tuning parameters to " + path);
+  }
+  else if(logger != nullptr) {
+    logger->write(prefix + "Saved tuning parameters to: " + path);
+  }
+}
+
+// For the C shim: where the handle's tile choices came from (0 built-in,
+// 1 tuning file, 2 tuned at creation) and the table itself.
+int hipBackendTuning(const ComputeHandle* h, std::string& table) {
+  vector<char> buf(1 << 16);
+  checkKgh(kgh_handle_get_tuning(h->handle, buf.data(), (int32_t)buf.size()), "kgh_handle_get_tuning");
+  table = buf.data();
+  return h->tuningSource;
+}
+
+int32_t hipBackendSetTuning(ComputeHandle* h, const std::string& table) {
+  checkKgh(kgh_handle_set_tuning(h->handle, table.c_str()), "kgh_handle_set_tuning");
+  return 0;
+}
+
 ComputeContext* NeuralNet::createComputeContext(const vector<int>& gpuIdxs, Logger* logger, int nnXLen, int nnYLen,
                                                 const string& homeDataDirOverride, enabled_t useFP16Mode,
                                                 const LoadedModel* loadedModel, ConfigParser& cfg) {
   (void)gpuIdxs;
   (void)logger;
-  (void)homeDataDirOverride;
   (void)loadedModel;
-  (void)cfg;
   if(nnXLen <= 0 || nnYLen <= 0 || nnXLen > NNPos::MAX_BOARD_LEN || nnYLen > NNPos::MAX_BOARD_LEN)
     throw StringError("HIP backend: invalid nnXLen/nnYLen " + Global::intToString(nnXLen) + "x" + Global::intToString(nnYLen));
-  return new ComputeContext(nnXLen, nnYLen, useFP16Mode);
+  ComputeContext* c = new ComputeContext(nnXLen, nnYLen, useFP16Mode);
+  if(cfg.contains("hipAutoTune")) c->autoTune = cfg.getBool("hipAutoTune");
+  if(cfg.contains("hipTunerFile")) c->tunerFile = cfg.getString("hipTunerFile");
+  string home = homeDataDirOverride;
+  if(home.empty()) {
+    const char* env = getenv("HOME");
+    home = string(env != nullptr ? env : ".") + "/.katago";
+  }
+  c->tunerDir = home + "/hiptuning";
+  return c;
 }
 
 void NeuralNet::freeComputeContext(ComputeContext* computeContext) { delete computeContext; }
@@ -407,6 +502,21 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
       Flattener f;
       f.model(desc);
       kgh_model_desc d = f.describe(desc);
+      // FNV-1a over the layer table's shapes: the tile choices depend on them only.
+      uint64_t hsh = 1469598103934665603ULL;
+      auto mix = [&](int64_t v) {
+        for(int k = 0; k < 8; k++) {
+          hsh ^= (uint64_t)((v >> (8 * k)) & 0xff);
+          hsh *= 1099511628211ULL;
+        }
+      };
+      for(const kgh_layer& l : f.layers) {
+        mix(l.op);
+        for(int k = 0; k < 7; k++) mix(l.i[k]);
+        mix(l.wn[0]);
+        mix(l.wn[1]);
+      }
+      context->archHash = hsh;
       kgh_model* m = nullptr;
       checkKgh(kgh_model_create(h->device, &d, h->useFP16 ? 1 : 0, &m), "kgh_model_create");
       it = context->models.emplace(key, std::make_pair(m, 0)).first;
@@ -427,6 +537,8 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
   h->postParams.variance_time_multiplier = pp.varianceTimeMultiplier;
   h->postParams.shortterm_value_error_multiplier = pp.shorttermValueErrorMultiplier;
   h->postParams.shortterm_score_error_multiplier = pp.shorttermScoreErrorMultiplier;
+
+  maybeAutoTune(*h, logger, serverThreadIdx);
 
   if(logger != nullptr) {
     char buf[512] = {0};

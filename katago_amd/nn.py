@@ -72,6 +72,11 @@ def host_library() -> ctypes.CDLL:
         lib.kgn_create_context.restype = c.c_void_p
         lib.kgn_create_context.argtypes = [c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_char_p, c.c_int32]
         lib.kgn_free_context.argtypes = [c.c_void_p]
+        lib.kgn_create_context_ex.restype = c.c_void_p
+        lib.kgn_create_context_ex.argtypes = [c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_char_p, c.c_int32, c.c_char_p,
+                                              c.c_char_p, c.c_int32]
+        lib.kgn_handle_tuning.argtypes = [c.c_void_p, c.c_char_p, c.c_int32]
+        lib.kgn_handle_set_tuning.argtypes = [c.c_void_p, c.c_char_p, c.c_char_p, c.c_int32]
         lib.kgn_create_handle.restype = c.c_void_p
         lib.kgn_create_handle.argtypes = [c.c_void_p, c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_char_p,
                                           c.c_int32]
@@ -146,15 +151,21 @@ class LoadedModel:
 
 
 class ComputeContext:
-    """NeuralNet::createComputeContext. use_fp16: True, False or None (auto)."""
+    """NeuralNet::createComputeContext. use_fp16: True, False or None (auto).
+    auto_tune: None keeps the backend default (on), True/False sets
+    hipAutoTune; home_data_dir is homeDataDirOverride (tuning tables under
+    <dir>/hiptuning); tuner_file sets hipTunerFile."""
 
-    def __init__(self, model: LoadedModel, nn_x: int = 19, nn_y: int = 19, use_fp16=None):
+    def __init__(self, model: LoadedModel, nn_x: int = 19, nn_y: int = 19, use_fp16=None, auto_tune=None,
+                 home_data_dir: str = "", tuner_file: str = ""):
         lib = host_library()
         err = _errbuf()
         mode = 2 if use_fp16 is None else (1 if use_fp16 else 0)
         self.model = model
         self.nn_x, self.nn_y = nn_x, nn_y
-        self._ptr = lib.kgn_create_context(model._ptr, nn_x, nn_y, mode, err, len(err))
+        tune = -1 if auto_tune is None else int(bool(auto_tune))
+        self._ptr = lib.kgn_create_context_ex(model._ptr, nn_x, nn_y, mode, home_data_dir.encode(), tune, tuner_file.encode(),
+                                              err, len(err))
         if not self._ptr:
             _raise(err)
 
@@ -186,6 +197,20 @@ class ComputeHandle:
     @property
     def using_fp16(self) -> bool:
         return bool(host_library().kgn_is_using_fp16(self._ptr))
+
+    def tuning(self):
+        """(source, table): source 0 built-in choices, 1 loaded from a tuning
+        file, 2 tuned at creation; table as saved."""
+        buf = ctypes.create_string_buffer(1 << 16)
+        src = host_library().kgn_handle_tuning(self._ptr, buf, len(buf))
+        if src < 0:
+            raise StringError(buf.value.decode(errors="replace"))
+        return src, buf.value.decode()
+
+    def set_tuning(self, table: str):
+        err = _errbuf()
+        if host_library().kgn_handle_set_tuning(self._ptr, table.encode(), err, len(err)) != 0:
+            _raise(err)
 
     def get_output(self, spatial, global_in, symmetry=None, policy_optimism=None):
         """Returns raw outputs as a dict of arrays: policy [n, HW+1] (pass last),
@@ -442,6 +467,14 @@ class DeviceHandle:
 
     def synchronize(self):
         hip_check(hip_library().kgh_handle_synchronize(self._ptr))
+
+    def autotune(self, reps: int = 3) -> str:
+        """kgh_handle_autotune: returns the table (one line per conv shape)."""
+        lib = hip_library()
+        lib.kgh_handle_autotune.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_char_p, ctypes.c_int32]
+        buf = ctypes.create_string_buffer(1 << 16)
+        hip_check(lib.kgh_handle_autotune(self._ptr, reps, buf, len(buf)))
+        return buf.value.decode()
 
     def set_profiling(self, on: bool):
         hip_check(hip_library().kgh_handle_set_profiling(self._ptr, int(on)))
