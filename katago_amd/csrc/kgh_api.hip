@@ -686,15 +686,26 @@ struct Runner {
 
   // On entry, if blocks[0] is a conv-kind block, A[depth] holds
   // act(blocks[0].preBN(R[depth])) * mask. On exit, if tail != null, A[depth]
-  // holds act(tail(R[depth])) * mask.
-  void runStack(const std::vector<Block>& blocks, int depth, const BNAct* tail) {
+  // holds act(tail(R[depth])) * mask, and R[depth] holds the raw stream only
+  // if rawLive (nothing reads it after an inner stack, or after a trunk
+  // whose tip BN is applied in the last epilogue, so that store is skipped).
+  void runStack(const std::vector<Block>& blocks, int depth, const BNAct* tail, bool rawLive = true) {
     for(size_t i = 0; i < blocks.size(); i++) {
-      const BNAct* next = (i + 1 < blocks.size()) ? (isConvKind(blocks[i + 1]) ? &blocks[i + 1].preBN : nullptr) : tail;
-      runBlock(blocks[i], depth, next);
+      const bool last = i + 1 == blocks.size();
+      const BNAct* next = !last ? (isConvKind(blocks[i + 1]) ? &blocks[i + 1].preBN : nullptr) : tail;
+      runBlock(blocks[i], depth, next, !last || rawLive);
     }
   }
 
-  void runBlock(const Block& b, int depth, const BNAct* next) {
+  // The residual update's raw output is dropped when nothing reads it (the
+  // activated output, if any, is still written).
+  static void dropDeadRaw(ConvEpilogue<T>& e, bool rawNeeded) {
+    if(rawNeeded || e.outAct == nullptr) return;
+    e.outRaw = nullptr;
+    e.rawEnd = 0;
+  }
+
+  void runBlock(const Block& b, int depth, const BNAct* next, bool rawNeeded = true) {
     T* Rd = R[depth];
     T* Ad = A[depth];
     const int C = (b.kind == BK_ATTENTION || b.kind == BK_FFN) ? b.C : b.preBN.C;
@@ -711,6 +722,7 @@ struct Runner {
       e2.ldRaw = C;
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
+      dropDeadRaw(e2, rawNeeded);
       conv(b.conv2, tmp1, b.conv1.cout, e2);
     }
     else if(b.kind == BK_GPOOL) {
@@ -751,6 +763,7 @@ struct Runner {
       e2.ldRaw = C;
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
+      dropDeadRaw(e2, rawNeeded);
       conv(b.conv2, tmp3, b.regC, e2);
     }
     else if(b.kind == BK_NBT) {
@@ -764,7 +777,7 @@ struct Runner {
       const BNAct* firstInner = isConvKind(b.inner[0]) ? &b.inner[0].preBN : nullptr;
       setAct(e1, firstInner, Am, midC);
       conv(b.conv1, Ad, C, e1);
-      runStack(b.inner, depth + 1, &b.midBN);
+      runStack(b.inner, depth + 1, &b.midBN, false);
       ConvEpilogue<T> e2 = epi();
       e2.residual = Rd;
       e2.ldRes = C;
@@ -772,6 +785,7 @@ struct Runner {
       e2.ldRaw = C;
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
+      dropDeadRaw(e2, rawNeeded);
       conv(b.conv2, Am, midC, e2);
     }
     else if(b.kind == BK_ATTENTION) {
@@ -804,6 +818,7 @@ struct Runner {
       e2.ldRaw = C;
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
+      dropDeadRaw(e2, rawNeeded);
       conv(b.proj, att, aC, e2);
     }
     else if(b.kind == BK_FFN) {
@@ -827,6 +842,7 @@ struct Runner {
       e2.ldRaw = C;
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
+      dropDeadRaw(e2, rawNeeded);
       conv(b.proj, hid, F, e2);
     }
     else {
@@ -869,7 +885,7 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
     Runner<T>::setAct(e, first, r.A[0], net.trunkC);
     r.conv(net.initialConv, (const T*)h->x0, net.inputCPad, e);
   }
-  r.runStack(net.blocks, 0, net.tipKind == 0 ? &net.tipBN : nullptr);
+  r.runStack(net.blocks, 0, net.tipKind == 0 ? &net.tipBN : nullptr, net.tipKind != 0);
   if(net.tipKind != 0) {
     // Trunk-tip RMSNorm + activation into A[0], the heads' input.
     if(net.tipSpatial)
