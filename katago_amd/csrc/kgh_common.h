@@ -159,6 +159,9 @@ enum ConvVariant {
   CONV_TILE_96,
   CONV_TILE_64,
   CONV_TILE_32,
+  CONV_BOARD_192,  // 3x3 fp16 one-board-per-workgroup kernel (19x19 boards), 192 output channels per tile
+  CONV_BOARD_128,
+  CONV_BOARD_64,
   CONV_VARIANT_COUNT
 };
 

@@ -73,9 +73,23 @@ __device__ __forceinline__ void rowColTile(int colTiles, int& rowTile, int& colT
 // Epilogue shared by the matrix-core conv kernels; requires
 // convStageBytes(WM) bytes of LDS at smem and must be reached by every
 // thread of the workgroup (it contains barriers).
-template<typename T, int BN, int WM>
-__device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM / 32][BN / (4 / WM) / 32], unsigned char* smem,
-                                                  int m0, int n0, int M, int HW, const ConvEpilogue<T>& epi) {
+// Calls f(std::integral_constant<int, ACT>()) for the epilogue's activation
+// kind, so the per-element activation is selected at compile time instead of
+// branching on every element.
+template<typename F>
+__device__ __forceinline__ void withActKind(int act, bool used, F&& f) {
+  switch(used ? act : KGH_ACT_IDENTITY) {
+    case KGH_ACT_RELU: f(std::integral_constant<int, KGH_ACT_RELU>()); break;
+    case KGH_ACT_MISH: f(std::integral_constant<int, KGH_ACT_MISH>()); break;
+    case KGH_ACT_SILU: f(std::integral_constant<int, KGH_ACT_SILU>()); break;
+    case KGH_ACT_MISH_SCALE8: f(std::integral_constant<int, KGH_ACT_MISH_SCALE8>()); break;
+    default: f(std::integral_constant<int, KGH_ACT_IDENTITY>()); break;
+  }
+}
+
+template<typename T, int BN, int WM, int ACT>
+__device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / WM / 32][BN / (4 / WM) / 32], unsigned char* smem,
+                                                     int m0, int n0, int M, int HW, const ConvEpilogue<T>& epi) {
   // Epilogue. For each 32-column block the wave writes its accumulators to
   // its own LDS region, then each lane takes 16 contiguous channels of one
   // row: 16-byte vector loads of the residual, 16-byte stores of the raw and
@@ -157,7 +171,7 @@ __device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM /
         if(actCols && epi.glu) {
           T o[8];
 #pragma unroll
-          for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], epi.actKind) * v[8 + j]);
+          for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], ACT) * v[8 + j]);
           uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin) / 2);
 #pragma unroll
           for(int q = 0; q < 8 / VEC; q++) dst[q] = ((const uint4*)o)[q];
@@ -165,7 +179,7 @@ __device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM /
         else if(actCols) {
           T o[16];
 #pragma unroll
-          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk);
+          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], ACT) * msk);
           uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin));
 #pragma unroll
           for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
@@ -176,37 +190,49 @@ __device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM /
   }
 }
 
+template<typename T, int BN, int WM>
+__device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM / 32][BN / (4 / WM) / 32], unsigned char* smem,
+                                                  int m0, int n0, int M, int HW, const ConvEpilogue<T>& epi) {
+  withActKind(epi.actKind, epi.outAct != nullptr, [&](auto actTag) {
+    storeTileEpilogueAct<T, BN, WM, decltype(actTag)::value>(acc, smem, m0, n0, M, HW, epi);
+  });
+}
+
 // Loads a wave's RB x CB tiles of a plain residual into the accumulators:
 // 16-byte row-major loads (lane: row lane >> 1, channels 16 * (lane & 1)..),
 // all issued before the first is used, then a transpose through this wave's
 // stage (32 x CONV_STAGE_LD floats) into the matrix-core C layout (lane l,
 // register r of tile (rb, cb) is C[(r/4)*8 + (l/32)*4 + r%4][l % 32]). Rows
 // at or past M read row M - 1; the epilogue never stores them.
-template<typename T, int RB, int CB>
+template<typename T, int RB, int CB, int RBATCH = RB>
 __device__ __forceinline__ void residualToAcc(floatx16 (&acc)[RB][CB], const T* __restrict__ residual, int ldRes, int mBase,
                                               int nBase, int M, float* stage) {
   constexpr int RV = 16 * (int)sizeof(T) / 16;  // 16-byte vectors per 16 channels
+  static_assert(RB % RBATCH == 0, "row blocks are loaded RBATCH at a time");
   const int lane = threadIdx.x & 63;
   const int half = lane & 1;
   const int lrow = lane >> 1;
   const int laneRow = lane & 31;
-  uint4 raw[RB][CB][RV];
 #pragma unroll
-  for(int rb = 0; rb < RB; rb++) {
-    int m = mBase + rb * 32 + lrow;
+  for(int rb0 = 0; rb0 < RB; rb0 += RBATCH) {
+  uint4 raw[RBATCH][CB][RV];
+#pragma unroll
+  for(int rr = 0; rr < RBATCH; rr++) {
+    int m = mBase + (rb0 + rr) * 32 + lrow;
     m = m < M ? m : M - 1;
 #pragma unroll
     for(int cb = 0; cb < CB; cb++) {
       const uint4* rp = (const uint4*)(residual + (size_t)m * ldRes + nBase + cb * 32 + half * 16);
 #pragma unroll
-      for(int q = 0; q < RV; q++) raw[rb][cb][q] = rp[q];
+      for(int q = 0; q < RV; q++) raw[rr][cb][q] = rp[q];
     }
   }
 #pragma unroll
-  for(int rb = 0; rb < RB; rb++)
+  for(int rr = 0; rr < RBATCH; rr++)
 #pragma unroll
     for(int cb = 0; cb < CB; cb++) {
-      const T* hv = (const T*)raw[rb][cb];
+      const int rb = rb0 + rr;
+      const T* hv = (const T*)raw[rr][cb];
       asm volatile("" ::: "memory");
 #pragma unroll
       for(int q = 0; q < 4; q++) {
@@ -218,6 +244,7 @@ __device__ __forceinline__ void residualToAcc(floatx16 (&acc)[RB][CB], const T* 
 #pragma unroll
       for(int r = 0; r < 16; r++) acc[rb][cb][r] = stage[((r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * CONV_STAGE_LD + laneRow];
     }
+  }
   asm volatile("" ::: "memory");
 }
 
@@ -440,11 +467,13 @@ __device__ __forceinline__ int swizzled(int row, int group) { return row * 64 + 
 // logical group (l & 3) ^ swizzleTerm(row), independent of j.
 __device__ __forceinline__ int dmaLogicalGroup(int lane) { return (lane & 3) ^ swizzleTerm(lane >> 2); }
 
-// s_waitcnt vmcnt(n) (n < 16) leaving the other counters unconstrained.
+// s_waitcnt vmcnt(n) (n < 64) leaving the other counters unconstrained: the
+// gfx9 encoding keeps vmcnt bits 3:0 in imm[3:0] and bits 5:4 in imm[15:14],
+// expcnt in imm[6:4] and lgkmcnt in imm[11:8] (all-ones = no wait).
 template<int N>
 __device__ __forceinline__ void waitVmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0xF70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0xF70);
 }
 
 // Workgroup barrier without the memory fence of __syncthreads(), whose
@@ -466,9 +495,9 @@ __device__ __forceinline__ void barrierNoFence() {
 // and only the outputs touch memory here. The stage is private to the wave and a wave's LDS operations execute in order, so no
 // workgroup barrier is needed; the empty asm statements only keep the
 // compiler from reordering the stage accesses.
-template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU>
-__device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
-                                                  const ConvEpilogue<T>& epi) {
+template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, int ACT>
+__device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
+                                                     const ConvEpilogue<T>& epi) {
   constexpr int VEC = 16 / (int)sizeof(T);
   constexpr int RV = 16 / VEC;  // 16-byte vectors per lane per block
   const int lane = threadIdx.x & 63;
@@ -540,7 +569,7 @@ __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float
           if(actCols) {
             T o[8];
 #pragma unroll
-            for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], epi.actKind) * v[8 + j]);
+            for(int j = 0; j < 8; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j], ACT < 0 ? epi.actKind : ACT) * v[8 + j]);
             uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin) / 2);
 #pragma unroll
             for(int q = 0; q < RV / 2; q++) dst[q] = ((const uint4*)o)[q];
@@ -549,7 +578,8 @@ __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float
         else if(actCols) {
           T o[16];
 #pragma unroll
-          for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], epi.actKind) * msk[rb]);
+          for(int j = 0; j < 16; j++)
+            o[j] = kgh_from_float<T>(kgh_activate_fast(v[j] * aS[j] + aB[j], ACT < 0 ? epi.actKind : ACT) * msk[rb]);
           uint4* dst = (uint4*)(epi.outAct + (size_t)m * epi.ldAct + (c0 - epi.actBegin));
 #pragma unroll
           for(int q = 0; q < RV; q++) dst[q] = ((const uint4*)o)[q];
@@ -559,9 +589,29 @@ __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float
   }
 }
 
+// ACT_FIXED instantiates the epilogue per activation kind (no per-element
+// branch on the kind); kernels with no registers to spare keep one body that
+// selects the activation at run time (KGH_ACT_DYNAMIC).
+constexpr int KGH_ACT_DYNAMIC = -1;
+template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, bool ACT_FIXED = true>
+__device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
+                                                  const ConvEpilogue<T>& epi) {
+  if constexpr(ACT_FIXED) {
+    withActKind(epi.actKind, epi.outAct != nullptr, [&](auto actTag) {
+      storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, GLU, decltype(actTag)::value>(acc, stage, mBase, nBase, M, HW, epi);
+    });
+  }
+  else {
+    storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, GLU, KGH_ACT_DYNAMIC>(acc, stage, mBase, nBase, M, HW, epi);
+  }
+}
+
 // RW row-waves by two column-waves: RW = 4 gives 8 waves of 96 x BN/2,
 // RW = 6 gives 12 waves of 64 x BN/2 (three per SIMD for latency hiding).
-template<int BN, int RW>
+// NB weight buffers: the weights of step s + NB - 1 are requested during step
+// s and waited for at the end of step s + NB - 4, so each weight DMA has
+// NB - 3 steps to land.
+template<int BN, int RW, int NB>
 __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
                                                                      int cout, const half_t* __restrict__ w, BoardGeom g,
                                                                      ConvEpilogue<half_t> epi) {
@@ -572,11 +622,13 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
   constexpr int RB = WTM / 32;
   constexpr int CB = WTN / 32;
   static_assert(WTN % 32 == 0, "wave tile must be a multiple of 32 columns");
-  // Waves 0-3 stream the weights (B_PER 1 KB wave-loads each per step, three
-  // steps ahead into four buffers); the other waves stream the next chunk's
-  // window (W_PER wave-loads each, spread over taps 0..4 of the current
-  // chunk). Each wave waits only on its own kind of load, with exact vmcnt
-  // counts.
+  // Waves 0-3 stream the weights (B_PER 1 KB wave-loads each per step,
+  // NB - 1 steps ahead into NB buffers); the other waves stream the next
+  // chunk's window (W_PER wave-loads each, spread over taps 0..4 of the
+  // current chunk). Each wave waits only on its own kind of load, with exact
+  // vmcnt counts.
+  static_assert(NB == 4 || NB == 6 || NB == 8, "weight buffer count");
+  constexpr int LOOKAHEAD = NB - 1;
   constexpr int B_PER = BN / 16 / 4;
   static_assert(B_PER * 64 == BN, "weights split evenly over four waves");
   constexpr int W_LOADERS = WAVES - 4;
@@ -584,15 +636,26 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
   static_assert(W_PER <= 8, "window loads fit before the tap-7 wait");
   __shared__ __attribute__((aligned(1024))) unsigned char win0[TW_WIN_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char win1[TW_WIN_BYTES];
+  // Separate arrays, each addressed at compile time, so the compiler never
+  // makes a fragment read wait for DMA into another buffer.
   __shared__ __attribute__((aligned(1024))) unsigned char wt0[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char wt1[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char wt2[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char wt3[BN * 64];
-  __shared__ __attribute__((aligned(16))) float stage[WAVES * 32 * CONV_STAGE_LD];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt4[NB > 4 ? BN * 64 : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt5[NB > 4 ? BN * 64 : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt6[NB > 6 ? BN * 64 : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt7[NB > 6 ? BN * 64 : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // The epilogue's per-wave accumulator stage (32 x CONV_STAGE_LD floats)
+  // lives in the window buffers, which are idle before the first window DMA
+  // and after the K loop: waves 0-5 in win0, 6-11 in win1.
+  constexpr int STAGE_BYTES = 32 * CONV_STAGE_LD * 4;
+  static_assert(6 * STAGE_BYTES <= TW_WIN_BYTES && WAVES <= 12, "stage fits in the windows");
+  float* stage = (float*)((wave < 6 ? win0 : win1) + (wave < 6 ? wave : wave - 6) * STAGE_BYTES);
   const bool weightWave = wave < 4;
   const int loaderIdx = weightWave ? wave : wave - 4;
   const int wm = wave / WN;
@@ -680,7 +743,8 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
   // The residual (if any) starts the accumulators.
   floatx16 acc[RB][CB];
   if(epi.residual != nullptr) {
-    residualToAcc<half_t, RB, CB>(acc, epi.residual, epi.ldRes, m0 + wm * WTM, n0 + wn * WTN, M, stage + wave * 32 * CONV_STAGE_LD);
+    residualToAcc<half_t, RB, CB>(acc, epi.residual, epi.ldRes, m0 + wm * WTM, n0 + wn * WTN, M, stage);
+    __syncthreads();  // every stage read done before the window DMA overwrites it
   }
   else {
 #pragma unroll
@@ -712,12 +776,15 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
       for(int cb = 0; cb < CB; cb++) acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[rb], b[cb], acc[rb][cb], 0, 0, 0);
   };
 
-  // Prologue: weights of steps 0..2 (0 and 1 landed), window of chunk 0.
+  auto wtBuf = [&](int i) -> unsigned char* {
+    i %= NB;
+    return i == 0 ? wt0 : i == 1 ? wt1 : i == 2 ? wt2 : i == 3 ? wt3 : i == 4 ? wt4 : i == 5 ? wt5 : i == 6 ? wt6 : wt7;
+  };
+  // Prologue: weights of steps 0..NB-2 (0 and 1 landed), window of chunk 0.
   if(weightWave) {
-    loadWeights(wt0, 0);
-    loadWeights(wt1, 1);
-    loadWeights(wt2, 2);
-    waitVmcnt<B_PER>();
+#pragma unroll
+    for(int s = 0; s < LOOKAHEAD; s++) loadWeights(wtBuf(s), s);
+    waitVmcnt<(LOOKAHEAD - 2) * B_PER>();
   }
   else {
 #pragma unroll
@@ -732,17 +799,14 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
     readHalf(win0, wt0, rows0, 0, 0);
   }
 
-  // Step s = 9c + t uses weight buffer s % 4 = (c + t) % 4 (9 = 1 mod 4), so
-  // the chunk loop is unrolled by four and P = c % 4 is a constant. During
-  // step s: DMA the weights of step s + 3 and parts of the next chunk's
-  // window; read the second half-step fragments of s, then (after the first
-  // half's matrix work) the first half-step fragments of s + 1, whose
+  // Step s = 9c + t uses weight buffer s % NB = (P + t) % NB with
+  // P = 9c % NB, which repeats every PERIOD chunks (4 for NB = 4 and 8, 2 for
+  // NB = 6), so the chunk loop is unrolled by PERIOD and P is a constant.
+  // During step s: DMA the weights of step s + NB - 1 and parts of the next
+  // chunk's window; read the second half-step fragments of s, then (after the
+  // first half's matrix work) the first half-step fragments of s + 1, whose
   // weights landed before the previous barrier; the barrier that ends step s
   // publishes the weights of step s + 2.
-  auto wtBuf = [&](int i) -> unsigned char* {
-    i &= 3;
-    return i == 0 ? wt0 : i == 1 ? wt1 : i == 2 ? wt2 : wt3;
-  };
   auto chunk = [&](auto pTag, int c) {
     constexpr int P = decltype(pTag)::value;
     unsigned char* cur = (P & 1) ? win1 : win0;
@@ -759,7 +823,7 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
 #pragma unroll
     for(int t = 0; t < 9; t++) {
       const unsigned char* wCur = wtBuf(P + t);
-      if(weightWave) loadWeights(wtBuf(P + t + 3), 9 * c + t + 3);
+      if(weightWave) loadWeights(wtBuf(P + t + LOOKAHEAD), 9 * c + t + LOOKAHEAD);
       else if(moreChunks) {
 #pragma unroll
         for(int i = 0; i < W_PER; i++)
@@ -782,22 +846,290 @@ __global__ __launch_bounds__(RW * 2 * 64, 1) void convTapWindowKernel(const half
       if(t < 8) readHalf(cur, wtBuf(P + t + 1), rowsC, t + 1, 0);
       else readHalf(nxt, wtBuf(P + t + 1), rowsC, 0, 0);
       mma(a1, b1);
-      if(weightWave) waitVmcnt<B_PER>();
+      if(weightWave) waitVmcnt<(LOOKAHEAD - 2) * B_PER>();
       else if(t == 7) waitVmcnt<0>();  // next chunk's window complete before step t = 8 reads it
       barrierNoFence();
     }
   };
 
-  for(int c = 0; c < cChunks; c += 4) {
-    chunk(std::integral_constant<int, 0>(), c);
-    if(c + 1 < cChunks) chunk(std::integral_constant<int, 1>(), c + 1);
-    if(c + 2 < cChunks) chunk(std::integral_constant<int, 2>(), c + 2);
-    if(c + 3 < cChunks) chunk(std::integral_constant<int, 3>(), c + 3);
+  constexpr int PERIOD = NB == 6 ? 2 : NB;  // NB / gcd(9, NB)
+  static_assert((9 * PERIOD) % NB == 0, "buffer pattern repeats after PERIOD chunks");
+  auto phase = [&](auto jTag, int c) {
+    constexpr int J = decltype(jTag)::value;
+    if(J < PERIOD && c + J < cChunks) chunk(std::integral_constant<int, (9 * J) % NB>(), c + J);
+  };
+  for(int c = 0; c < cChunks; c += PERIOD) {
+    phase(std::integral_constant<int, 0>(), c);
+    phase(std::integral_constant<int, 1>(), c);
+    if constexpr(PERIOD > 2) {
+      phase(std::integral_constant<int, 2>(), c);
+      phase(std::integral_constant<int, 3>(), c);
+    }
+    if constexpr(PERIOD > 4) {
+      phase(std::integral_constant<int, 4>(), c);
+      phase(std::integral_constant<int, 5>(), c);
+      phase(std::integral_constant<int, 6>(), c);
+      phase(std::integral_constant<int, 7>(), c);
+    }
   }
   waitVmcnt<0>();
   __syncthreads();
 
-  storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, epi);
+  storeWaveEpilogue<half_t, RB, CB, true, false, false>(acc, stage, m0 + wm * WTM, n0 + wn * WTN, M, HW, epi);
+}
+
+// ---------------------------------------------------------------------------
+// 3x3 fp16 convolution over 19x19 boards for large batches: one board per
+// workgroup (384 matrix rows: the 361 positions and 23 unused) and BN output
+// channels. Eight wave64s, two per SIMD: wave w owns rows 96 (w % 4).. of the
+// board and columns (w / 4) * BN/2.. (3 x BN/64 blocks of 32x32 on
+// v_mfma_f32_32x32x16_f16, 144 accumulators at BN = 192). Waves 0-3 DMA the
+// weights, waves 4-7 the windows.
+//
+// Per 32-channel chunk the board is staged in LDS as a zero-bordered 21 x 21
+// window with 80 bytes per position (64 bytes of channels, a 16-byte gap):
+//  * the A operand of tap (dy, dx) for position (y, x) is window position
+//    (y + 1 + dy) * 21 + (x + 1 + dx), a compile-time byte offset from the
+//    lane's base address, and taps that leave the board read the zero border,
+//    so the K loop needs no masking and no address arithmetic;
+//  * a 16-lane ds_read_b128 phase over 16 consecutive positions p starts at
+//    bank 20 p mod 64, which runs through all sixteen 4-bank groups, so the
+//    reads are conflict-free without a swizzle.
+// Every slot of the window is DMA'd each chunk: board positions from the
+// input, border positions and gaps from kZeroChannels.
+//
+// Measured on MI355X (C2 192->192, batch 256): the kernel matches the
+// tap-window kernel's K loop and removes its masking; what remains is the
+// epilogue's activation math and stores (~15 us of ~70 us, one tile per CU
+// leaves nothing to overlap it with) and LDS contention between fragment
+// reads and DMA writes.
+constexpr int BW_SIDE = 19;
+constexpr int BW_HW = BW_SIDE * BW_SIDE;
+constexpr int BW_PSIDE = BW_SIDE + 2;
+constexpr int BW_ROWS = BW_PSIDE * BW_PSIDE;  // 441 window positions
+constexpr int BW_ROW_BYTES = 80;
+constexpr int BW_ROW_WAVES = 4;                        // row blocks of 96; also the number of DMA waves of each kind
+constexpr int BW_THREADS = 64 * 2 * BW_ROW_WAVES;
+constexpr int BW_WIN_PER = 9;                          // window wave-loads per window wave per chunk
+constexpr int BW_LOADS = BW_ROW_WAVES * BW_WIN_PER;    // 36 KB >= 441 * 80 bytes
+static_assert(BW_LOADS * 1024 >= BW_ROWS * BW_ROW_BYTES, "window covers the board");
+constexpr int BW_WIN_BYTES = BW_LOADS * 1024;
+constexpr int BW_BM = 384;
+constexpr int BW_WTM = BW_BM / BW_ROW_WAVES;           // 96 rows per wave
+constexpr int BW_MAX_CIN = 1024;
+constexpr int BW_WEIGHT_BUFS = 6;
+
+// Zero source of the window's border and gap slots (zero-initialised at load;
+// never written). Long enough for every chunk offset up to BW_MAX_CIN.
+__device__ __attribute__((aligned(256))) half_t kZeroChannels[BW_MAX_CIN + 64];
+
+// Tap at which window load i (0..8) of a window wave is issued (taps 0..5).
+__host__ __device__ constexpr int winLoadTap(int i) { return i * 6 / BW_WIN_PER; }
+
+template<int BN>
+__global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
+                                                                      int cout, const half_t* __restrict__ w, int batch,
+                                                                      ConvEpilogue<half_t> epi) {
+  constexpr int WTN = BN / 2;
+  constexpr int RB = BW_WTM / 32;
+  constexpr int CB = WTN / 32;
+  static_assert(WTN % 32 == 0, "wave tile must be a multiple of 32 columns");
+  constexpr int B_PER = BN / 16 / 4;
+  static_assert(B_PER * 64 == BN, "weights split evenly over four waves");
+  // Separate arrays, each addressed at compile time, so the compiler never
+  // makes a fragment read wait for DMA into another buffer. The weight
+  // buffers are declared first so that they sit in the low 64 KB, where
+  // their base addresses fit the 16-bit offset field of ds_read.
+  __shared__ __attribute__((aligned(1024))) unsigned char wt0[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt1[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt2[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt3[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt4[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt5[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char win0[BW_WIN_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char win1[BW_WIN_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // The accumulator stage of the residual load and the epilogue (32 x
+  // CONV_STAGE_LD floats per wave) lives in win0 while the windows are idle.
+  constexpr int STAGE_BYTES = 32 * CONV_STAGE_LD * 4;
+  static_assert(2 * BW_ROW_WAVES * STAGE_BYTES <= BW_WIN_BYTES, "stage fits in a window");
+  float* stage = (float*)(win0 + wave * STAGE_BYTES);
+  const int wm = wave & 3;   // row block of 96
+  const int wn = wave >> 2;  // column half
+  const int loader = wave & 3;
+  const bool loadsWeights = wave < 4;
+  const bool loadsWindow = wave >= 4;
+  int board, colTile;
+  rowColTile(cout / BN, board, colTile);
+  const int m0 = board * BW_HW;
+  const int mEnd = m0 + BW_HW;
+  const int n0 = colTile * BN;
+  const int laneRow = lane & 31;
+  const int kq = lane >> 5;
+  const int cChunks = cinPad / 32;
+  const int steps = 9 * cChunks;
+  const int tapStride = cout * cinPad;
+
+  // Window load i of this wave fills LDS bytes [1024 j, 1024 j + 1024),
+  // j = wave + 4 i: lane l writes slot q = 64 j + l, which is 16-byte group
+  // q % 5 of window position q / 5. Element offsets into x are 32-bit: the
+  // host keeps tensors below 2^31 elements.
+  const half_t* winPtr[BW_WIN_PER];
+#pragma unroll
+  for(int i = 0; i < BW_WIN_PER; i++) {
+    const int q = 64 * (loader + BW_ROW_WAVES * i) + lane;
+    const int pos = q / 5;
+    const int grp = q - 5 * pos;
+    const int py = pos / BW_PSIDE;
+    const int px = pos - BW_PSIDE * py;
+    const bool onBoard = grp < 4 && py >= 1 && py <= BW_SIDE && px >= 1 && px <= BW_SIDE;
+    winPtr[i] = onBoard ? x + ((m0 + (py - 1) * BW_SIDE + (px - 1)) * cinStride + grp * 8) : kZeroChannels;
+  }
+  auto loadWindow = [&](unsigned char* dst, int c, int i) {
+    __builtin_amdgcn_global_load_lds((const void*)(winPtr[i] + c * 32), (lds_void_t*)(dst + (loader + BW_ROW_WAVES * i) * 1024),
+                                     16, 0, 0);
+  };
+  // Weight wave-load i of this wave covers rows 16 (wave * B_PER + i) .. +15
+  // of the swizzled 64-byte-row weight buffer. Steps past the end re-read the
+  // last step (valid addresses) into a buffer nobody reads again, so the
+  // vmcnt counts stay constant.
+  const int dRow = lane >> 2;
+  const int dGroup = dmaLogicalGroup(lane);
+  const int wtSrc = (n0 + 16 * loader * B_PER + dRow) * cinPad + dGroup * 8;
+  auto loadWeights = [&](unsigned char* dst, int s) {
+    s = s < steps ? s : steps - 1;
+    const int c = s / 9;
+    const int t = s - 9 * c;
+#pragma unroll
+    for(int i = 0; i < B_PER; i++)
+      __builtin_amdgcn_global_load_lds((const void*)(w + t * tapStride + wtSrc + i * 16 * cinPad + c * 32),
+                                       (lds_void_t*)(dst + (loader * B_PER + i) * 1024), 16, 0, 0);
+  };
+  auto wtBuf = [&](int i) -> unsigned char* {
+    i %= BW_WEIGHT_BUFS;
+    return i == 0 ? wt0 : i == 1 ? wt1 : i == 2 ? wt2 : i == 3 ? wt3 : i == 4 ? wt4 : wt5;
+  };
+
+  // Byte offset of the lane's A rows at tap (dy, dx) = (-1, -1); rows past
+  // the board's 361 positions read position 0 and are discarded.
+  int aBase[RB];
+#pragma unroll
+  for(int rb = 0; rb < RB; rb++) {
+    const int i = wm * BW_WTM + rb * 32 + laneRow;
+    const int pos = i < BW_HW ? (i / BW_SIDE + 1) * BW_PSIDE + (i % BW_SIDE + 1) : BW_PSIDE + 1;
+    aBase[rb] = (pos - BW_PSIDE - 1) * BW_ROW_BYTES + kq * 16;
+  }
+  // Weight fragment of column block cb, half step ks: the swizzle term of
+  // row cb * 32 + laneRow does not depend on cb, so the address is
+  // bBase[ks] + cb * 2048 with the block offset as an immediate.
+  int bBase[2];
+#pragma unroll
+  for(int ks = 0; ks < 2; ks++) bBase[ks] = swizzled(wn * WTN + laneRow, ks * 2 + kq);
+
+  // The residual (if any) starts the accumulators; its stage lives in win0,
+  // so every wave is past it before the window DMA starts.
+  floatx16 acc[RB][CB];
+  if(epi.residual != nullptr) {
+    residualToAcc<half_t, RB, CB, 1>(acc, epi.residual, epi.ldRes, m0 + wm * BW_WTM, n0 + wn * WTN, mEnd, stage);
+    __syncthreads();
+  }
+  else {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++)
+#pragma unroll
+        for(int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+  }
+  // Prologue: weights of steps 0..2 and the window of chunk 0.
+  if(loadsWeights) {
+    loadWeights(wt0, 0);
+    loadWeights(wt1, 1);
+    loadWeights(wt2, 2);
+  }
+  if(loadsWindow) {
+#pragma unroll
+    for(int i = 0; i < BW_WIN_PER; i++) loadWindow(win0, 0, i);
+  }
+  waitVmcnt<0>();
+  barrierNoFence();
+
+  half8_t af[RB], bf[CB];
+  auto readHalf = [&](const unsigned char* winBuf, const unsigned char* wtBuf, int t, int ks) {
+    const int off = ((t / 3) * BW_PSIDE + t % 3) * BW_ROW_BYTES + ks * 32;
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++) af[rb] = *(const half8_t*)(winBuf + aBase[rb] + off);
+#pragma unroll
+    for(int cb = 0; cb < CB; cb++) bf[cb] = *(const half8_t*)(wtBuf + bBase[ks] + cb * 2048);
+  };
+  auto mma = [&](const half8_t (&a)[RB], const half8_t (&b)[CB]) {
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++) acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[rb], b[cb], acc[rb][cb], 0, 0, 0);
+  };
+  readHalf(win0, wt0, 0, 0);
+
+  // Step s = 9c + t uses weight buffer s % 6 = (3c + t) % 6 and window c % 2,
+  // a pattern that repeats every two chunks: the chunk loop body is one pair
+  // of chunks (cinPad is a multiple of 64), so there is a single loop body
+  // and the accumulators keep their registers. During step s: DMA the weights
+  // of step s + 3 and parts of the next chunk's window; read the second
+  // half-step fragments of s, then (after the first half's matrix work) the
+  // first half-step fragments of s + 1, whose weights landed before the
+  // previous barrier; the barrier that ends step s publishes the weights of
+  // step s + 2.
+  auto chunk = [&](auto pTag, int c) {
+    constexpr int P = decltype(pTag)::value;  // 3 * (c % 2)
+    unsigned char* cur = P ? win1 : win0;
+    unsigned char* nxt = P ? win0 : win1;
+    // The last chunk re-loads itself into the idle window (never read), so
+    // every step issues the same loads.
+    const int cNext = c + 1 < cChunks ? c + 1 : c;
+#pragma unroll
+    for(int t = 0; t < 9; t++) {
+      const unsigned char* wCur = wtBuf(P + t);
+      if(loadsWeights) loadWeights(wtBuf(P + t + 3), 9 * c + t + 3);
+      if(loadsWindow) {
+#pragma unroll
+        for(int i = 0; i < BW_WIN_PER; i++)
+          if(winLoadTap(i) == t) loadWindow(nxt, cNext, i);
+      }
+      half8_t a0[RB], b0[CB];
+#pragma unroll
+      for(int rb = 0; rb < RB; rb++) a0[rb] = af[rb];
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++) b0[cb] = bf[cb];
+      readHalf(cur, wCur, t, 1);
+      mma(a0, b0);
+      half8_t a1[RB], b1[CB];
+#pragma unroll
+      for(int rb = 0; rb < RB; rb++) a1[rb] = af[rb];
+#pragma unroll
+      for(int cb = 0; cb < CB; cb++) b1[cb] = bf[cb];
+      // First half of step s + 1 (past the last step it re-reads valid LDS
+      // and is discarded).
+      if(t < 8) readHalf(cur, wtBuf(P + t + 1), t + 1, 0);
+      else readHalf(nxt, wtBuf(P + t + 1), 0, 0);
+      mma(a1, b1);
+      // Weight waves: only the weights of step s + 3 may still be in flight.
+      // Window waves: the next window is complete before step t = 8 reads it.
+      if(loadsWeights) waitVmcnt<B_PER>();
+      else if(t == 7) waitVmcnt<0>();
+      barrierNoFence();
+    }
+  };
+  for(int c = 0; c < cChunks; c += 2) {
+    chunk(std::integral_constant<int, 0>(), c);
+    chunk(std::integral_constant<int, 3>(), c + 1);
+  }
+  waitVmcnt<0>();
+  __syncthreads();
+
+  storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage, m0 + wm * BW_WTM, n0 + wn * WTN, mEnd, BW_HW, epi);
 }
 
 // ---------------------------------------------------------------------------
@@ -1021,13 +1353,32 @@ void launchMfma(const T* x, int cinStride, int cinPad, int cout, const T* w, Boa
 
 constexpr int TW_ROW_WAVES = 6;  // 12 wave64s, three per SIMD: ~5% faster than 8 (sustained-clock measurement)
 
-template<int BN, int RW = TW_ROW_WAVES>
+constexpr int TW_WEIGHT_BUFFERS = 4;
+
+template<int BN, int RW = TW_ROW_WAVES, int NB = TW_WEIGHT_BUFFERS>
 void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                      const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   int M = g.batch * g.H * g.W;
   dim3 grid((M + TW_BM - 1) / TW_BM * (cout / BN));
-  hipLaunchKernelGGL((convTapWindowKernel<BN, RW>), grid, dim3(RW * 2 * 64), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  hipLaunchKernelGGL((convTapWindowKernel<BN, RW, NB>), grid, dim3(RW * 2 * 64), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
   KGH_CHECK_LAUNCH();
+}
+
+template<int BN>
+void launchBoardWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                       const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  dim3 grid(g.batch * (cout / BN));
+  hipLaunchKernelGGL((convBoardWindowKernel<BN>), grid, dim3(BW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g.batch, epi);
+  KGH_CHECK_LAUNCH();
+}
+
+// Shape conditions of the board kernel apart from batch size: 19x19 boards,
+// an even number of 32-channel chunks up to BW_MAX_CIN, 32-bit element
+// offsets, a plain residual.
+bool boardWindowFits(int cinStride, int cinPad, int cout, int bn, BoardGeom g, const ConvEpilogue<half_t>& epi) {
+  const long M = (long)g.batch * g.H * g.W;
+  return g.H == BW_SIDE && g.W == BW_SIDE && cinPad % 64 == 0 && cinPad <= BW_MAX_CIN && cinStride % 8 == 0 &&
+         !epi.maskResidualAdd && !epi.glu && cout % bn == 0 && M * cinStride < (1L << 31) && 9L * cout * cinPad < (1L << 31);
 }
 
 // Shape conditions of the window kernel apart from batch size.
@@ -1049,6 +1400,13 @@ template<>
 bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                                const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   const long M = (long)g.batch * g.H * g.W;
+  // One board per workgroup: enough boards to fill most CUs.
+  if(g.batch >= 128 && boardWindowFits(cinStride, cinPad, cout, 64, g, epi)) {
+    if(cout % 192 == 0) launchBoardWindow<192>(x, cinStride, cinPad, cout, w, g, epi, stream);
+    else if(cout % 128 == 0) launchBoardWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream);
+    else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+    return true;
+  }
   if(g.W + 1 > TW_PAD_MAX || cinPad % 32 != 0 || cinStride % 8 != 0 || epi.maskResidualAdd) return false;
   if(M < 128L * TW_BM) return false;
   if(M * cinStride >= (1L << 31) || 9L * cout * cinPad >= (1L << 31)) return false;
@@ -1108,6 +1466,9 @@ bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g
       if(v == CONV_TW_192 || v == CONV_TW8_192) return tapWindowFits(cinStride, cinPad, cout, 192, g, epi);
       if(v == CONV_TW_128) return tapWindowFits(cinStride, cinPad, cout, 128, g, epi);
       if(v == CONV_TW_64) return tapWindowFits(cinStride, cinPad, cout, 64, g, epi);
+      if(v == CONV_BOARD_192) return boardWindowFits(cinStride, cinPad, cout, 192, g, epi);
+      if(v == CONV_BOARD_128) return boardWindowFits(cinStride, cinPad, cout, 128, g, epi);
+      if(v == CONV_BOARD_64) return boardWindowFits(cinStride, cinPad, cout, 64, g, epi);
     }
     else {
       if(v == CONV_DMA1_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
@@ -1136,7 +1497,7 @@ void launchTileVariant(int v, const T* x, int cinStride, int cinPad, int cout, c
 template<typename T>
 void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cout, const T* w, BoardGeom g,
                    const ConvEpilogue<T>& epi, hipStream_t stream) {
-  if(v >= CONV_TILE_192) {
+  if(v >= CONV_TILE_192 && v <= CONV_TILE_32) {
     if(ky == 3) launchTileVariant<T, 3>(v, x, cinStride, cinPad, cout, w, g, epi, stream);
     else launchTileVariant<T, 1>(v, x, cinStride, cinPad, cout, w, g, epi, stream);
     return;
@@ -1147,6 +1508,9 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
       case CONV_TW_128: launchTapWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_TW_64: launchTapWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_TW8_192: launchTapWindow<192, 4>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_BOARD_192: launchBoardWindow<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_BOARD_128: launchBoardWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_BOARD_64: launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_192: launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_128: launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_64: launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
@@ -1179,7 +1543,7 @@ bool convMfmaSupported(int cinPad, int cout) {
 
 const char* convVariantName(int variant) {
   static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
-                                "tile192", "tile128", "tile96", "tile64", "tile32"};
+                                "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64"};
   return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
 }
 

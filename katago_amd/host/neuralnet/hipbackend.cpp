@@ -27,7 +27,7 @@
 #include "katago_hip.h"
 
 static const int HIP_TUNER_VERSION = 1;
-static const char* HIP_TUNER_VERSION_LINE = "VERSION=1";
+static const char* HIP_TUNER_VERSION_LINE = "VERSION=2";
 
 using std::string;
 using std::vector;

@@ -34,10 +34,10 @@ def test_tune_save_load_and_identical_results(model_dir, tmp_path):
     assert len(lines) >= 3  # the 3x3 trunk conv, the head 1x1s, ...
     for l in lines:
         f = l.split()
-        assert int(f[4]) == n * 361 and 0 <= int(f[8]) < 13  # M, variant id (0: built-in choice kept)
+        assert int(f[4]) == n * 361 and 0 <= int(f[8]) < 16  # M, variant id (0: built-in choice kept)
     files = glob.glob(os.path.join(home, "hiptuning", f"tune1_*_x19_y19_b{n}_fp16_arch*.txt"))
     assert len(files) == 1
-    assert open(files[0]).read().startswith("VERSION=1")
+    assert open(files[0]).read().startswith("VERSION=2")
 
     loaded = nn.ComputeHandle(nn.ComputeContext(lm, use_fp16=True, auto_tune=True, home_data_dir=home), max_batch=n)
     src2, table2 = loaded.tuning()
@@ -82,7 +82,7 @@ def test_every_kernel_variant_gives_identical_bits(model_dir, fp16):
     shapes = [l.split()[:8] for l in tuned.tuning()[1].splitlines() if l.strip()]
     assert shapes
     ref = _forward(nn.ComputeHandle(nn.ComputeContext(lm, use_fp16=fp16, auto_tune=False), max_batch=n), sp, gl)
-    for v in range(1, 13):
+    for v in range(1, 16):
         tuned.set_tuning("".join(" ".join(k) + f" {v}\n" for k in shapes))
         out = _forward(tuned, sp, gl)
         for k in out:
