@@ -61,13 +61,16 @@ __device__ __forceinline__ float kgh_activate(float x, int act) {
 
 // Fast forms used in kernel epilogues, from the identity
 //   tanh(log(1 + e^y)) = n / (n + 2),  n = e^y (e^y + 2),
-// so mish needs one exponential and one reciprocal. For y > 20 the factor is
-// 1 to fp32 precision (and n would overflow), as in the clamped reference
-// formula. Relative error against the formulas above is a few ulp.
+// so mish needs one exponential and one reciprocal. The exponent is clamped
+// at 20 as in the reference formula: there n = 2.4e17, n + 2 rounds to n and
+// the factor is 1 within one fp32 ulp (the reference's factor is exactly 1
+// there), so no separate branch for large y is needed; a NaN input stays NaN
+// through the caller's multiply by y. Relative error against the formulas
+// above is a few ulp.
 __device__ __forceinline__ float kgh_tanh_softplus_fast(float y) {
   float e = __expf(fminf(y, 20.0f));
   float n = e * (e + 2.0f);
-  return y > 20.0f ? 1.0f : n * __builtin_amdgcn_rcpf(n + 2.0f);
+  return n * __builtin_amdgcn_rcpf(n + 2.0f);
 }
 
 __device__ __forceinline__ float kgh_activate_fast(float x, int act) {

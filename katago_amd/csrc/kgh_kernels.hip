@@ -124,15 +124,31 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
     }
     if(pg < PG) {
       const T* base = g + (size_t)n * HW * ld + (cg0 + cgl) * VEC;
-      for(int p = pg; p < HW; p += PG) {
-        T v[VEC];
-        *(uint4*)v = *(const uint4*)(base + (size_t)p * ld);
-        const float mk = mask[(size_t)n * HW + p] - 1.0f;
+      // Four positions per iteration, loaded before any is used: with one
+      // block per board the loop is bound by memory latency, not bandwidth.
+      // The positions combine in the same order as a one-at-a-time loop.
+      constexpr int U = 4;
+      for(int p0 = pg; p0 < HW; p0 += U * PG) {
+        T v[U][VEC];
+        float mk[U];
 #pragma unroll
-        for(int j = 0; j < VEC; j++) {
-          const float f = kgh_to_float(v[j]);
-          sm[j] += f;
-          mx[j] = fmaxf(mx[j], f + mk);
+        for(int u = 0; u < U; u++) {
+          const int p = p0 + u * PG;
+          if(p < HW) {
+            *(uint4*)v[u] = *(const uint4*)(base + (size_t)p * ld);
+            mk[u] = mask[(size_t)n * HW + p] - 1.0f;
+          }
+        }
+#pragma unroll
+        for(int u = 0; u < U; u++) {
+          if(p0 + u * PG < HW) {
+#pragma unroll
+            for(int j = 0; j < VEC; j++) {
+              const float f = kgh_to_float(v[u][j]);
+              sm[j] += f;
+              mx[j] = fmaxf(mx[j], f + mk[u]);
+            }
+          }
         }
       }
 #pragma unroll
@@ -182,6 +198,9 @@ __global__ void poolVecKernel(const T* __restrict__ g, int ldG, int C, const flo
   if(Wt != nullptr) {
     for(int co = threadIdx.x; co < cout; co += blockDim.x) {
       float acc = 0.0f;
+      // Unrolled so that several weight loads are in flight at once (the sum
+      // order is unchanged).
+#pragma unroll 8
       for(int i = 0; i < 3 * C; i++) acc += pooled[i] * Wt[(size_t)i * cout + co];
       out[(size_t)n * ldOut + co] = acc;
     }
@@ -296,9 +315,10 @@ __global__ void bnActVecKernel(const T* __restrict__ x, int ldX, T* __restrict__
 // Per-position part of the heads: policy = p2Conv(act(p1BN(p1 + g1Bias)) * mask),
 // ownership = ownershipConv(v1). 16-byte loads of the p1 and v1 rows when the
 // channel counts and strides allow.
-template<typename T>
+template<typename T, int ACT>
 __global__ void headSpatialKernel(HeadSpatialArgs<T> a) {
   constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int MAX_PC = 4;  // policy channels: 1, 2 or 4 (desc.cpp:1922-1934)
   int m = blockIdx.x * blockDim.x + threadIdx.x;
   if(m >= a.M) return;
   int n = m / a.HW;
@@ -315,19 +335,25 @@ __global__ void headSpatialKernel(HeadSpatialArgs<T> a) {
 #pragma unroll
       for(int j = 0; j < VEC; j++) {
         const int c = c0 + j;
-        const float act = kgh_activate((kgh_to_float(v[j]) + gb[c]) * a.p1Scale[c] + a.p1Bias[c], a.p1Act) * msk;
-        for(int pc = 0; pc < a.policyC; pc++) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
+        const float act = kgh_activate_fast((kgh_to_float(v[j]) + gb[c]) * a.p1Scale[c] + a.p1Bias[c], ACT) * msk;
+#pragma unroll
+        for(int pc = 0; pc < MAX_PC; pc++)
+          if(pc < a.policyC) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
       }
     }
   }
   else {
     for(int c = 0; c < a.p1C; c++) {
       float v = kgh_to_float(p1[c]) + gb[c];
-      float act = kgh_activate(v * a.p1Scale[c] + a.p1Bias[c], a.p1Act) * msk;
-      for(int pc = 0; pc < a.policyC; pc++) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
+      float act = kgh_activate_fast(v * a.p1Scale[c] + a.p1Bias[c], ACT) * msk;
+#pragma unroll
+      for(int pc = 0; pc < MAX_PC; pc++)
+        if(pc < a.policyC) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
     }
   }
-  for(int pc = 0; pc < a.policyC; pc++) a.policy[(size_t)m * a.policyC + pc] = pol[pc];
+#pragma unroll
+  for(int pc = 0; pc < MAX_PC; pc++)
+    if(pc < a.policyC) a.policy[(size_t)m * a.policyC + pc] = pol[pc];
   const T* v1 = a.v1 + (size_t)m * a.ldV1;
   float own = 0.0f;
   if(vec) {
@@ -637,7 +663,15 @@ void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, 
 
 template<typename T>
 void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream) {
-  hipLaunchKernelGGL(headSpatialKernel<T>, dim3((a.M + 255) / 256), dim3(256), 0, stream, a);
+  if(a.policyC < 1 || a.policyC > 4) throw KghError(3, "policy head: 1 to 4 output channels supported");
+  const dim3 grid((a.M + 255) / 256), block(256);
+  switch(a.p1Act) {
+    case KGH_ACT_RELU: hipLaunchKernelGGL((headSpatialKernel<T, KGH_ACT_RELU>), grid, block, 0, stream, a); break;
+    case KGH_ACT_MISH: hipLaunchKernelGGL((headSpatialKernel<T, KGH_ACT_MISH>), grid, block, 0, stream, a); break;
+    case KGH_ACT_SILU: hipLaunchKernelGGL((headSpatialKernel<T, KGH_ACT_SILU>), grid, block, 0, stream, a); break;
+    case KGH_ACT_MISH_SCALE8: hipLaunchKernelGGL((headSpatialKernel<T, KGH_ACT_MISH_SCALE8>), grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL((headSpatialKernel<T, KGH_ACT_IDENTITY>), grid, block, 0, stream, a); break;
+  }
   KGH_CHECK_LAUNCH();
 }
 
