@@ -272,6 +272,23 @@ def test_c2_full_batch_rows_are_independent(model_dir):
         assert np.isfinite(full[k]).all()
 
 
+def test_c1_batch_128_rows_are_independent(model_dir):
+    """b10c128 at 128 boards (19x19 and 13x13, all eight symmetries) runs its
+    3x3 convs on the one-board kernel (128 output channels); the same rows in
+    a batch of 4 take the 128-row tile kernels: bitwise equal."""
+    cfg = modelgen.configs()[1]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=True)
+    h = nn.ComputeHandle(ctx, max_batch=128)
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, 128, board_sizes=(19, 13))
+    full = h.get_output(sp, gl, symmetry=np.arange(128) % 8)
+    rows = [0, 5, 64, 127]
+    part = h.get_output(sp[rows], gl[rows], symmetry=np.array(rows) % 8)
+    for k in full:
+        assert np.array_equal(full[k][rows], part[k]), k
+        assert np.isfinite(full[k]).all()
+
+
 def test_graph_replays_match_eager_forwards(model_dir):
     """A repeated forward is captured into a HIP graph and replayed. Every
     replay, with eager work and synchronisations in between (a different
