@@ -264,7 +264,7 @@ def main():
     # Roofline kernel: the 3x3 conv for the convolutional nets, the 1x1
     # (per-position GEMM) kernel for a transformer trunk.
     if ms3 >= ms1:
-        ms_k, n_k, fl_k, kname = ms3, n3, fl3, "convBoardWindowKernel (3x3, fp16, one board per workgroup; stem: convTapWindowKernel)"
+        ms_k, n_k, fl_k, kname = ms3, n3, fl3, "convBoardWindowKernel (3x3, fp16, one board per workgroup, trunk and stem)"
     else:
         ms_k, n_k, fl_k, kname = ms1, n1, fl1, "conv1x1DmaKernel / convMfmaKernel (1x1 GEMM, fp16)"
     avg_ms = ms_k / max(n_k, 1)
