@@ -124,10 +124,12 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
     }
     if(pg < PG) {
       const T* base = g + (size_t)n * HW * ld + (cg0 + cgl) * VEC;
-      // Four positions per iteration, loaded before any is used: with one
-      // block per board the loop is bound by memory latency, not bandwidth.
-      // The positions combine in the same order as a one-at-a-time loop.
-      constexpr int U = 4;
+      // Twelve positions per iteration, loaded before any is used: with one
+      // block per board the loop is bound by memory latency, not bandwidth
+      // (at C = 64 and 256 threads, each thread's 11-12 positions take one
+      // round trip). The positions combine in the same order as a
+      // one-at-a-time loop.
+      constexpr int U = 12;
       for(int p0 = pg; p0 < HW; p0 += U * PG) {
         T v[U][VEC];
         float mk[U];
@@ -172,8 +174,11 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
 }
 
 // poolKernel with 16-byte loads spread over all threads (see poolBoardVec).
+// Launched with POOL_THREADS threads (the bound lets the unrolled loads keep
+// their registers).
+constexpr int POOL_THREADS = 256;
 template<typename T, bool VALUE_MODE>
-__global__ void poolVecKernel(const T* __restrict__ g, int ldG, int C, const float* __restrict__ mask,
+__global__ __launch_bounds__(POOL_THREADS) void poolVecKernel(const T* __restrict__ g, int ldG, int C, const float* __restrict__ mask,
                               const float* __restrict__ maskSum, int HW, float* __restrict__ pooledOut, int ldPooled,
                               const float* __restrict__ Wt, int cout, float* __restrict__ out, int ldOut) {
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -198,9 +203,9 @@ __global__ void poolVecKernel(const T* __restrict__ g, int ldG, int C, const flo
   if(Wt != nullptr) {
     for(int co = threadIdx.x; co < cout; co += blockDim.x) {
       float acc = 0.0f;
-      // Unrolled so that several weight loads are in flight at once (the sum
-      // order is unchanged).
-#pragma unroll 8
+      // Unrolled so that 32 weight loads are in flight at once (the sum order
+      // is unchanged): the loop is a chain of L2 round trips otherwise.
+#pragma unroll 32
       for(int i = 0; i < 3 * C; i++) acc += pooled[i] * Wt[(size_t)i * cout + co];
       out[(size_t)n * ldOut + co] = acc;
     }
@@ -597,7 +602,7 @@ void launchPool(const T* g, int ldG, int C, const float* mask, const float* mask
                 float* pooledOut, int ldPooled, const float* Wt, int cout, float* out, int ldOut, hipStream_t stream) {
   constexpr int VEC = 16 / (int)sizeof(T);
   if(C % VEC == 0 && ldG % VEC == 0 && ((uintptr_t)g & 15) == 0) {
-    const int threads = 256;
+    const int threads = POOL_THREADS;
     const size_t smem = (size_t)(5 * C + 2 * threads * VEC) * sizeof(float);
     if(valueMode)
       hipLaunchKernelGGL((poolVecKernel<T, true>), dim3(batch), dim3(threads), smem, stream, g, ldG, C, mask, maskSum, HW, pooledOut,
