@@ -913,10 +913,43 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
     e.actKind = hc.act.act;
     r.conv(hc.conv, r.A[0], net.trunkC, e);
   }
-  // Pooled head features per row (vectorised per-board pooling), then the
-  // small matmuls as row-parallel launches (eigenbackend.cpp:1980-2024,
-  // 2067-2102).
-  {
+  // Pooled head features and the small matmuls (eigenbackend.cpp:1980-2024,
+  // 2067-2102): one per-board launch when the shapes allow vector pooling,
+  // else pooling launches and row-parallel matmuls.
+  HeadVectorArgs<T> hv;
+  hv.gv = gv;
+  hv.ldGv = gvC;
+  hv.g1C = net.g1C;
+  hv.v1C = net.v1C;
+  hv.HW = HW;
+  hv.batch = n;
+  hv.mask = h->mask;
+  hv.maskSum = h->maskSum;
+  hv.g1W = net.gpoolToBiasMul.w;
+  hv.p1C = net.p1C;
+  hv.g1Bias = h->g1Bias;
+  hv.passW = net.passMul.w;
+  hv.passC = net.passMul2.w != nullptr ? net.passMul.cout : net.policyC;
+  hv.passB = net.passMul2.w != nullptr ? net.passBias.b : nullptr;
+  hv.passAct = net.passMul2.w != nullptr ? net.passAct : KGH_ACT_IDENTITY;
+  hv.pass2W = net.passMul2.w;
+  hv.policyC = net.policyC;
+  hv.pass = h->pass;
+  hv.v2W = net.v2Mul.w;
+  hv.v2C = net.v2Mul.cout;
+  hv.v2B = net.v2Bias.b;
+  hv.v2Act = net.v2Act;
+  hv.v3W = net.v3Mul.w;
+  hv.v3B = net.v3Bias.b;
+  hv.value = h->value;
+  hv.sv3W = net.sv3Mul.w;
+  hv.scoreC = net.scoreC;
+  hv.sv3B = net.sv3Bias.b;
+  hv.score = h->score;
+  if(kgh::headVectorApplies<T>(hv)) {
+    kgh::launchHeadVector<T>(hv, s);
+  }
+  else {
     const int ld = h->headFeatLd;
     float* gfeat = h->headFeat;
     float* vfeat = gfeat + 3 * net.g1C;

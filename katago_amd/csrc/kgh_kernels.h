@@ -23,6 +23,44 @@ struct HeadSpatialArgs {
   float* ownership;  // out [M]
 };
 
+// The per-board head vectors in one launch (eigenbackend.cpp:1980-2024,
+// 2067-2102): g1 and v1 pooled in one pass over the head conv output, then
+//   g1Bias = pool(g1) . g1W
+//   pass   = pool(g1) . passW                                (pass2W null)
+//          = act(pool(g1) . passW + passB) . pass2W          (otherwise)
+//   hidden = act(pool(v1) . v2W + v2B)
+//   value  = hidden . v3W + v3B,  score = hidden . sv3W + sv3B
+// Weights are input-major ([cin][cout]); each output sums in the order of
+// the row-parallel matmul kernel.
+template<typename T>
+struct HeadVectorArgs {
+  const T* gv;  // [M][ldGv]: activated g1 (g1C channels), then v1 (v1C)
+  int ldGv, g1C, v1C, HW, batch;
+  const float* mask;
+  const float* maskSum;
+  const float* g1W;
+  int p1C;
+  float* g1Bias;  // [batch][p1C]
+  const float* passW;
+  int passC;  // passW's outputs (policyC when pass2W is null)
+  const float* passB;
+  int passAct;
+  const float* pass2W;
+  int policyC;
+  float* pass;  // [batch][policyC]
+  const float* v2W;
+  int v2C;
+  const float* v2B;
+  int v2Act;
+  const float* v3W;
+  const float* v3B;
+  float* value;  // [batch][3]
+  const float* sv3W;
+  int scoreC;
+  const float* sv3B;
+  float* score;  // [batch][scoreC]
+};
+
 struct UnpackArgs {
   const float* policy;  // [M][policyC]
   const float* pass;    // [batch][policyC]
@@ -81,6 +119,13 @@ void launchBnAct(const T* x, int ldX, T* y, int ldY, int C, const float* scale, 
 
 template<typename T>
 void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream);
+
+// Whether launchHeadVector takes these shapes (vector loads over g1C + v1C
+// channels, LDS within the default limit).
+template<typename T>
+bool headVectorApplies(const HeadVectorArgs<T>& a);
+template<typename T>
+void launchHeadVector(const HeadVectorArgs<T>& a, hipStream_t stream);
 
 void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream);
 void launchPostprocess(const PostArgs& a, hipStream_t stream);

@@ -104,7 +104,7 @@ __global__ void rowMatmulKernel(const float* __restrict__ in, int ldIn, int cin,
 // part; thread t moves 16-byte channel groups of the positions
 // p = t / CG (mod threads / CG). red holds 2 * blockDim.x * VEC floats.
 // Requires C and ld multiples of the vector width and 16-byte rows.
-template<typename T>
+template<typename T, int U = 12>
 __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float* __restrict__ mask, int n, int HW, float* sums,
                              float* maxs, float* red) {
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -124,12 +124,11 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
     }
     if(pg < PG) {
       const T* base = g + (size_t)n * HW * ld + (cg0 + cgl) * VEC;
-      // Twelve positions per iteration, loaded before any is used: with one
+      // U positions per iteration, loaded before any is used: with one
       // block per board the loop is bound by memory latency, not bandwidth
-      // (at C = 64 and 256 threads, each thread's 11-12 positions take one
-      // round trip). The positions combine in the same order as a
-      // one-at-a-time loop.
-      constexpr int U = 12;
+      // (at C = 64 and 256 threads, U = 12 covers each thread's 11-12
+      // positions in one round trip). The positions combine in the same
+      // order as a one-at-a-time loop, whatever U is.
       for(int p0 = pg; p0 < HW; p0 += U * PG) {
         T v[U][VEC];
         float mk[U];
@@ -211,6 +210,99 @@ __global__ __launch_bounds__(POOL_THREADS) void poolVecKernel(const T* __restric
     }
   }
   (void)VEC;
+}
+
+// out[co] = act(sum_i x[i] W[i][co] + bias[co]) for one board, x in LDS.
+// The inputs of each output are split into S consecutive segments (S about
+// blockDim / cout), one thread each, summed in order and then added segment
+// by segment in order: short chains of L2 round trips instead of one of
+// length cin. part holds S * cout floats of LDS (at most blockDim.x, or
+// 4 * cout when cout > blockDim.x / 4); out may be LDS or global memory.
+__device__ void blockRowMatmul(const float* x, int cin, const float* __restrict__ W, int cout, const float* __restrict__ bias, int act,
+                               float* part, float* out) {
+  const int S = max(1, min(cin, (int)blockDim.x / cout));
+  const int seg = (cin + S - 1) / S;
+  // Neighbouring lanes take neighbouring outputs, so each weight load of a
+  // wave reads consecutive floats of one row.
+  for(int item = threadIdx.x; item < S * cout; item += blockDim.x) {
+    const int k = item / cout;
+    const int co = item - k * cout;
+    const int i1 = min(cin, (k + 1) * seg);
+    float a = 0.0f;
+#pragma unroll 16
+    for(int i = k * seg; i < i1; i++) a += x[i] * W[(size_t)i * cout + co];
+    part[item] = a;
+  }
+  __syncthreads();
+  for(int co = threadIdx.x; co < cout; co += blockDim.x) {
+    float acc = 0.0f;
+    for(int k = 0; k < S; k++) acc += part[k * cout + co];
+    if(bias != nullptr) acc += bias[co];
+    out[co] = kgh_activate(acc, act);
+  }
+  __syncthreads();
+}
+
+constexpr int HEADVEC_THREADS = 512;
+
+// Floats of dynamic LDS headVectorKernel uses (the pooling scratch, pooled
+// features, hidden layers and matmul partials).
+template<typename T>
+static size_t headVectorSmemFloats(const HeadVectorArgs<T>& a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int C = a.g1C + a.v1C;
+  const int hidP = a.pass2W != nullptr ? a.passC : 0;
+  int maxCout = std::max(std::max(a.p1C, a.passC), std::max(a.policyC, a.v2C));
+  maxCout = std::max(maxCout, std::max(3, a.scoreC));
+  return (size_t)2 * C + 3 * C + hidP + a.v2C + std::max(HEADVEC_THREADS, maxCout) + 2 * HEADVEC_THREADS * VEC;
+}
+
+template<typename T>
+__global__ __launch_bounds__(HEADVEC_THREADS) void headVectorKernel(HeadVectorArgs<T> a) {
+  extern __shared__ float smem[];
+  const int n = blockIdx.x;
+  const int C = a.g1C + a.v1C;
+  float* sums = smem;
+  float* maxs = sums + C;
+  float* gfeat = maxs + C;            // [3 g1C]
+  float* vfeat = gfeat + 3 * a.g1C;   // [3 v1C]
+  float* hidP = vfeat + 3 * a.v1C;    // [passC] when pass2W is set
+  float* hidV = hidP + (a.pass2W != nullptr ? a.passC : 0);
+  float* part = hidV + a.v2C;
+  int maxCout = max(max(a.p1C, a.passC), max(a.policyC, a.v2C));
+  maxCout = max(maxCout, max(3, a.scoreC));
+  float* red = part + max(HEADVEC_THREADS, maxCout);
+  // Eight positions in flight: at 512 threads twelve would not fit the
+  // 256 registers per lane.
+  poolBoardVec<T, 8>(a.gv, a.ldGv, C, a.mask, n, a.HW, sums, maxs, red);
+  // poolRowsGPool (eigenbackend.cpp:152-177) for g1, poolRowsValueHead
+  // (eigenbackend.cpp:179-197) for v1.
+  const float div = a.maskSum[n];
+  const float sq = sqrtf(div) - 14.0f;
+  for(int c = threadIdx.x; c < a.g1C; c += blockDim.x) {
+    const float mean = sums[c] / div;
+    gfeat[c] = mean;
+    gfeat[c + a.g1C] = mean * sq * 0.1f;
+    gfeat[c + 2 * a.g1C] = maxs[c];
+  }
+  for(int c = threadIdx.x; c < a.v1C; c += blockDim.x) {
+    const float mean = sums[a.g1C + c] / div;
+    vfeat[c] = mean;
+    vfeat[c + a.v1C] = mean * sq * 0.1f;
+    vfeat[c + 2 * a.v1C] = mean * (sq * sq * 0.01f - 0.1f);
+  }
+  __syncthreads();
+  blockRowMatmul(gfeat, 3 * a.g1C, a.g1W, a.p1C, nullptr, KGH_ACT_IDENTITY, part, a.g1Bias + (size_t)n * a.p1C);
+  if(a.pass2W != nullptr) {
+    blockRowMatmul(gfeat, 3 * a.g1C, a.passW, a.passC, a.passB, a.passAct, part, hidP);
+    blockRowMatmul(hidP, a.passC, a.pass2W, a.policyC, nullptr, KGH_ACT_IDENTITY, part, a.pass + (size_t)n * a.policyC);
+  }
+  else {
+    blockRowMatmul(gfeat, 3 * a.g1C, a.passW, a.policyC, nullptr, KGH_ACT_IDENTITY, part, a.pass + (size_t)n * a.policyC);
+  }
+  blockRowMatmul(vfeat, 3 * a.v1C, a.v2W, a.v2C, a.v2B, a.v2Act, part, hidV);
+  blockRowMatmul(hidV, a.v2C, a.v3W, 3, a.v3B, KGH_ACT_IDENTITY, part, a.value + (size_t)n * 3);
+  blockRowMatmul(hidV, a.v2C, a.sv3W, a.scoreC, a.sv3B, KGH_ACT_IDENTITY, part, a.score + (size_t)n * a.scoreC);
 }
 
 template<typename T, bool VALUE_MODE>
@@ -596,6 +688,26 @@ void launchRowMatmul(const float* in, int ldIn, int cin, const float* Wt, int co
                      ldOut, batch);
   KGH_CHECK_LAUNCH();
 }
+
+template<typename T>
+bool headVectorApplies(const HeadVectorArgs<T>& a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const int C = a.g1C + a.v1C;
+  return C % VEC == 0 && a.ldGv % VEC == 0 && ((uintptr_t)a.gv & 15) == 0 && C <= HEADVEC_THREADS * VEC &&
+         headVectorSmemFloats(a) * sizeof(float) <= 64 * 1024;
+}
+
+template<typename T>
+void launchHeadVector(const HeadVectorArgs<T>& a, hipStream_t stream) {
+  if(!headVectorApplies(a)) throw KghError(5, "head vector kernel: shapes not supported");
+  hipLaunchKernelGGL((headVectorKernel<T>), dim3(a.batch), dim3(HEADVEC_THREADS), headVectorSmemFloats(a) * sizeof(float), stream, a);
+  KGH_CHECK_LAUNCH();
+}
+
+template bool headVectorApplies<float>(const HeadVectorArgs<float>&);
+template bool headVectorApplies<half_t>(const HeadVectorArgs<half_t>&);
+template void launchHeadVector<float>(const HeadVectorArgs<float>&, hipStream_t);
+template void launchHeadVector<half_t>(const HeadVectorArgs<half_t>&, hipStream_t);
 
 template<typename T>
 void launchPool(const T* g, int ldG, int C, const float* mask, const float* maskSum, int batch, int HW, bool valueMode,

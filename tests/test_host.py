@@ -169,7 +169,7 @@ def test_hot_kernels_keep_everything_in_registers():
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "katago_amd", "lib", "kernel_resources.json")
     with open(path) as f:
         usage = json.load(f)
-    hot = ("convBoardWindowKernel", "convTapWindowKernel", "conv1x1DmaKernel", "convMfmaKernel", "flashAttentionKernel", "poolVecKernel",
+    hot = ("convBoardWindowKernel", "convTapWindowKernel", "conv1x1DmaKernel", "convMfmaKernel", "flashAttentionKernel", "poolVecKernel", "headVectorKernel",
            "bnActVecKernel", "rmsNormRowKernel", "headSpatialKernel")
     seen = set()
     for name, u in usage.items():
