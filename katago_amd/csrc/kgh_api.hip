@@ -751,11 +751,34 @@ struct Runner {
         eg.actBegin = 0;
         conv(b.convGpool, Ad, C, eg);
       }
-      // masked pooling of the gpool channels, then the bias matvec
-      kgh::launchPool<T>(tmp2, b.gpC, b.gpC, mask, maskSum, g.batch, g.H * g.W, false, nullptr, 0, b.gpoolMul.w, b.regC, nbias,
-                         b.regC, s);
-      // x = act(midBN(regular + bias)) * mask
-      bnAct(tmp1, b.regC, tmp3, b.regC, b.midBN, nbias, b.regC);
+      // masked pooling of the gpool channels, the bias matvec, then
+      // x = act(midBN(regular + bias)) * mask: one per-board launch when the
+      // shapes allow, else a pooling launch and a BN/activation launch.
+      GpoolBiasActArgs<T> ga;
+      ga.g = tmp2;
+      ga.ldG = b.gpC;
+      ga.C = b.gpC;
+      ga.HW = g.H * g.W;
+      ga.batch = g.batch;
+      ga.mask = mask;
+      ga.maskSum = maskSum;
+      ga.Wt = b.gpoolMul.w;
+      ga.cout = b.regC;
+      ga.x = tmp1;
+      ga.ldX = b.regC;
+      ga.y = tmp3;
+      ga.ldY = b.regC;
+      ga.scale = b.midBN.scale;
+      ga.shift = b.midBN.bias;
+      ga.act = b.midBN.act;
+      if(b.midBN.C == b.regC && kgh::gpoolBiasActApplies<T>(ga)) {
+        kgh::launchGpoolBiasAct<T>(ga, s);
+      }
+      else {
+        kgh::launchPool<T>(tmp2, b.gpC, b.gpC, mask, maskSum, g.batch, g.H * g.W, false, nullptr, 0, b.gpoolMul.w, b.regC, nbias,
+                           b.regC, s);
+        bnAct(tmp1, b.regC, tmp3, b.regC, b.midBN, nbias, b.regC);
+      }
       ConvEpilogue<T> e2 = epi();
       e2.residual = Rd;
       e2.ldRes = C;

@@ -61,6 +61,28 @@ struct HeadVectorArgs {
   float* score;  // [batch][scoreC]
 };
 
+// A gpool block's middle in one per-board launch (eigenbackend.cpp:1138-1218):
+// masked pooling of the gpool channels g, the bias matvec
+//   nb = pool(g) . Wt                       ([3 C][cout], input-major)
+// and the regular channels' BN + activation
+//   y = act((x + nb) * scale + shift) * mask.
+template<typename T>
+struct GpoolBiasActArgs {
+  const T* g;  // [M][ldG], C activated gpool channels
+  int ldG, C, HW, batch;
+  const float* mask;
+  const float* maskSum;
+  const float* Wt;
+  int cout;
+  const T* x;  // [M][ldX], cout raw regular channels
+  int ldX;
+  T* y;  // [M][ldY]
+  int ldY;
+  const float* scale;
+  const float* shift;
+  int act;
+};
+
 struct UnpackArgs {
   const float* policy;  // [M][policyC]
   const float* pass;    // [batch][policyC]
@@ -122,6 +144,11 @@ void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream);
 
 // Whether launchHeadVector takes these shapes (vector loads over g1C + v1C
 // channels, LDS within the default limit).
+template<typename T>
+bool gpoolBiasActApplies(const GpoolBiasActArgs<T>& a);
+template<typename T>
+void launchGpoolBiasAct(const GpoolBiasActArgs<T>& a, hipStream_t stream);
+
 template<typename T>
 bool headVectorApplies(const HeadVectorArgs<T>& a);
 template<typename T>

@@ -106,7 +106,7 @@ __global__ void rowMatmulKernel(const float* __restrict__ in, int ldIn, int cin,
 // Requires C and ld multiples of the vector width and 16-byte rows.
 template<typename T, int U = 12>
 __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float* __restrict__ mask, int n, int HW, float* sums,
-                             float* maxs, float* red) {
+                             float* maxs, float* red, float* red2) {
   constexpr int VEC = 16 / (int)sizeof(T);
   const int CG = C / VEC;
   const int nt = blockDim.x;
@@ -159,14 +159,47 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
       }
     }
     __syncthreads();
-    for(int c = t; c < cgN * VEC; c += nt) {
-      float a = 0.0f, b = -1.0f;
-      for(int q = 0; q < PG; q++) {
-        a += red[q * cgN * VEC + c];
-        b = fmaxf(b, red[(nt + q * cgN) * VEC + c]);
+    // The PG partials of a channel in K consecutive runs, one thread each,
+    // then the K run totals in order. K >= 2 needs K * CV <= blockDim, so
+    // the run totals fit red2 (2 * blockDim floats); with K = 1 the partials
+    // are summed directly.
+    const int CV = cgN * VEC;
+    const int K = min(8, nt / CV);
+    if(K >= 2) {
+      const int L = (PG + K - 1) / K;
+      if(t < K * CV) {
+        const int k = t / CV;
+        const int c = t - k * CV;
+        const int q1 = min(PG, (k + 1) * L);
+        float a = 0.0f, b = -1.0f;
+        for(int q = k * L; q < q1; q++) {
+          a += red[q * CV + c];
+          b = fmaxf(b, red[nt * VEC + q * CV + c]);
+        }
+        red2[k * CV + c] = a;
+        red2[nt + k * CV + c] = b;
       }
-      sums[cg0 * VEC + c] = a;
-      maxs[cg0 * VEC + c] = b;
+      __syncthreads();
+      if(t < CV) {
+        float a = 0.0f, b = -1.0f;
+        for(int k = 0; k < K; k++) {
+          a += red2[k * CV + t];
+          b = fmaxf(b, red2[nt + k * CV + t]);
+        }
+        sums[cg0 * VEC + t] = a;
+        maxs[cg0 * VEC + t] = b;
+      }
+    }
+    else {
+      for(int c = t; c < CV; c += nt) {
+        float a = 0.0f, b = -1.0f;
+        for(int q = 0; q < PG; q++) {
+          a += red[q * CV + c];
+          b = fmaxf(b, red[nt * VEC + q * CV + c]);
+        }
+        sums[cg0 * VEC + c] = a;
+        maxs[cg0 * VEC + c] = b;
+      }
     }
     __syncthreads();
   }
@@ -187,7 +220,8 @@ __global__ __launch_bounds__(POOL_THREADS) void poolVecKernel(const T* __restric
   float* maxs = sums + C;             // [C]
   float* pooled = maxs + C;           // [3C]
   float* red = pooled + 3 * C;        // [2 * blockDim.x * VEC]
-  poolBoardVec<T>(g, ldG, C, mask, n, HW, sums, maxs, red);
+  float* red2 = red + 2 * blockDim.x * VEC;  // [2 * blockDim.x]
+  poolBoardVec<T>(g, ldG, C, mask, n, HW, sums, maxs, red, red2);
   const float div = maskSum[n];
   const float sq = sqrtf(div) - 14.0f;
   for(int c = threadIdx.x; c < C; c += blockDim.x) {
@@ -210,6 +244,74 @@ __global__ __launch_bounds__(POOL_THREADS) void poolVecKernel(const T* __restric
     }
   }
   (void)VEC;
+}
+
+// poolVecKernel's pooling and bias matvec (same sums), then bnActVecKernel's
+// BN + activation of the board's regular channels with the bias from LDS:
+// bitwise the outputs of those two launches, without the bias round trip
+// through global memory and the second launch.
+constexpr int GPOOL_ACT_THREADS = 512;
+template<typename T, int ACT>
+__global__ __launch_bounds__(GPOOL_ACT_THREADS) void gpoolBiasActKernel(GpoolBiasActArgs<T> a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  extern __shared__ float smem[];
+  const int n = blockIdx.x;
+  const int C = a.C;
+  float* sums = smem;                 // [C]
+  float* maxs = sums + C;             // [C]
+  float* pooled = maxs + C;           // [3C]
+  float* nb = pooled + 3 * C;         // [cout]
+  float* red = nb + a.cout;           // [2 * blockDim.x * VEC], then [2 * blockDim.x]
+  // Eight positions in flight: at 512 threads twelve would not fit the
+  // 256 registers per lane.
+  poolBoardVec<T, 8>(a.g, a.ldG, C, a.mask, n, a.HW, sums, maxs, red, red + 2 * GPOOL_ACT_THREADS * VEC);
+  const float div = a.maskSum[n];
+  const float sq = sqrtf(div) - 14.0f;
+  for(int c = threadIdx.x; c < C; c += blockDim.x) {
+    const float mean = sums[c] / div;
+    pooled[c] = mean;
+    pooled[c + C] = mean * sq * 0.1f;
+    pooled[c + 2 * C] = maxs[c];
+  }
+  __syncthreads();
+  for(int co = threadIdx.x; co < a.cout; co += blockDim.x) {
+    float acc = 0.0f;
+#pragma unroll 32
+    for(int i = 0; i < 3 * C; i++) acc += pooled[i] * a.Wt[(size_t)i * a.cout + co];
+    nb[co] = acc;
+  }
+  __syncthreads();
+  // Twelve 16-byte rows in flight per thread (one round at C2's 361 x 128).
+  const int CG = a.cout / VEC;
+  const int items = a.HW * CG;
+  constexpr int U = 12;
+  for(int it0 = threadIdx.x; it0 < items; it0 += U * blockDim.x) {
+    T in[U][VEC];
+#pragma unroll
+    for(int u = 0; u < U; u++) {
+      const int it = it0 + u * blockDim.x;
+      if(it < items) {
+        const int p = it / CG;
+        const int c = (it - p * CG) * VEC;
+        *(uint4*)in[u] = *(const uint4*)(a.x + ((size_t)n * a.HW + p) * a.ldX + c);
+      }
+    }
+#pragma unroll
+    for(int u = 0; u < U; u++) {
+      const int it = it0 + u * blockDim.x;
+      if(it < items) {
+        const int p = it / CG;
+        const int c = (it - p * CG) * VEC;
+        const size_t m = (size_t)n * a.HW + p;
+        const float msk = a.mask[m];
+        T out[VEC];
+#pragma unroll
+        for(int j = 0; j < VEC; j++)
+          out[j] = kgh_from_float<T>(kgh_activate_fast((kgh_to_float(in[u][j]) + nb[c + j]) * a.scale[c + j] + a.shift[c + j], ACT) * msk);
+        *(uint4*)(a.y + m * a.ldY + c) = *(const uint4*)out;
+      }
+    }
+  }
 }
 
 // out[co] = act(sum_i x[i] W[i][co] + bias[co]) for one board, x in LDS.
@@ -254,11 +356,12 @@ static size_t headVectorSmemFloats(const HeadVectorArgs<T>& a) {
   const int hidP = a.pass2W != nullptr ? a.passC : 0;
   int maxCout = std::max(std::max(a.p1C, a.passC), std::max(a.policyC, a.v2C));
   maxCout = std::max(maxCout, std::max(3, a.scoreC));
-  return (size_t)2 * C + 3 * C + hidP + a.v2C + std::max(HEADVEC_THREADS, maxCout) + 2 * HEADVEC_THREADS * VEC;
+  return (size_t)2 * C + 3 * C + hidP + a.v2C + std::max(HEADVEC_THREADS, maxCout) + 2 * HEADVEC_THREADS * VEC + 2 * HEADVEC_THREADS;
 }
 
 template<typename T>
 __global__ __launch_bounds__(HEADVEC_THREADS) void headVectorKernel(HeadVectorArgs<T> a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
   extern __shared__ float smem[];
   const int n = blockIdx.x;
   const int C = a.g1C + a.v1C;
@@ -274,7 +377,7 @@ __global__ __launch_bounds__(HEADVEC_THREADS) void headVectorKernel(HeadVectorAr
   float* red = part + max(HEADVEC_THREADS, maxCout);
   // Eight positions in flight: at 512 threads twelve would not fit the
   // 256 registers per lane.
-  poolBoardVec<T, 8>(a.gv, a.ldGv, C, a.mask, n, a.HW, sums, maxs, red);
+  poolBoardVec<T, 8>(a.gv, a.ldGv, C, a.mask, n, a.HW, sums, maxs, red, red + 2 * HEADVEC_THREADS * VEC);
   // poolRowsGPool (eigenbackend.cpp:152-177) for g1, poolRowsValueHead
   // (eigenbackend.cpp:179-197) for v1.
   const float div = a.maskSum[n];
@@ -690,6 +793,39 @@ void launchRowMatmul(const float* in, int ldIn, int cin, const float* Wt, int co
 }
 
 template<typename T>
+bool gpoolBiasActApplies(const GpoolBiasActArgs<T>& a) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const bool aligned = (((uintptr_t)a.g | (uintptr_t)a.x | (uintptr_t)a.y) & 15) == 0;
+  const bool actOk = a.act == KGH_ACT_IDENTITY || a.act == KGH_ACT_RELU || a.act == KGH_ACT_MISH || a.act == KGH_ACT_SILU ||
+                     a.act == KGH_ACT_MISH_SCALE8;
+  const size_t smem = (size_t)(5 * a.C + a.cout + 2 * GPOOL_ACT_THREADS * VEC + 2 * GPOOL_ACT_THREADS) * sizeof(float);
+  return aligned && actOk && a.C % VEC == 0 && a.ldG % VEC == 0 && a.cout % VEC == 0 && a.ldX % VEC == 0 && a.ldY % VEC == 0 &&
+         a.Wt != nullptr && smem <= 64 * 1024;
+}
+
+template<typename T>
+void launchGpoolBiasAct(const GpoolBiasActArgs<T>& a, hipStream_t stream) {
+  if(!gpoolBiasActApplies(a)) throw KghError(5, "gpool bias/activation kernel: shapes not supported");
+  constexpr int VEC = 16 / (int)sizeof(T);
+  const size_t smem = (size_t)(5 * a.C + a.cout + 2 * GPOOL_ACT_THREADS * VEC + 2 * GPOOL_ACT_THREADS) * sizeof(float);
+  const dim3 grid(a.batch), block(GPOOL_ACT_THREADS);
+  switch(a.act) {
+    case KGH_ACT_IDENTITY: hipLaunchKernelGGL((gpoolBiasActKernel<T, KGH_ACT_IDENTITY>), grid, block, smem, stream, a); break;
+    case KGH_ACT_RELU: hipLaunchKernelGGL((gpoolBiasActKernel<T, KGH_ACT_RELU>), grid, block, smem, stream, a); break;
+    case KGH_ACT_MISH: hipLaunchKernelGGL((gpoolBiasActKernel<T, KGH_ACT_MISH>), grid, block, smem, stream, a); break;
+    case KGH_ACT_SILU: hipLaunchKernelGGL((gpoolBiasActKernel<T, KGH_ACT_SILU>), grid, block, smem, stream, a); break;
+    case KGH_ACT_MISH_SCALE8: hipLaunchKernelGGL((gpoolBiasActKernel<T, KGH_ACT_MISH_SCALE8>), grid, block, smem, stream, a); break;
+    default: throw KghError(1, "gpool bias/activation: unknown activation " + std::to_string(a.act));
+  }
+  KGH_CHECK_LAUNCH();
+}
+
+template bool gpoolBiasActApplies<float>(const GpoolBiasActArgs<float>&);
+template bool gpoolBiasActApplies<half_t>(const GpoolBiasActArgs<half_t>&);
+template void launchGpoolBiasAct<float>(const GpoolBiasActArgs<float>&, hipStream_t);
+template void launchGpoolBiasAct<half_t>(const GpoolBiasActArgs<half_t>&, hipStream_t);
+
+template<typename T>
 bool headVectorApplies(const HeadVectorArgs<T>& a) {
   constexpr int VEC = 16 / (int)sizeof(T);
   const int C = a.g1C + a.v1C;
@@ -715,7 +851,7 @@ void launchPool(const T* g, int ldG, int C, const float* mask, const float* mask
   constexpr int VEC = 16 / (int)sizeof(T);
   if(C % VEC == 0 && ldG % VEC == 0 && ((uintptr_t)g & 15) == 0) {
     const int threads = POOL_THREADS;
-    const size_t smem = (size_t)(5 * C + 2 * threads * VEC) * sizeof(float);
+    const size_t smem = (size_t)(5 * C + 2 * threads * VEC + 2 * threads) * sizeof(float);
     if(valueMode)
       hipLaunchKernelGGL((poolVecKernel<T, true>), dim3(batch), dim3(threads), smem, stream, g, ldG, C, mask, maskSum, HW, pooledOut,
                          ldPooled, Wt, cout, out, ldOut);

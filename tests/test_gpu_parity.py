@@ -72,6 +72,7 @@ def _random_block(kind, c, mid, gp, act, rng):
     ("residual", 32, 64, 0, "ACTIVATION_SILU"),
     ("gpool", 64, 64, 32, "ACTIVATION_MISH"),
     ("gpool", 96, 96, 32, "ACTIVATION_RELU"),
+    ("gpool", 48, 40, 6, "ACTIVATION_MISH"),
 ])
 def test_random_blocks_match_oracle(kind, c, mid, gp, act, fp16):
     rng = np.random.default_rng(c + mid + gp)
@@ -243,6 +244,18 @@ def test_tiny_transformers_match_oracle(model_dir, heads, kv, dq, dv, c, learnab
     arch = _tiny_transformer(heads, kv, dq, dv, c, learnable, tip)
     path = modelgen.write_model(arch, 31 + heads + dq, f"{model_dir}/{arch.name}-{learnable}-{tip}.bin.gz")
     _run_parity(path, fp16, 5, board_sizes=(19, 9, 13, 7), label=arch.name)
+
+
+@pytest.mark.parametrize("fp16", [False, True], ids=["fp32", "fp16"])
+@pytest.mark.parametrize("g1,v1", [(5, 6), (8, 16)], ids=["g1-5-v1-6", "g1-8-v1-16"])
+def test_head_channel_counts_match_oracle(model_dir, g1, v1, fp16):
+    """Head vectors (pooling, g1 bias, pass, value, score) through both
+    device paths: g1 + v1 = 11 channels takes the pooling launches and
+    row-parallel matmuls, 24 channels the one-launch per-board kernel."""
+    arch = modelgen.Arch(f"tiny-heads-g{g1}v{v1}", 15, 32, 32, 16, ["regular", "regulargpool", "regular"], 8, g1, v1, 12,
+                         "ACTIVATION_MISH", residual_gain=0.5)
+    path = modelgen.write_model(arch, 17 + g1 + v1, f"{model_dir}/{arch.name}.bin.gz")
+    _run_parity(path, fp16, 5, board_sizes=(19, 9, 13), label=arch.name)
 
 
 def test_c4_transformer_d384_fp16_matches_oracle(model_dir):
