@@ -32,7 +32,8 @@ __device__ __forceinline__ void symDest(int h, int w, int H, int W, int sym, boo
   }
 }
 
-template<typename T>
+// VEC_ROW: cin even, cinPad <= 64 and cinPad * sizeof(T) a multiple of 16.
+template<typename T, bool VEC_ROW>
 __global__ void packInputsKernel(const float* __restrict__ spatial, const int* __restrict__ sym, int batch, int H, int W,
                                  int cin, T* __restrict__ x, int cinPad, float* __restrict__ mask) {
   int HW = H * W;
@@ -47,9 +48,30 @@ __global__ void packInputsKernel(const float* __restrict__ spatial, const int* _
   int md = n * HW + hd * W + wd;
   const float* src = spatial + (size_t)idx * cin;
   T* dst = x + (size_t)md * cinPad;
-  for(int c = 0; c < cin; c++) dst[c] = (T)src[c];
-  for(int c = cin; c < cinPad; c++) dst[c] = (T)0.0f;
-  mask[md] = src[0];
+  if(VEC_ROW) {
+    // The padded row built in registers: float2 loads (rows start on 8-byte
+    // boundaries when cin is even), 16-byte stores (cinPad * sizeof(T) is a
+    // multiple of 16).
+    constexpr int MAXC = 64;
+    T row[MAXC];
+#pragma unroll
+    for(int c2 = 0; c2 < MAXC / 2; c2++) {
+      float2 v = make_float2(0.0f, 0.0f);
+      if(2 * c2 < cin) v = *(const float2*)(src + 2 * c2);
+      row[2 * c2] = (T)v.x;
+      row[2 * c2 + 1] = (T)v.y;
+    }
+    constexpr int PER16 = 16 / (int)sizeof(T);
+#pragma unroll
+    for(int q = 0; q < MAXC / PER16; q++)
+      if(q * PER16 < cinPad) *(uint4*)(dst + q * PER16) = *(const uint4*)(row + q * PER16);
+    mask[md] = src[0];
+  }
+  else {
+    for(int c = 0; c < cin; c++) dst[c] = (T)src[c];
+    for(int c = cin; c < cinPad; c++) dst[c] = (T)0.0f;
+    mask[md] = src[0];
+  }
 }
 
 __global__ void maskSumKernel(const float* __restrict__ mask, int HW, float* __restrict__ maskSum) {
@@ -777,8 +799,14 @@ template<typename T>
 void launchPackInputs(const float* spatial, const int* sym, int batch, int H, int W, int cin, T* x, int cinPad, float* mask,
                       float* maskSum, hipStream_t stream) {
   int total = batch * H * W;
-  hipLaunchKernelGGL(packInputsKernel<T>, dim3((total + 255) / 256), dim3(256), 0, stream, spatial, sym, batch, H, W, cin, x,
-                     cinPad, mask);
+  const bool vecRow = cin % 2 == 0 && cinPad <= 64 && (cinPad * sizeof(T)) % 16 == 0 && ((uintptr_t)spatial & 7) == 0 &&
+                      ((uintptr_t)x & 15) == 0;
+  if(vecRow)
+    hipLaunchKernelGGL((packInputsKernel<T, true>), dim3((total + 255) / 256), dim3(256), 0, stream, spatial, sym, batch, H, W, cin, x,
+                       cinPad, mask);
+  else
+    hipLaunchKernelGGL((packInputsKernel<T, false>), dim3((total + 255) / 256), dim3(256), 0, stream, spatial, sym, batch, H, W, cin,
+                       x, cinPad, mask);
   KGH_CHECK_LAUNCH();
   hipLaunchKernelGGL(maskSumKernel, dim3(batch), dim3(256), 0, stream, mask, H * W, maskSum);
   KGH_CHECK_LAUNCH();
