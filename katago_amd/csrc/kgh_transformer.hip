@@ -26,69 +26,80 @@ __device__ __forceinline__ float waveSum(float v) {
   return v;
 }
 
-// Sixteen lanes per row, four rows per wave: lane l of a row holds 16-byte
-// channel groups l, l + 16, ... (NG of them) in registers across both
-// passes, with gamma/beta loaded before the reduction and the activation
-// fixed at compile time.
-template<typename T, int NG, int ACT>
-__global__ void rmsNormRowKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C, const float* __restrict__ gamma,
-                                 const float* __restrict__ beta, float eps, const float* __restrict__ mask, int M) {
+// Sixteen lanes per row group, four groups per wave, RPG consecutive rows per
+// group: lane l of a row holds 16-byte channel groups l, l + 16, ... (NG of
+// them) in registers across both passes, with gamma/beta loaded before the
+// reduction and the activation fixed at compile time.
+template<typename T, int NG, int ACT, int RPG>
+__global__ __launch_bounds__(256) void rmsNormRowKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C,
+                                                       const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+                                                       const float* __restrict__ mask, int M) {
   constexpr int VEC = 16 / (int)sizeof(T);
   const int sub = threadIdx.x & 15;
-  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 4;
-  const bool live = row < M;  // whole 16-lane groups share one row
-  const int r = live ? row : M - 1;
-  const T* xr = x + (size_t)r * ldX;
-  T* yr = y + (size_t)r * ldY;
+  // RPG consecutive rows per 16-lane group: gamma and beta are loaded once
+  // per group, and all the group's row loads are issued before any is used.
+  const int row0 = ((blockIdx.x * blockDim.x + threadIdx.x) >> 4) * RPG;
   // Wide rows (NG > 4) load gamma/beta in the second pass instead, to stay
   // within registers.
   constexpr bool PRELOAD = NG <= 4;
   constexpr int NP = PRELOAD ? NG : 1;
-  T v[NG][VEC];
   float gm[NP][VEC], bt[NP][VEC];
+  if constexpr(PRELOAD) {
 #pragma unroll
-  for(int i = 0; i < NG; i++) {
-    const int c = (sub + 16 * i) * VEC;
-    if(c < C) {
-      *(uint4*)v[i] = *(const uint4*)(xr + c);
-      if constexpr(PRELOAD) {
-#pragma unroll
-        for(int j = 0; j < VEC; j++) {
-          gm[i][j] = gamma[c + j];
-          bt[i][j] = beta != nullptr ? beta[c + j] : 0.0f;
-        }
-      }
-    }
-    else {
-      *(uint4*)v[i] = make_uint4(0, 0, 0, 0);
-    }
-  }
-  const bool on = mask[r] != 0.0f;
-  float ss = 0.0f;
-#pragma unroll
-  for(int i = 0; i < NG; i++)
-#pragma unroll
-    for(int j = 0; j < VEC; j++) {
-      const float f = kgh_to_float(v[i][j]);
-      ss += f * f;
-    }
-#pragma unroll
-  for(int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-  const float inv = 1.0f / sqrtf(ss / (float)C + eps);
-  if(!live) return;
-#pragma unroll
-  for(int i = 0; i < NG; i++) {
-    const int c = (sub + 16 * i) * VEC;
-    if(c < C) {
-      T o[VEC];
+    for(int i = 0; i < NG; i++) {
+      const int c = (sub + 16 * i) * VEC;
 #pragma unroll
       for(int j = 0; j < VEC; j++) {
-        const float g = PRELOAD ? gm[PRELOAD ? i : 0][j] : gamma[c + j];
-        const float b = PRELOAD ? bt[PRELOAD ? i : 0][j] : (beta != nullptr ? beta[c + j] : 0.0f);
-        const float f = kgh_activate(kgh_to_float(v[i][j]) * inv * g + b, ACT);
-        o[j] = kgh_from_float<T>(on ? f : 0.0f);
+        gm[i][j] = c < C ? gamma[c + j] : 0.0f;
+        bt[i][j] = c < C && beta != nullptr ? beta[c + j] : 0.0f;
       }
-      *(uint4*)(yr + c) = *(const uint4*)o;
+    }
+  }
+  T v[RPG][NG][VEC];
+#pragma unroll
+  for(int rr = 0; rr < RPG; rr++) {
+    const int r = min(row0 + rr, M - 1);  // rows past M are loaded, never stored
+    const T* xr = x + (size_t)r * ldX;
+#pragma unroll
+    for(int i = 0; i < NG; i++) {
+      const int c = (sub + 16 * i) * VEC;
+      if(c < C) *(uint4*)v[rr][i] = *(const uint4*)(xr + c);
+      else *(uint4*)v[rr][i] = make_uint4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for(int rr = 0; rr < RPG; rr++) {
+    const int row = row0 + rr;
+    const bool live = row < M;  // the same for the whole 16-lane group
+    const int r = live ? row : M - 1;
+    float ss = 0.0f;
+#pragma unroll
+    for(int i = 0; i < NG; i++)
+#pragma unroll
+      for(int j = 0; j < VEC; j++) {
+        const float f = kgh_to_float(v[rr][i][j]);
+        ss += f * f;
+      }
+#pragma unroll
+    for(int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+    if(!live) continue;
+    const bool on = mask[r] != 0.0f;
+    T* yr = y + (size_t)r * ldY;
+#pragma unroll
+    for(int i = 0; i < NG; i++) {
+      const int c = (sub + 16 * i) * VEC;
+      if(c < C) {
+        T o[VEC];
+#pragma unroll
+        for(int j = 0; j < VEC; j++) {
+          const float g = PRELOAD ? gm[PRELOAD ? i : 0][j] : gamma[c + j];
+          const float b = PRELOAD ? bt[PRELOAD ? i : 0][j] : (beta != nullptr ? beta[c + j] : 0.0f);
+          const float f = kgh_activate(kgh_to_float(v[rr][i][j]) * inv * g + b, ACT);
+          o[j] = kgh_from_float<T>(on ? f : 0.0f);
+        }
+        *(uint4*)(yr + c) = *(const uint4*)o;
+      }
     }
   }
 }
@@ -429,20 +440,27 @@ namespace kgh {
 template<typename T, int NG>
 void launchRmsNormNG(const T* x, int ldX, T* y, int ldY, int C, const float* gamma, const float* beta, float eps, int act,
                      const float* mask, int M, hipStream_t stream) {
-  const int rowsPerBlock = 16;  // 256 threads, 16 lanes per row
+  // Rows per 16-lane group: four while a row takes at most three 16-byte
+  // loads per lane, fewer for wider rows (registers).
+  constexpr int RPG = NG <= 3 ? 4 : NG <= 4 ? 2 : 1;
+  const int rowsPerBlock = 16 * RPG;  // 256 threads, 16 lanes per group
   const dim3 grid((M + rowsPerBlock - 1) / rowsPerBlock), block(256);
   switch(act) {
     case KGH_ACT_IDENTITY:
-      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_IDENTITY>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_IDENTITY, RPG>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps,
+                         mask, M);
       break;
     case KGH_ACT_RELU:
-      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_RELU>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_RELU, RPG>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask,
+                         M);
       break;
     case KGH_ACT_MISH:
-      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_MISH>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_MISH, RPG>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask,
+                         M);
       break;
     case KGH_ACT_SILU:
-      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_SILU>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask, M);
+      hipLaunchKernelGGL((rmsNormRowKernel<T, NG, KGH_ACT_SILU, RPG>), grid, block, 0, stream, x, ldX, y, ldY, C, gamma, beta, eps, mask,
+                         M);
       break;
     default: throw KghError(1, "RMSNorm: unsupported activation " + std::to_string(act));
   }
