@@ -165,6 +165,9 @@ enum ConvVariant {
   CONV_BOARD_192,  // 3x3 fp16 one-board-per-workgroup kernel (19x19 boards), 192 output channels per tile
   CONV_BOARD_128,
   CONV_BOARD_64,
+  CONV_DMA1H_192,  // 1x1 fp16 DMA kernel with 192-row tiles, two workgroups per CU
+  CONV_DMA1H_128,
+  CONV_DMA1H_64,
   CONV_VARIANT_COUNT
 };
 

@@ -1144,40 +1144,54 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
 constexpr int G1_A_LOADS = TW_BM / 16;  // 24 wave-loads of A per step
 
 // GLU selects the gated epilogue at compile time: the branch alone pushes the
-// accumulators of the non-gated variant out of registers.
-template<int BN, bool GLU>
-__global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
-                                                                 int cout, const half_t* __restrict__ w, BoardGeom g,
-                                                                 ConvEpilogue<half_t> epi) {
+// accumulators of the non-gated variant out of registers. BM = 384: 8 waves,
+// one workgroup per CU. BM = 192: 4 waves and 72 KB of LDS or less (the
+// epilogue stage in the first two A buffers), two workgroups per CU, so one
+// workgroup's prologue and epilogue overlap the other's matrix work (for
+// GEMM-shaped calls with K of a few hundred or more).
+template<int BN, bool GLU, int BM>
+__global__ __launch_bounds__(BM / 48 * 64, BM == 384 ? 1 : 2) void conv1x1DmaKernel(const half_t* __restrict__ x, int cinStride,
+                                                                                   int cinPad, int cout, const half_t* __restrict__ w,
+                                                                                   BoardGeom g, ConvEpilogue<half_t> epi) {
+  static_assert(BM == 384 || BM == 192, "row tiles of 384 or 192");
+  constexpr int NW = BM / 48;  // waves: row blocks of 96 x two column halves
+  constexpr int LW = NW / 2;   // waves loading each operand
   constexpr int WN = 2;
-  constexpr int WTM = TW_BM / 4;  // 96
+  constexpr int WTM = 96;
   constexpr int WTN = BN / WN;
   constexpr int RB = WTM / 32;
   constexpr int CB = WTN / 32;
   static_assert(WTN % 32 == 0, "wave tile must be a multiple of 32 columns");
-  constexpr int B_PER = BN / 16 / 4;
-  static_assert(B_PER * 64 == BN, "weights split evenly over four waves");
-  constexpr int A_PER = G1_A_LOADS / 4;  // 6
-  __shared__ __attribute__((aligned(1024))) unsigned char a0s[G1_A_LOADS * 1024];
-  __shared__ __attribute__((aligned(1024))) unsigned char a1s[G1_A_LOADS * 1024];
-  __shared__ __attribute__((aligned(1024))) unsigned char a2s[G1_A_LOADS * 1024];
+  constexpr int B_PER = BN / 16 / LW;
+  static_assert(B_PER * 16 * LW == BN, "weights split evenly over the weight waves");
+  constexpr int A_LOADS = BM / 16;
+  constexpr int A_PER = A_LOADS / LW;  // 6
+  __shared__ __attribute__((aligned(1024))) unsigned char a0s[A_LOADS * 1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char a1s[A_LOADS * 1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char a2s[A_LOADS * 1024];
   __shared__ __attribute__((aligned(1024))) unsigned char b0s[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char b1s[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char b2s[BN * 64];
-  __shared__ __attribute__((aligned(16))) float stage[8 * 32 * CONV_STAGE_LD];
+  __shared__ __attribute__((aligned(16))) float stageArr[BM == 384 ? 8 * 32 * CONV_STAGE_LD : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool weightWave = wave < 4;
-  const int loaderIdx = wave & 3;
+  const bool weightWave = wave < LW;
+  const int loaderIdx = wave % LW;
   const int wm = wave / WN;
   const int wn = wave % WN;
   const int HW = g.H * g.W;
   const int M = g.batch * HW;
   int rowTile, colTile;
   rowColTile(cout / BN, rowTile, colTile);
-  const int m0 = rowTile * TW_BM;
+  const int m0 = rowTile * BM;
+  // The wave's 32 x CONV_STAGE_LD floats for the residual load and the
+  // epilogue: a separate array at BM = 384, else two waves per A buffer
+  // (idle then).
+  constexpr int STAGE_BYTES = 32 * CONV_STAGE_LD * 4;
+  static_assert(BM == 384 || 2 * STAGE_BYTES <= A_LOADS * 1024, "two stages fit in an A buffer");
+  float* stage = BM == 384 ? stageArr + wave * 32 * CONV_STAGE_LD : (float*)((wave < 2 ? a0s : a1s) + (wave & 1) * STAGE_BYTES);
   const int n0 = colTile * BN;
   const int laneRow = lane & 31;
   const int kq = lane >> 5;
@@ -1188,7 +1202,7 @@ __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* 
   int aSrc[A_PER];
 #pragma unroll
   for(int i = 0; i < A_PER; i++) {
-    int gm = m0 + 16 * (loaderIdx + 4 * i) + dRow;
+    int gm = m0 + 16 * (loaderIdx + LW * i) + dRow;
     gm = gm < M ? gm : M - 1;  // rows past M are never stored
     aSrc[i] = gm * cinStride + dGroup * 8;
   }
@@ -1214,7 +1228,7 @@ __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* 
     else {
 #pragma unroll
       for(int i = 0; i < A_PER; i++)
-        __builtin_amdgcn_global_load_lds((const void*)(x + aSrc[i] + st * 32), (lds_void_t*)(aBuf(buf) + (loaderIdx + 4 * i) * 1024),
+        __builtin_amdgcn_global_load_lds((const void*)(x + aSrc[i] + st * 32), (lds_void_t*)(aBuf(buf) + (loaderIdx + LW * i) * 1024),
                                          16, 0, 0);
       asm volatile("; activation dma");
     }
@@ -1233,12 +1247,17 @@ __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* 
     for(int cb = 0; cb < CB; cb++) bOff[cb][ks] = swizzled(wn * WTN + cb * 32 + laneRow, ks * 2 + kq);
   }
 
-  load(0, 0);
-  load(1, 1);
   const bool resInAcc = epi.residual != nullptr && !epi.maskResidualAdd;
   floatx16 acc[RB][CB];
+  // BM = 384: the first two steps' DMA overlaps the residual load. BM = 192:
+  // the stage shares the A buffers, so the residual is loaded first.
+  if constexpr(BM == 384) {
+    load(0, 0);
+    load(1, 1);
+  }
   if(resInAcc) {
-    residualToAcc<half_t, RB, CB>(acc, epi.residual, epi.ldRes, m0 + wm * WTM, n0 + wn * WTN, M, stage + wave * 32 * CONV_STAGE_LD);
+    residualToAcc<half_t, RB, CB>(acc, epi.residual, epi.ldRes, m0 + wm * WTM, n0 + wn * WTN, M, stage);
+    if constexpr(BM != 384) __syncthreads();
   }
   else {
 #pragma unroll
@@ -1247,6 +1266,10 @@ __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* 
       for(int cb = 0; cb < CB; cb++)
 #pragma unroll
         for(int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
+  }
+  if constexpr(BM != 384) {
+    load(0, 0);
+    load(1, 1);
   }
   waitStep();
   barrierNoFence();
@@ -1281,7 +1304,7 @@ __global__ __launch_bounds__(TW_THREADS, 1) void conv1x1DmaKernel(const half_t* 
 
   ConvEpilogue<half_t> e = epi;
   if(resInAcc) e.residual = nullptr;
-  storeWaveEpilogue<half_t, RB, CB, false, GLU>(acc, stage + wave * 32 * CONV_STAGE_LD, m0 + wm * WTM, n0 + wn * WTN, M, HW, e);
+  storeWaveEpilogue<half_t, RB, CB, false, GLU>(acc, stage, m0 + wm * WTM, n0 + wn * WTN, M, HW, e);
 }
 
 // Direct convolution: one thread per output element. Used for shapes the
@@ -1418,13 +1441,13 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
   return true;
 }
 
-template<int BN>
+template<int BN, int BM = 384>
 void launch1x1Dma(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                   const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   int M = g.batch * g.H * g.W;
-  dim3 grid((M + TW_BM - 1) / TW_BM * (cout / BN));
-  if(epi.glu) hipLaunchKernelGGL((conv1x1DmaKernel<BN, true>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
-  else hipLaunchKernelGGL((conv1x1DmaKernel<BN, false>), grid, dim3(TW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  dim3 grid((M + BM - 1) / BM * (cout / BN)), block(BM / 48 * 64);
+  if(epi.glu) hipLaunchKernelGGL((conv1x1DmaKernel<BN, true, BM>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  else hipLaunchKernelGGL((conv1x1DmaKernel<BN, false, BM>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
   KGH_CHECK_LAUNCH();
 }
 
@@ -1475,6 +1498,9 @@ bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g
       if(v == CONV_DMA1_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
       if(v == CONV_DMA1_128) return dma1x1Fits(cinStride, cinPad, cout, 128, g);
       if(v == CONV_DMA1_64) return dma1x1Fits(cinStride, cinPad, cout, 64, g);
+      if(v == CONV_DMA1H_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
+      if(v == CONV_DMA1H_128) return dma1x1Fits(cinStride, cinPad, cout, 128, g);
+      if(v == CONV_DMA1H_64) return dma1x1Fits(cinStride, cinPad, cout, 64, g);
     }
   }
   else {
@@ -1515,6 +1541,9 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
       case CONV_DMA1_192: launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_128: launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_64: launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_DMA1H_192: launch1x1Dma<192, 192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_DMA1H_128: launch1x1Dma<128, 192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_DMA1H_64: launch1x1Dma<64, 192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       default: break;
     }
   }
@@ -1544,7 +1573,8 @@ bool convMfmaSupported(int cinPad, int cout) {
 
 const char* convVariantName(int variant) {
   static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
-                                "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64"};
+                                "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64",
+                                "dma1x1h_192", "dma1x1h_128", "dma1x1h_64"};
   return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
 }
 

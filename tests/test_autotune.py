@@ -13,6 +13,9 @@ import pytest
 
 from katago_amd import modelgen, nn
 
+# Kernel variant ids 0..VARIANTS-1 (ConvVariant in kgh_common.h).
+VARIANTS = 19
+
 pytestmark = pytest.mark.gpu
 
 
@@ -34,7 +37,7 @@ def test_tune_save_load_and_identical_results(model_dir, tmp_path):
     assert len(lines) >= 3  # the 3x3 trunk conv, the head 1x1s, ...
     for l in lines:
         f = l.split()
-        assert int(f[4]) == n * 361 and 0 <= int(f[8]) < 16  # M, variant id (0: built-in choice kept)
+        assert int(f[4]) == n * 361 and 0 <= int(f[8]) < VARIANTS  # M, variant id (0: built-in choice kept)
     files = glob.glob(os.path.join(home, "hiptuning", f"tune1_*_x19_y19_b{n}_fp16_arch*.txt"))
     assert len(files) == 1
     assert open(files[0]).read().startswith("VERSION=2")
@@ -82,8 +85,28 @@ def test_every_kernel_variant_gives_identical_bits(model_dir, fp16):
     shapes = [l.split()[:8] for l in tuned.tuning()[1].splitlines() if l.strip()]
     assert shapes
     ref = _forward(nn.ComputeHandle(nn.ComputeContext(lm, use_fp16=fp16, auto_tune=False), max_batch=n), sp, gl)
-    for v in range(1, 16):
+    for v in range(1, VARIANTS):
         tuned.set_tuning("".join(" ".join(k) + f" {v}\n" for k in shapes))
         out = _forward(tuned, sp, gl)
         for k in out:
             assert np.array_equal(out[k], ref[k]), (v, k)
+
+
+@pytest.mark.parametrize("variant", [16, 17, 18], ids=["dma1x1h_192", "dma1x1h_128", "dma1x1h_64"])
+def test_half_height_1x1_variants_give_identical_bits_on_nbt(model_dir, variant):
+    """The 192-row 1x1 kernels on C2's nested-bottleneck shapes, including
+    the post 1x1 conv whose residual is loaded into the accumulators through
+    the stage that shares the A buffers: bitwise the built-in outputs."""
+    cfg = modelgen.configs()[2]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    n = 12  # batches of 8 boards or fewer are not tuned
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, n, board_sizes=(19, 13))
+    tuned = nn.ComputeHandle(nn.ComputeContext(lm, use_fp16=True, auto_tune=True, tuner_file=str(model_dir) + "/t_nbt.txt"),
+                             max_batch=n)
+    shapes = [l.split()[:8] for l in tuned.tuning()[1].splitlines() if l.strip()]
+    assert any(k[0] == "1" and k[6] == "1" for k in shapes)  # a 1x1 shape with a residual
+    ref = _forward(nn.ComputeHandle(nn.ComputeContext(lm, use_fp16=True, auto_tune=False), max_batch=n), sp, gl)
+    tuned.set_tuning("".join(" ".join(k) + f" {variant}\n" for k in shapes))
+    out = _forward(tuned, sp, gl)
+    for k in out:
+        assert np.array_equal(out[k], ref[k]), k
