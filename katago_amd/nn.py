@@ -476,6 +476,13 @@ class DeviceHandle:
         hip_check(lib.kgh_handle_autotune(self._ptr, reps, buf, len(buf)))
         return buf.value.decode()
 
+    def set_tuning(self, table: str):
+        """kgh_handle_set_tuning: kernel choices per conv shape, in the format
+        autotune() returns."""
+        lib = hip_library()
+        lib.kgh_handle_set_tuning.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
+        hip_check(lib.kgh_handle_set_tuning(self._ptr, table.encode()))
+
     def set_profiling(self, on: bool):
         hip_check(hip_library().kgh_handle_set_profiling(self._ptr, int(on)))
 
