@@ -1431,6 +1431,12 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
     else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
     return true;
   }
+  // From 64 boards, 64-column tiles when they give at least 128 workgroups
+  // (b10c128 at 64 boards: 21-23 us per conv vs 30-35 us on 128-row tiles).
+  if(g.batch >= 64 && g.batch * (cout / 64) >= 128 && boardWindowFits(cinStride, cinPad, cout, 64, g, epi)) {
+    launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+    return true;
+  }
   if(g.W + 1 > TW_PAD_MAX || cinPad % 32 != 0 || cinStride % 8 != 0 || epi.maskResidualAdd) return false;
   if(M < 128L * TW_BM) return false;
   if(M * cinStride >= (1L << 31) || 9L * cout * cinPad >= (1L << 31)) return false;
