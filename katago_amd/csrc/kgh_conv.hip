@@ -1431,9 +1431,11 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
     else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
     return true;
   }
-  // From 64 boards, 64-column tiles when they give at least 128 workgroups
-  // (b10c128 at 64 boards: 21-23 us per conv vs 30-35 us on 128-row tiles).
-  if(g.batch >= 64 && g.batch * (cout / 64) >= 128 && boardWindowFits(cinStride, cinPad, cout, 64, g, epi)) {
+  // Below 128 boards, 64-column tiles (the most workgroups): at 1 to 64
+  // boards, b10c128's 3x3 convs take 19-23 us on them vs 28-35 us on the
+  // 128-row tiles, b18c384nbt's 22-29 us vs 42-57 us. The stem (one
+  // 32-channel chunk) stays on the tile kernel, which the tuner keeps there.
+  if(cinPad >= 64 && boardWindowFits(cinStride, cinPad, cout, 64, g, epi)) {
     launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
     return true;
   }
