@@ -1475,9 +1475,17 @@ template<>
 bool dispatch1x1Dma<half_t>(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                             const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   const long M = (long)g.batch * g.H * g.W;
-  // Enough workgroups (row tiles x column tiles) to fill most CUs.
-  if(cinPad % 32 != 0 || cinStride % 8 != 0 || (M + TW_BM - 1) / TW_BM * (cout / 64) < 3 * 128) return false;
+  if(cinPad % 32 != 0 || cinStride % 8 != 0) return false;
   if(M * cinStride >= (1L << 31) || (long)cout * cinPad >= (1L << 31)) return false;
+  // Too few 384-row tiles to fill most CUs: from 24 tiles of 192 rows, the
+  // 192-row kernel with 64-column tiles (two workgroups per CU; the tuner
+  // picks it for b18c384nbt's 1x1 convs at 16 to 64 boards, 12-20 us vs
+  // 18-24 us on the 128-row tile kernel); below that, the tile kernel.
+  if((M + TW_BM - 1) / TW_BM * (cout / 64) < 3 * 128) {
+    if(M < 24L * 192 || cout % 64 != 0) return false;
+    launch1x1Dma<64, 192>(x, cinStride, cinPad, cout, w, g, epi, stream);
+    return true;
+  }
   if(cout % 192 == 0) launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream);
   else if(cout % 128 == 0) launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream);
   else if(cout % 64 == 0) launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
@@ -1561,13 +1569,26 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
 template<typename T, int KS>
 bool dispatchMfmaTile(const T* x, int cinStride, int cinPad, int cout, const T* w, BoardGeom g, const ConvEpilogue<T>& epi,
                       hipStream_t stream) {
-  if(cout % 192 == 0) launchMfma<T, KS, 192, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
-  else if(cout % 128 == 0) launchMfma<T, KS, 128, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
-  else if(cout % 96 == 0) launchMfma<T, KS, 96, 4>(x, cinStride, cinPad, cout, w, g, epi, stream);
-  else if(cout % 64 == 0) launchMfma<T, KS, 64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
-  else if(cout % 32 == 0) launchMfma<T, KS, 32, 4>(x, cinStride, cinPad, cout, w, g, epi, stream);
-  else return false;
-  return true;
+  // The widest column tile dividing cout that still gives about three
+  // workgroups per CU; at small batches the narrowest one (the tuner picks
+  // 32-column tiles at 8 boards: b18c384nbt's 1x1 convs 10.7/12.2 us vs
+  // 17.1/20.3 us on 192-column tiles).
+  static const int bns[] = {192, 128, 96, 64, 32};
+  const long rowTiles = ((long)g.batch * g.H * g.W + CONV_BM - 1) / CONV_BM;
+  int bn = 0;
+  for(int cand : bns) {
+    if(cout % cand != 0) continue;
+    bn = cand;
+    if(rowTiles * (cout / cand) >= 3L * 256) break;
+  }
+  switch(bn) {
+    case 192: launchMfma<T, KS, 192, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return true;
+    case 128: launchMfma<T, KS, 128, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return true;
+    case 96: launchMfma<T, KS, 96, 4>(x, cinStride, cinPad, cout, w, g, epi, stream); return true;
+    case 64: launchMfma<T, KS, 64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return true;
+    case 32: launchMfma<T, KS, 32, 4>(x, cinStride, cinPad, cout, w, g, epi, stream); return true;
+    default: return false;
+  }
 }
 
 }  // namespace
