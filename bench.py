@@ -178,6 +178,7 @@ def main():
     ap.add_argument("--config", type=int, default=CFG_INDEX,
                     help="BASELINE.json config index; 2 (default) is the headline, 4 the transformer trunk")
     ap.add_argument("--no-autotune", action="store_true", help="keep the built-in kernel choices")
+    ap.add_argument("--batch", type=int, default=0, help="boards per forward instead of the config's (not the headline line)")
     ap.add_argument("--no-serve", action="store_true",
                     help="skip the PCIe-inclusive measurement through the batching evaluator")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -201,13 +202,13 @@ def main():
         return
 
     # Before anything here initialises the GPU.
-    vendor = vendor_gemm_rate() if args.config == CFG_INDEX else None
+    vendor = vendor_gemm_rate() if args.config == CFG_INDEX and not args.batch else None
 
     import numpy as np
     from katago_amd import modelgen, nn
 
     cfg = modelgen.configs()[args.config]
-    batch, hw = cfg.batch, 19 * 19
+    batch, hw = (args.batch or cfg.batch), 19 * 19
     model_dir = args.model_dir or os.path.join(tempfile.gettempdir(), "katago_amd_models")
     path = modelgen.ensure_model(model_dir, cfg)
     print(f"bench: model {path}", file=sys.stderr, flush=True)
@@ -261,7 +262,7 @@ def main():
     value = evals / elapsed
     print(f"bench: {args.steps} steps in {elapsed:.3f} s; profiled {prof_steps} eager steps: 3x3 conv {n3} launches "
           f"{ms3:.2f} ms total, 1x1 conv {n1} launches {ms1:.2f} ms total", file=sys.stderr, flush=True)
-    headline = args.config == CFG_INDEX
+    headline = args.config == CFG_INDEX and batch == cfg.batch
     # Roofline kernel: the 3x3 conv for the convolutional nets, the 1x1
     # (per-position GEMM) kernel for a transformer trunk.
     # Which 3x3 kernel runs: the one-board kernel for fp16 batches of 128 or

@@ -1424,20 +1424,25 @@ template<>
 bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                                const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   const long M = (long)g.batch * g.H * g.W;
-  // One board per workgroup: enough boards to fill most CUs.
-  if(g.batch >= 128 && boardWindowFits(cinStride, cinPad, cout, 64, g, epi)) {
-    if(cout % 192 == 0) launchBoardWindow<192>(x, cinStride, cinPad, cout, w, g, epi, stream);
-    else if(cout % 128 == 0) launchBoardWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream);
-    else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
-    return true;
-  }
-  // Below 128 boards, 64-column tiles (the most workgroups): at 1 to 64
-  // boards, b10c128's 3x3 convs take 19-23 us on them vs 28-35 us on the
-  // 128-row tiles, b18c384nbt's 22-29 us vs 42-57 us. The stem (one
-  // 32-channel chunk) stays on the tile kernel, which the tuner keeps there.
-  if(cinPad >= 64 && boardWindowFits(cinStride, cinPad, cout, 64, g, epi)) {
-    launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
-    return true;
+  // One board per workgroup. The widest column tile while it gives at least
+  // 160 workgroups; below that, 64-column tiles (the most workgroups), but
+  // not for the stem (one 32-channel chunk), which the tuner keeps on the
+  // tile kernel. Tuner measurements: at 128 boards the 64-column tiles take
+  // b10c128's convs in 23-26 us vs 29-33 us, b18c384nbt's in 50-55 us vs
+  // 52-57 us; at 192 boards the wide tiles win; at 1 to 96 boards the
+  // 64-column tiles beat the 128-row tile kernel by 1.5-2x.
+  if(boardWindowFits(cinStride, cinPad, cout, 64, g, epi)) {
+    const int wide = cout % 192 == 0 ? 192 : cout % 128 == 0 ? 128 : 64;
+    if((long)g.batch * (cout / wide) >= 160) {
+      if(wide == 192) launchBoardWindow<192>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      else if(wide == 128) launchBoardWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      return true;
+    }
+    if(cinPad >= 64) {
+      launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      return true;
+    }
   }
   if(g.W + 1 > TW_PAD_MAX || cinPad % 32 != 0 || cinStride % 8 != 0 || epi.maskResidualAdd) return false;
   if(M < 128L * TW_BM) return false;

@@ -286,9 +286,10 @@ def test_c2_full_batch_rows_are_independent(model_dir):
 
 
 def test_c1_batch_128_rows_are_independent(model_dir):
-    """b10c128 at 128 boards (19x19 and 13x13, all eight symmetries) runs its
-    3x3 convs on the one-board kernel (128 output channels); the same rows in
-    a batch of 4 take the 128-row tile kernels: bitwise equal."""
+    """b10c128 at 128 boards (19x19 and 13x13, all eight symmetries) and the
+    same rows in a batch of 4: the batches take different kernel choices
+    (column tiles, the stem's kernel), which sum in the same order: bitwise
+    equal."""
     cfg = modelgen.configs()[1]
     lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
     ctx = nn.ComputeContext(lm, 19, 19, use_fp16=True)
