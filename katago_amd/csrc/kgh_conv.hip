@@ -917,7 +917,6 @@ constexpr int BW_WIN_BYTES = BW_LOADS * 1024;
 constexpr int BW_BM = 384;
 constexpr int BW_WTM = BW_BM / BW_ROW_WAVES;           // 96 rows per wave
 constexpr int BW_MAX_CIN = 1024;
-constexpr int BW_WEIGHT_BUFS = 6;
 
 // Zero source of the window's border and gap slots (zero-initialised at load;
 // never written). Long enough for every chunk offset up to BW_MAX_CIN.
@@ -926,10 +925,17 @@ __device__ __attribute__((aligned(256))) half_t kZeroChannels[BW_MAX_CIN + 64];
 // Tap at which window load i (0..8) of a window wave is issued (taps 0..5).
 __host__ __device__ constexpr int winLoadTap(int i) { return i * 6 / BW_WIN_PER; }
 
-template<int BN>
+template<int BN, int NB>
 __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
                                                                       int cout, const half_t* __restrict__ w, int batch,
                                                                       ConvEpilogue<half_t> epi) {
+  // NB weight buffers, loaded LA = NB - 3 steps ahead: the DMA for step
+  // s + LA goes to buffer (s - 3) mod NB, free once step s - 1's barrier is
+  // passed. Nine buffers (six steps ahead) for 64-column tiles, whose small
+  // batches leave each step waiting on weight DMA latency; six otherwise
+  // (nine 192-column buffers would not fit in LDS).
+  static_assert(NB == 6 || NB == 9, "six or nine weight buffers");
+  constexpr int LA = NB - 3;
   constexpr int WTN = BN / 2;
   constexpr int RB = BW_WTM / 32;
   constexpr int CB = WTN / 32;
@@ -946,6 +952,9 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   __shared__ __attribute__((aligned(1024))) unsigned char wt3[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char wt4[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char wt5[BN * 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt6[NB > 6 ? BN * 64 : 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt7[NB > 6 ? BN * 64 : 64];
+  __shared__ __attribute__((aligned(1024))) unsigned char wt8[NB > 6 ? BN * 64 : 64];
   __shared__ __attribute__((aligned(1024))) unsigned char win0[BW_WIN_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char win1[BW_WIN_BYTES];
 
@@ -1009,8 +1018,8 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
                                        (lds_void_t*)(dst + (loader * B_PER + i) * 1024), 16, 0, 0);
   };
   auto wtBuf = [&](int i) -> unsigned char* {
-    i %= BW_WEIGHT_BUFS;
-    return i == 0 ? wt0 : i == 1 ? wt1 : i == 2 ? wt2 : i == 3 ? wt3 : i == 4 ? wt4 : wt5;
+    i %= NB;
+    return i == 0 ? wt0 : i == 1 ? wt1 : i == 2 ? wt2 : i == 3 ? wt3 : i == 4 ? wt4 : i == 5 ? wt5 : i == 6 ? wt6 : i == 7 ? wt7 : wt8;
   };
 
   // Byte offset of the lane's A rows at tap (dy, dx) = (-1, -1); rows past
@@ -1048,9 +1057,8 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   }
   // Prologue: weights of steps 0..2 and the window of chunk 0.
   if(loadsWeights) {
-    loadWeights(wt0, 0);
-    loadWeights(wt1, 1);
-    loadWeights(wt2, 2);
+#pragma unroll
+    for(int i = 0; i < LA; i++) loadWeights(wtBuf(i), i);
   }
   if(loadsWindow) {
 #pragma unroll
@@ -1083,17 +1091,18 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   // then (after the first half's matrix work) the first half-step fragments
   // of s + 1, whose weights landed before the previous barrier; the barrier
   // that ends step s publishes the weights of step s + 2.
-  auto chunk = [&](auto pTag, int c) {
-    constexpr int P = decltype(pTag)::value;  // 3 * (c % 2)
-    unsigned char* cur = P ? win1 : win0;
-    unsigned char* nxt = P ? win0 : win1;
+  auto chunk = [&](auto pTag, auto wTag, int c) {
+    constexpr int P = decltype(pTag)::value;  // 9c mod NB
+    constexpr int WP = decltype(wTag)::value;  // c mod 2
+    unsigned char* cur = WP ? win1 : win0;
+    unsigned char* nxt = WP ? win0 : win1;
     // The last chunk re-loads itself into the idle window (never read), so
     // every step issues the same loads.
     const int cNext = c + 1 < cChunks ? c + 1 : c;
 #pragma unroll
     for(int t = 0; t < 9; t++) {
       const unsigned char* wCur = wtBuf(P + t);
-      if(loadsWeights) loadWeights(wtBuf(P + t + 3), 9 * c + t + 3);
+      if(loadsWeights) loadWeights(wtBuf(P + t + LA), 9 * c + t + LA);
       if(loadsWindow) {
 #pragma unroll
         for(int i = 0; i < BW_WIN_PER; i++)
@@ -1118,14 +1127,14 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
       mma(a1, b1);
       // Weight waves: only the weights of step s + 3 may still be in flight.
       // Window waves: the next window is complete before step t = 8 reads it.
-      if(loadsWeights) waitVmcnt<B_PER>();
+      if(loadsWeights) waitVmcnt<(LA - 2) * B_PER>();
       else if(t == 7) waitVmcnt<0>();
       barrierNoFence();
     }
   };
   for(int c = 0; c < cChunks; c += 2) {
-    chunk(std::integral_constant<int, 0>(), c);
-    if(c + 1 < cChunks) chunk(std::integral_constant<int, 3>(), c + 1);
+    chunk(std::integral_constant<int, 0>(), std::integral_constant<int, 0>(), c);
+    if(c + 1 < cChunks) chunk(std::integral_constant<int, 9 % NB>(), std::integral_constant<int, 1>(), c + 1);
   }
   waitVmcnt<0>();
   __syncthreads();
@@ -1392,7 +1401,8 @@ template<int BN>
 void launchBoardWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                        const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   dim3 grid(g.batch * (cout / BN));
-  hipLaunchKernelGGL((convBoardWindowKernel<BN>), grid, dim3(BW_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g.batch, epi);
+  hipLaunchKernelGGL((convBoardWindowKernel<BN, BN == 64 ? 9 : 6>), grid, dim3(BW_THREADS), 0, stream, x, cinStride, cinPad, cout, w,
+                     g.batch, epi);
   KGH_CHECK_LAUNCH();
 }
 
