@@ -936,6 +936,10 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   // (nine 192-column buffers would not fit in LDS).
   static_assert(NB == 6 || NB == 9, "six or nine weight buffers");
   constexpr int LA = NB - 3;
+  // Taps per barrier: with nine buffers a chunk's nine taps run as three
+  // super-steps of three, one barrier each (the weights of a super-step are
+  // published by the barrier before it); with six, one barrier per tap.
+  constexpr int TPB = NB == 9 ? 3 : 1;
   constexpr int WTN = BN / 2;
   constexpr int RB = BW_WTM / 32;
   constexpr int CB = WTN / 32;
@@ -1121,15 +1125,26 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
 #pragma unroll
       for(int cb = 0; cb < CB; cb++) b1[cb] = bf[cb];
       // First half of step s + 1 (past the last step it re-reads valid LDS
-      // and is discarded).
-      if(t < 8) readHalf(cur, wtBuf(P + t + 1), t + 1, 0);
-      else readHalf(nxt, wtBuf(P + t + 1), 0, 0);
+      // and is discarded): before the barrier when its weights are already
+      // published, after it at a super-step boundary.
+      const bool boundary = (t % TPB) == TPB - 1;
+      auto readNext = [&]() {
+        if(t < 8) readHalf(cur, wtBuf(P + t + 1), t + 1, 0);
+        else readHalf(nxt, wtBuf(P + t + 1), 0, 0);
+      };
+      if(TPB == 1) readNext();
+      else if(!boundary) readNext();
       mma(a1, b1);
-      // Weight waves: only the weights of step s + 3 may still be in flight.
-      // Window waves: the next window is complete before step t = 8 reads it.
-      if(loadsWeights) waitVmcnt<(LA - 2) * B_PER>();
-      else if(t == 7) waitVmcnt<0>();
-      barrierNoFence();
+      if(boundary) {
+        // Weight waves: TPB = 1, the weights of step s + 2 have landed (only
+        // steps s + 3 .. s + LA may be in flight); TPB = 3, those of the
+        // next super-step (steps s + 1 .. s + 3). Window waves: the next
+        // window is complete before its first read.
+        if(loadsWeights) waitVmcnt<(TPB == 1 ? LA - 2 : LA - 3) * B_PER>();
+        else if(t == (TPB == 1 ? 7 : 8)) waitVmcnt<0>();
+        barrierNoFence();
+        if(TPB != 1) readNext();
+      }
     }
   };
   for(int c = 0; c < cChunks; c += 2) {
