@@ -7,6 +7,7 @@ the same workload, run right after the timed steps; and the same-run CPU
 baseline (the oracle: a restatement of KataGo's Eigen backend).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py --config 3 --batch 1      # C3 latency at batch 1
 
 Prints one JSON line.
 """
@@ -109,17 +110,25 @@ def vendor_gemm_rate(n=8192, iters=40):
     return {"tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1), "what": f"torch.matmul fp16 {n}x{n}x{n}, random N(0,1) operands"}
 
 
+# CPU threads this process may keep busy on a GPU box: its share of the host
+# is 16 CPUs per GPU, whatever the host's own core count is.
+BOX_CPU_SHARE = 16
+
+
 def cpu_baseline(path, seconds_target=15.0):
     """The oracle (fp32 Eigen-algorithm restatement) on T host threads, each
     running forwards of batch 8, as the reference's Eigen deployment runs one
-    single-threaded forward per server thread (eigenbackend.cpp:8-9)."""
+    single-threaded forward per server thread (eigenbackend.cpp:8-9). T is
+    every core of the affinity set, up to the GPU box's CPU share; the host's
+    hardware_concurrency and the affinity set size are reported beside it."""
     from katago_amd import modelgen
     from oracle import oracle
+    host_cores = os.cpu_count() or 1
     try:
-        cores = len(os.sched_getaffinity(0))
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    threads = max(1, min(cores, 16))
+        affinity = host_cores
+    threads = max(1, min(affinity, BOX_CPU_SHARE))
     om = oracle.OracleModel(path)
     sp, gl = modelgen.synthetic_inputs(2000 + CFG_INDEX, 8)
     t0 = time.perf_counter()
@@ -142,9 +151,45 @@ def cpu_baseline(path, seconds_target=15.0):
     for t in ths:
         t.join()
     wall = time.perf_counter() - t0
-    return {"value": round(done[0] / wall, 3), "unit": "evals/s", "cores": threads, "kind": "port",
+    value = done[0] / wall
+    return {"value": round(value, 3), "unit": "evals/s", "cores": threads, "kind": "port",
+            "host_hardware_concurrency": host_cores, "affinity_cores": affinity,
+            "per_thread": round(value / threads, 3),
             "sample": f"b18c384nbt fp32, Eigen-algorithm restatement (oracle/eigen_oracle.cpp), {threads} threads x "
-                      f"{iters} forwards x batch 8 = {done[0]} evals in {wall:.1f} s"}
+                      f"{iters} forwards x batch 8 = {done[0]} evals in {wall:.1f} s; threads = the affinity set "
+                      f"({affinity} of the host's {host_cores}) capped at the box's CPU share of {BOX_CPU_SHARE} per GPU"}
+
+
+def latency(h, call, lm, cfg, steps=200):
+    """Batch-1 latency: each forward timed alone on the host clock (launch to
+    synchronize), inputs resident in HBM; and the same through the host-memory
+    entry point (featurized row in pageable host memory -> pinned staging ->
+    H2D -> forward -> D2H), as a KataGo search thread waiting on one
+    evaluation sees it."""
+    import numpy as np
+    from katago_amd import modelgen, nn
+    lat = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        call()
+        h.synchronize()
+        lat.append(time.perf_counter() - t0)
+    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=cfg.fp16, auto_tune=False)
+    ch = nn.ComputeHandle(ctx, max_batch=1)
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, 1, board_sizes=cfg.board_sizes)
+    for _ in range(5):
+        ch.get_output(sp, gl)
+    host = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        ch.get_output(sp, gl)
+        host.append(time.perf_counter() - t0)
+    ch.close()
+    ctx.close()
+    q = lambda a, p: round(1000.0 * float(np.percentile(a, p)), 4)
+    return {"hbm_resident_ms": {"p50": q(lat, 50), "p90": q(lat, 90), "min": q(lat, 0)},
+            "pcie_inclusive_ms": {"p50": q(host, 50), "p90": q(host, 90), "min": q(host, 0)},
+            "forwards": steps, "what": "one board per forward, host wall clock from launch to synchronize"}
 
 
 def serve_rate(lm, cfg, batch, server_threads=2, rounds=40):
@@ -179,6 +224,7 @@ def main():
                     help="BASELINE.json config index; 2 (default) is the headline, 4 the transformer trunk")
     ap.add_argument("--no-autotune", action="store_true", help="keep the built-in kernel choices")
     ap.add_argument("--batch", type=int, default=0, help="boards per forward instead of the config's (not the headline line)")
+    ap.add_argument("--latency", action="store_true", help="also time single forwards (always on at --batch 1)")
     ap.add_argument("--no-serve", action="store_true",
                     help="skip the PCIe-inclusive measurement through the batching evaluator")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -257,6 +303,9 @@ def main():
     ms3, n3, fl3 = h.profile(0)
     ms1, n1, fl1 = h.profile(1)
     h.set_profiling(False)
+    # Every conv kernel together (3x3 and 1x1): the conv-kernel fraction of the
+    # dense peak as the target defines it, direct-conv FLOPs over conv time.
+    conv_frac = (fl3 + fl1) / ((ms3 + ms1) * 1e-3) / 1e12 if ms3 + ms1 > 0 else 0.0
 
     evals = batch * args.steps
     value = evals / elapsed
@@ -299,6 +348,12 @@ def main():
                    "autotuned_shapes": len([l for l in tuning.splitlines() if l.strip()])},
         "mfma_frac_end_to_end": round(value * flops_per_eval / (peak * 1e12), 4),
         "gflop_per_eval": round(flops_per_eval / 1e9, 3),
+        "conv_frac": {"achieved": round(conv_frac, 2), "peak": peak, "unit": "TFLOP/s",
+                      "frac": round(conv_frac / peak, 4), "frac_3x3": round((fl3 / (ms3 * 1e-3) / 1e12) / peak, 4) if ms3 else None,
+                      "frac_1x1": round((fl1 / (ms1 * 1e-3) / 1e12) / peak, 4) if ms1 else None,
+                      "ms_3x3": round(ms3 / prof_steps, 4), "ms_1x1": round(ms1 / prof_steps, 4),
+                      "what": "sum of direct-conv FLOPs of every 3x3 and 1x1 conv launch over the sum of their durations "
+                              "(HIP events), per forward"},
         "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2),
                      "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic() if headline else None, "avg_launch_ms": round(avg_ms, 5), "launches": n_k,
@@ -310,7 +365,9 @@ def main():
         result["roofline"]["vendor_gemm_sustained"] = vendor
         if vendor["tflops"]:
             result["roofline"]["frac_of_vendor_gemm"] = round(achieved / vendor["tflops"], 4)
-    if not args.no_serve:
+    if batch == 1 or args.latency:
+        result["latency"] = latency(h, call, lm, cfg)
+    if not args.no_serve and batch > 1:
         result["pcie_inclusive"] = serve_rate(lm, cfg, batch)
     if not args.no_cpu:
         print("bench: timing CPU baseline", file=sys.stderr, flush=True)

@@ -74,8 +74,8 @@ int32_t kgn_get_output(void* handle, void* loaded_model, int32_t nn_x, int32_t n
                        const int32_t* symmetry, const float* policy_optimism, float* policy, float* value, float* score,
                        float* ownership, char* err, int32_t errlen);
 
-/* kgn_get_output with device post-processing (NNResultBuf's
- * postProcessOnDevice extension): per row legal[nn_x*nn_y+1] (1 = legal),
+/* kgn_get_output with device post-processing
+ * (HipBackend::getOutputPostProcessed, katago_hip_backend.h): per row legal[nn_x*nn_y+1] (1 = legal),
  * row_info (KGH_POST_* flags | board_x << 8 | board_y << 16, katago_hip.h),
  * temperature. Rows with KGH_POST_ENABLED come back post-processed as
  * NNEvaluator::evaluate leaves them (nneval.cpp:946-1240): policy

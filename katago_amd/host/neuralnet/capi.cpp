@@ -7,6 +7,7 @@
 #include "../neuralnet/nneval.h"
 #include "../neuralnet/nninterface.h"
 #include "katago_hip.h"
+#include "katago_hip_backend.h"
 #include "katago_nn.h"
 
 void hipBackendFlattenModel(const ModelDesc& desc, std::vector<kgh_layer>& layers, std::vector<float>& weights);
@@ -213,6 +214,8 @@ int32_t kgn_get_output_post(void* h, void* m, int32_t nn_x, int32_t nn_y, int32_
     vector<NNResultBuf*> rowPtrs;
     vector<std::unique_ptr<NNOutput>> outs;
     vector<NNOutput*> outPtrs;
+    vector<HipBackend::RowPostProcess> post(n);
+    vector<const HipBackend::RowPostProcess*> postPtrs(n, nullptr);
     for(int i = 0; i < n; i++) {
       rows.emplace_back(new NNResultBuf());
       NNResultBuf& r = *rows.back();
@@ -221,14 +224,17 @@ int32_t kgn_get_output_post(void* h, void* m, int32_t nn_x, int32_t nn_y, int32_
       r.symmetry = symmetry[i];
       r.policyOptimism = policy_optimism[i];
       const int info = row_info[i];
-      r.postProcessOnDevice = (info & KGH_POST_ENABLED) != 0;
-      r.nextPlayerIsWhite = (info & KGH_POST_WHITE_TO_MOVE) != 0;
-      r.noResultDisabled = (info & KGH_POST_NO_RESULT_DISABLED) != 0;
-      r.enablePassingHacks = (info & KGH_POST_PASSING_HACKS) != 0;
-      r.boardXSizeForServer = (info >> 8) & 0xff;
-      r.boardYSizeForServer = (info >> 16) & 0xff;
-      r.nnPolicyTemperature = temperature[i];
-      r.rowLegalBuf.assign(legal + (size_t)(HW + 1) * i, legal + (size_t)(HW + 1) * (i + 1));
+      HipBackend::RowPostProcess& p = post[i];
+      p.legal = legal + (size_t)(HW + 1) * i;
+      p.nextPlayerIsWhite = (info & KGH_POST_WHITE_TO_MOVE) != 0;
+      p.noResultDisabled = (info & KGH_POST_NO_RESULT_DISABLED) != 0;
+      p.enablePassingHacks = (info & KGH_POST_PASSING_HACKS) != 0;
+      p.boardXSize = (info >> 8) & 0xff;
+      p.boardYSize = (info >> 16) & 0xff;
+      p.nnPolicyTemperature = temperature[i];
+      r.boardXSizeForServer = p.boardXSize;
+      r.boardYSizeForServer = p.boardYSize;
+      postPtrs[i] = (info & KGH_POST_ENABLED) != 0 ? &p : nullptr;
       rowPtrs.push_back(&r);
       outs.emplace_back(new NNOutput());
       NNOutput& o = *outs.back();
@@ -238,7 +244,7 @@ int32_t kgn_get_output_post(void* h, void* m, int32_t nn_x, int32_t nn_y, int32_
       o.whiteOwnerMap = ownership + (size_t)HW * i;
       outPtrs.push_back(&o);
     }
-    NeuralNet::getOutput((ComputeHandle*)h, bufs.get(), n, rowPtrs.data(), outPtrs);
+    HipBackend::getOutputPostProcessed((ComputeHandle*)h, bufs.get(), n, rowPtrs.data(), postPtrs.data(), outPtrs);
     for(int i = 0; i < n; i++) {
       const NNOutput& o = *outPtrs[i];
       memcpy(policy + (size_t)(HW + 1) * i, o.policyProbs, (size_t)(HW + 1) * sizeof(float));

@@ -25,6 +25,7 @@
 #include "../neuralnet/modelversion.h"
 #include "../neuralnet/nneval.h"
 #include "katago_hip.h"
+#include "katago_hip_backend.h"
 
 static const int HIP_TUNER_VERSION = 1;
 static const char* HIP_TUNER_VERSION_LINE = "VERSION=2";
@@ -574,8 +575,12 @@ InputBuffers* NeuralNet::createInputBuffers(const LoadedModel* loadedModel, int 
 
 void NeuralNet::freeInputBuffers(InputBuffers* buffers) { delete buffers; }
 
-void NeuralNet::getOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFilled, NNResultBuf** inputBufs,
-                          vector<NNOutput*>& outputs) {
+namespace {
+
+// NeuralNet::getOutput, and HipBackend::getOutputPostProcessed when post is
+// non-null: rows i with post[i] set come back post-processed on the device.
+void runGetOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFilled, NNResultBuf** inputBufs,
+                  const HipBackend::RowPostProcess* const* post, vector<NNOutput*>& outputs) {
   const int n = numBatchEltsFilled;
   if(n <= 0 || n > b->maxBatchSize || n > h->maxBatchSize)
     throw StringError("HIP backend: numBatchEltsFilled " + Global::intToString(n) + " outside 1..maxBatchSize");
@@ -600,27 +605,28 @@ void NeuralNet::getOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFil
     h->stSymmetry[i] = row.symmetry;
     h->stOptimism[i] = (float)row.policyOptimism;
   }
-  // Rows asking for device post-processing (an extension of the reference's
-  // NNResultBuf) carry their legal moves, side to move and rules.
+  // Rows asking for device post-processing carry their legal moves, side to
+  // move and rules beside the row (HipBackend::RowPostProcess).
   bool anyPost = false;
-  for(int i = 0; i < n; i++) anyPost = anyPost || inputBufs[i]->postProcessOnDevice;
+  for(int i = 0; i < n && post != nullptr; i++) anyPost = anyPost || post[i] != nullptr;
   if(anyPost) {
     const size_t policySize = (size_t)HW + 1;
     for(int i = 0; i < n; i++) {
-      const NNResultBuf& row = *inputBufs[i];
+      const HipBackend::RowPostProcess* p = post[i];
       int32_t info = 0;
-      if(row.postProcessOnDevice) {
-        if(row.rowLegalBuf.size() < policySize) throw StringError("HIP backend: rowLegalBuf smaller than the policy size");
-        memcpy(h->stLegal + policySize * i, row.rowLegalBuf.data(), policySize);
-        info = KGH_POST_ENABLED | (row.nextPlayerIsWhite ? KGH_POST_WHITE_TO_MOVE : 0) |
-               (row.noResultDisabled ? KGH_POST_NO_RESULT_DISABLED : 0) | (row.enablePassingHacks ? KGH_POST_PASSING_HACKS : 0) |
-               (row.boardXSizeForServer << 8) | (row.boardYSizeForServer << 16);
-        if(row.boardXSizeForServer <= 0 || row.boardXSizeForServer > nnX || row.boardYSizeForServer <= 0 ||
-           row.boardYSizeForServer > nnY)
+      float temperature = 1.0f;
+      if(p != nullptr) {
+        if(p->legal == nullptr) throw StringError("HIP backend: post-processed row without legal moves");
+        memcpy(h->stLegal + policySize * i, p->legal, policySize);
+        info = KGH_POST_ENABLED | (p->nextPlayerIsWhite ? KGH_POST_WHITE_TO_MOVE : 0) |
+               (p->noResultDisabled ? KGH_POST_NO_RESULT_DISABLED : 0) | (p->enablePassingHacks ? KGH_POST_PASSING_HACKS : 0) |
+               (p->boardXSize << 8) | (p->boardYSize << 16);
+        if(p->boardXSize <= 0 || p->boardXSize > nnX || p->boardYSize <= 0 || p->boardYSize > nnY)
           throw StringError("HIP backend: post-processed row with a board size outside the net's");
+        temperature = p->nnPolicyTemperature;
       }
       h->stInfo[i] = info;
-      h->stTemperature[i] = row.nnPolicyTemperature;
+      h->stTemperature[i] = temperature;
     }
     checkKgh(kgh_forward_staged_post(h->handle, n, &h->postParams), "kgh_forward_staged_post");
   }
@@ -633,7 +639,7 @@ void NeuralNet::getOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFil
     NNOutput* out = outputs[i];
     if(out->nnXLen != nnX || out->nnYLen != nnY) throw StringError("HIP backend: NNOutput board size mismatch");
     out->policyOptimismUsed = (float)inputBufs[i]->policyOptimism;
-    if(inputBufs[i]->postProcessOnDevice) {
+    if(anyPost && post[i] != nullptr) {
       const float* r = h->stPost + postFloats * i;
       memcpy(out->policyProbs, r, (size_t)(HW + 1) * sizeof(float));
       for(int k = HW + 1; k < NNPos::MAX_NN_POLICY_SIZE; k++) out->policyProbs[k] = -1.0f;
@@ -690,6 +696,18 @@ void NeuralNet::getOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFil
     }
     if(out->whiteOwnerMap != nullptr) memcpy(out->whiteOwnerMap, sc + h->numScore, (size_t)HW * sizeof(float));
   }
+}
+
+}  // namespace
+
+void NeuralNet::getOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFilled, NNResultBuf** inputBufs,
+                          vector<NNOutput*>& outputs) {
+  runGetOutput(h, b, numBatchEltsFilled, inputBufs, nullptr, outputs);
+}
+
+void HipBackend::getOutputPostProcessed(ComputeHandle* h, InputBuffers* b, int numBatchEltsFilled, NNResultBuf** inputBufs,
+                                        const RowPostProcess* const* post, vector<NNOutput*>& outputs) {
+  runGetOutput(h, b, numBatchEltsFilled, inputBufs, post, outputs);
 }
 
 // ---------------------------------------------------------------------------

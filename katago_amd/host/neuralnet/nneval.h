@@ -49,16 +49,6 @@ struct NNResultBuf {
   int symmetry = 0;            // the symmetry to use, or NNInputs::SYMMETRY_NOTSPECIFIED
   double policyOptimism = 0.0;
 
-  // Device post-processing, an extension of the reference's record: with
-  // postProcessOnDevice set, getOutput returns this row as
-  // NNEvaluator::evaluate leaves it after post-processing (nneval.cpp:946-1240:
-  // probabilities, -1 for illegal moves, white's perspective) instead of raw.
-  bool postProcessOnDevice = false;
-  std::vector<uint8_t> rowLegalBuf;  // nnXLen*nnYLen + 1 entries, pass last; 1 = legal (history.isLegal)
-  bool nextPlayerIsWhite = false;
-  bool noResultDisabled = false;     // rules.koRule != KO_SIMPLE && rules.scoringRule != SCORING_TERRITORY
-  bool enablePassingHacks = false;   // nnInputParams.enablePassingHacks
-  float nnPolicyTemperature = 1.0f;  // nnInputParams.nnPolicyTemperature
 
   NNResultBuf() = default;
   NNResultBuf(const NNResultBuf&) = delete;

@@ -435,6 +435,11 @@ def configs() -> list[Config]:
 # Synthetic inputs
 
 
+def board_xy(bs):
+    """(x, y) size of a board given as a side length or an (x, y) pair."""
+    return (bs, bs) if np.isscalar(bs) else (int(bs[0]), int(bs[1]))
+
+
 def synthetic_inputs(seed: int, n: int, nn_x: int = 19, nn_y: int = 19, board_sizes=(19,), num_spatial: int = 22,
                      num_global: int = 19):
     """Rows of NHWC spatial features and global features.
@@ -443,15 +448,16 @@ def synthetic_inputs(seed: int, n: int, nn_x: int = 19, nn_y: int = 19, board_si
     top-left as in nninputs.h:23-38); plane 1 is Bernoulli(0.35) on-board;
     plane 2 is Bernoulli(0.35) on on-board points not in plane 1; planes 3..
     are Bernoulli(0.1) on-board. Globals are U(-1, 1). Board sizes cycle per
-    row through board_sizes.
+    row through board_sizes; an entry is a side length or an (x, y) pair for
+    a rectangular board.
     """
     rng = SplitMix64(seed)
     hw = nn_x * nn_y
     spatial = np.zeros((n, nn_y, nn_x, num_spatial), dtype=np.float32)
     for i in range(n):
-        bs = board_sizes[i % len(board_sizes)]
+        bx, by = board_xy(board_sizes[i % len(board_sizes)])
         on = np.zeros((nn_y, nn_x), dtype=bool)
-        on[:min(bs, nn_y), :min(bs, nn_x)] = True
+        on[:min(by, nn_y), :min(bx, nn_x)] = True
         u = rng.uniform(hw * num_spatial).reshape(nn_y, nn_x, num_spatial)
         spatial[i, :, :, 0] = on
         p1 = (u[:, :, 1] < 0.35) & on

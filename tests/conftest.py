@@ -36,3 +36,15 @@ def model_dir(tmp_path_factory):
 
 
 GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    try:
+        from helpers import ARGMAX_ROWS, ARGMAX_TIES
+    except ImportError:
+        return
+    if ARGMAX_ROWS[0] == 0:
+        return
+    terminalreporter.write_line(f"argmax tie allowance used on {len(ARGMAX_TIES)} of {ARGMAX_ROWS[0]} whole-net rows compared")
+    for line in ARGMAX_TIES:
+        terminalreporter.write_line("  " + line)
