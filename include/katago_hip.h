@@ -188,6 +188,23 @@ int kgh_forward_device(kgh_handle* handle, int32_t n, const float* d_spatial, co
                        const int32_t* d_symmetry, const float* d_policy_optimism, float* d_out);
 int kgh_handle_synchronize(kgh_handle* handle);
 
+/* kgh_forward_device without a handle, for callers that cannot allocate:
+ * code under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc. No counterpart in the reference. It allocates nothing: the
+ * activations live in a static device array of the library (64 MiB per GPU
+ * it runs on, held until the process ends, less a 64 KiB guard), set up by
+ * kgh_model_create. Same layouts and results as kgh_forward_device with the
+ * built-in kernel choices (bitwise). Runs on hip_stream (a hipStream_t, NULL
+ * for the null stream), asynchronously; the caller synchronizes. n boards of
+ * nn_x by nn_y must fit the array (C2's b18c384nbt: about 44 boards at 19x19),
+ * else KGH_ERR_INVALID_ARGUMENT names the bytes needed; nets with attention
+ * blocks return KGH_ERR_UNSUPPORTED (their rotary tables live in a handle).
+ * Every call on one GPU shares the array: calls that overlap on one GPU race
+ * and must be serialized by the caller (one stream, or events). */
+int kgh_forward_device_noalloc(kgh_model* model, int32_t n, int32_t nn_x, int32_t nn_y, const float* d_spatial,
+                               const float* d_global, const int32_t* d_symmetry, const float* d_policy_optimism, float* d_out,
+                               void* hip_stream);
+
 /* Device allocation helpers so that callers without a HIP runtime binding can
  * stage device-resident inputs (used by the benchmark). */
 int kgh_device_alloc(int32_t device, size_t bytes, void** ptr);

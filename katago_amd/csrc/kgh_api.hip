@@ -1254,6 +1254,88 @@ void requireHandle(kgh_handle* h) {
 
 }  // namespace
 
+namespace {
+
+// The activation buffers of a forward of up to maxBatch boards of nn_x by
+// nn_y, in the model's element type, handed out by take(bytes): the handle's
+// arena (kgh_handle_create) or the static scratch (kgh_forward_device_noalloc).
+// Returns the bytes taken, each buffer rounded up to 256.
+template<typename Take>
+size_t carveActivations(kgh_handle* h, int maxBatch, int nn_x, int nn_y, Take&& take) {
+  const Net& net = h->model->net;
+  const size_t M = (size_t)maxBatch * nn_x * nn_y;
+  const size_t es = net.fp16 ? 2 : 4;
+  const size_t B = (size_t)maxBatch;
+  size_t total = 0;
+  auto get = [&](size_t bytes) {
+    total += roundUp(std::max<size_t>(bytes, 256), 256);
+    return take(bytes);
+  };
+  auto getF = [&](size_t n) { return (float*)get(n * sizeof(float)); };
+  h->x0 = get(M * net.inputCPad * es);
+  h->mask = getF(M);
+  h->maskSum = getF(B);
+  h->gbias = getF(B * net.trunkC);
+  h->R.clear();
+  h->A.clear();
+  for(int c : net.depthC) {
+    h->R.push_back(get(M * c * es));
+    h->A.push_back(get(M * c * es));
+  }
+  const size_t tmpC = std::max(net.tmpC, 1);
+  h->tmp1 = get(M * tmpC * es);
+  h->tmp2 = get(M * tmpC * es);
+  h->tmp3 = get(M * tmpC * es);
+  h->nbias = getF(B * tmpC);
+  h->p1 = get(M * net.p1C * es);
+  h->gv = get(M * (net.g1C + net.v1C) * es);
+  h->g1Bias = getF(B * net.p1C);
+  h->headFeatLd = 3 * net.g1C + 3 * net.v1C + std::max(net.passMul.cout, net.v2Mul.cout);
+  h->headFeat = getF(B * h->headFeatLd);
+  h->pass = getF(B * net.policyC);
+  h->value = getF(B * 3);
+  h->score = getF(B * net.scoreC);
+  h->policyRaw = getF(M * net.policyC);
+  h->ownRaw = getF(M);
+  return total;
+}
+
+// ---------------------------------------------------------------------------
+// The device-resident scratch of kgh_forward_device_noalloc: one array per
+// GPU, allocated when the code object loads and held until the process ends.
+// A caller that cannot allocate (inside HIP graph capture, in a serving loop
+// that forbids hipMalloc) runs forwards in it. Calls that overlap on one GPU
+// share it and race; nothing in it needs to start at zero (every forward
+// writes each buffer before reading it).
+constexpr size_t KGH_NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;
+// Never handed out: keeps any read just past the last buffer inside the array.
+constexpr size_t KGH_NOALLOC_GUARD_BYTES = (size_t)64 << 10;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[KGH_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratchMutex;
+std::map<int, unsigned char*> g_scratchAddr;  // device -> address of its copy of scratch
+
+// The device address of the current device's copy of scratch, looked up once
+// per device (the host-side name of the array is only a stand-in for it).
+unsigned char* scratchAddress(int device) {
+  std::lock_guard<std::mutex> lock(g_scratchMutex);
+  auto it = g_scratchAddr.find(device);
+  if(it != g_scratchAddr.end()) return it->second;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if(e != hipSuccess || p == nullptr)
+    throw KghError(KGH_ERR_HIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+  g_scratchAddr[device] = (unsigned char*)p;
+  return (unsigned char*)p;
+}
+
+}  // namespace
+
 // ===========================================================================
 // C ABI
 
@@ -1292,6 +1374,7 @@ int kgh_model_create(int32_t device, const kgh_model_desc* desc, int32_t use_fp1
     if(desc->weights == nullptr && desc->num_weights > 0) invalid("null weights");
     *out = nullptr;
     KGH_HIP_CHECK(hipSetDevice(device));
+    scratchAddress(device);  // set-up of kgh_forward_device_noalloc's scratch on this device
     std::unique_ptr<kgh_model> m(new kgh_model());
     m->device = device;
     m->net.fp16 = use_fp16 != 0;
@@ -1334,31 +1417,8 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     h->exact = require_exact_nn_len != 0;
     KGH_HIP_CHECK(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
     const size_t M = (size_t)max_batch * nn_x * nn_y;
-    const size_t es = net.fp16 ? 2 : 4;
     DeviceArena& a = h->arena;
-    h->x0 = a.alloc(M * net.inputCPad * es);
-    h->mask = a.allocN<float>(M);
-    h->maskSum = a.allocN<float>(max_batch);
-    h->gbias = a.allocN<float>((size_t)max_batch * net.trunkC);
-    for(int c : net.depthC) {
-      h->R.push_back(a.alloc(M * c * es));
-      h->A.push_back(a.alloc(M * c * es));
-    }
-    size_t tmpC = std::max(net.tmpC, 1);
-    h->tmp1 = a.alloc(M * tmpC * es);
-    h->tmp2 = a.alloc(M * tmpC * es);
-    h->tmp3 = a.alloc(M * tmpC * es);
-    h->nbias = a.allocN<float>((size_t)max_batch * tmpC);
-    h->p1 = a.alloc(M * net.p1C * es);
-    h->gv = a.alloc(M * (net.g1C + net.v1C) * es);
-    h->g1Bias = a.allocN<float>((size_t)max_batch * net.p1C);
-    h->headFeatLd = 3 * net.g1C + 3 * net.v1C + std::max(net.passMul.cout, net.v2Mul.cout);
-    h->headFeat = a.allocN<float>((size_t)max_batch * h->headFeatLd);
-    h->pass = a.allocN<float>((size_t)max_batch * net.policyC);
-    h->value = a.allocN<float>((size_t)max_batch * 3);
-    h->score = a.allocN<float>((size_t)max_batch * net.scoreC);
-    h->policyRaw = a.allocN<float>(M * net.policyC);
-    h->ownRaw = a.allocN<float>(M);
+    carveActivations(h.get(), max_batch, nn_x, nn_y, [&](size_t bytes) { return a.alloc(bytes); });
     // Rotary tables per attention block, [table][pair][y * nn_x + x]: the
     // angle formulas of TransformerAttentionDesc::computeRopeCosSin
     // (desc.cpp:1212-1275).
@@ -1466,6 +1526,51 @@ void forwardStaged(kgh_handle* handle, int n) {
   KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
 }
 }  // namespace
+
+int kgh_forward_device_noalloc(kgh_model* model, int32_t n, int32_t nn_x, int32_t nn_y, const float* d_spatial,
+                               const float* d_global, const int32_t* d_symmetry, const float* d_policy_optimism, float* d_out,
+                               void* hip_stream) {
+  return guarded([&] {
+    requireModel(model);
+    if(n <= 0) invalid("batch size must be positive");
+    if(nn_x <= 0 || nn_y <= 0 || nn_x > 64 || nn_y > 64) invalid("nn_x and nn_y must be in 1..64");
+    if(!d_spatial || !d_global || !d_symmetry || !d_policy_optimism || !d_out) invalid("null device pointer");
+    if(!model->net.ropes.empty())
+      unsupported("kgh_forward_device_noalloc: attention blocks need rotary tables per board size, which only a handle "
+                  "holds; use kgh_forward_device");
+    KGH_HIP_CHECK(hipSetDevice(model->device));
+    unsigned char* base = scratchAddress(model->device);
+    const size_t limit = KGH_NOALLOC_SCRATCH_BYTES - KGH_NOALLOC_GUARD_BYTES;
+    // A view of a handle whose buffers are carved from the scratch: no stream,
+    // staging, graphs or tuning of its own (the built-in kernel choices, which
+    // give the same results as any tuned choice).
+    kgh_handle view;
+    view.model = model;
+    view.maxBatch = n;
+    view.H = nn_y;
+    view.W = nn_x;
+    view.rowFloats = kgh_output_row_floats(nn_x, nn_y, model->net.scoreC);
+    size_t used = 0;
+    const size_t need = carveActivations(&view, n, nn_x, nn_y, [&](size_t bytes) -> void* {
+      void* p = base + used;
+      used += roundUp(std::max<size_t>(bytes, 256), 256);
+      return p;
+    });
+    if(need > limit) {
+      const size_t perBoard = (need + n - 1) / n;
+      invalid("kgh_forward_device_noalloc: " + std::to_string(n) + " boards of " + std::to_string(nn_x) + "x" + std::to_string(nn_y) +
+              " need " + std::to_string(need) + " bytes of scratch; the static scratch holds " + std::to_string(limit) +
+              " (about " + std::to_string(limit / perBoard) + " boards of this model at this size)");
+    }
+    struct StreamGuard {
+      kgh_handle& v;
+      ~StreamGuard() { v.stream = nullptr; }  // the caller's stream: never destroyed here
+    } guard{view};
+    view.stream = (hipStream_t)hip_stream;
+    if(model->net.fp16) forwardImpl<half_t>(&view, n, d_spatial, d_global, d_symmetry, d_policy_optimism, d_out);
+    else forwardImpl<float>(&view, n, d_spatial, d_global, d_symmetry, d_policy_optimism, d_out);
+  });
+}
 
 int kgh_forward(kgh_handle* handle, int32_t n, const float* spatial, const float* global_in, const int32_t* symmetry,
                 const float* policy_optimism, float* out) {

@@ -428,6 +428,15 @@ class DeviceModel:
                                          ctypes.POINTER(ctypes.c_void_p)]
         hip_check(lib.kgh_model_create(device, ctypes.byref(d), int(use_fp16), ctypes.byref(self._ptr)))
 
+    def forward_device_noalloc(self, n, nn_x, nn_y, d_spatial, d_global, d_sym, d_opt, d_out, stream=None):
+        """kgh_forward_device_noalloc: a forward in the library's static device
+        scratch, on `stream` (a hipStream_t as an int, None for the null
+        stream); asynchronous."""
+        lib = hip_library()
+        lib.kgh_forward_device_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32] + \
+            [ctypes.c_void_p] * 6
+        hip_check(lib.kgh_forward_device_noalloc(self._ptr, n, nn_x, nn_y, d_spatial, d_global, d_sym, d_opt, d_out, stream))
+
     def close(self):
         if getattr(self, "_ptr", None) and self._ptr.value:
             hip_library().kgh_model_free(self._ptr)
