@@ -4,6 +4,9 @@
   katago_amd/lib/libkatago_host.so  g++: ModelDesc parser, NeuralNet::* backend
                                     (hipbackend.cpp) and its C shim (include/katago_nn.h)
   oracle/liboracle_eigen.so         g++: CPU oracle (test infrastructure)
+  oracle/_ref/                      g++: KataGo's own featurizer and model parser
+                                    built from the reference sources (checkers;
+                                    only where /root/reference exists)
 
 Every call recompiles (the driver uses it as the "does it build" check).
 Objects go to katago_amd/_build/. Run as ``python -m katago_amd.build``.
@@ -124,6 +127,20 @@ def build_oracle() -> str:
     return out
 
 
+REF_CPP = "/root/reference/cpp"
+
+
+def build_ref() -> str | None:
+    """oracle/_ref: KataGo's own featurizer and model parser compiled from the
+    reference sources where they lie (oracle/Makefile.ref), as checkers for the
+    tests' fixtures. Only where the reference tree exists (this container);
+    the GPU boxes use what was built here."""
+    if not os.path.isdir(REF_CPP):
+        return None
+    _run(["make", "-B", "-s", "-j8", "-f", os.path.join(ORACLE_DIR, "Makefile.ref"), f"REF={REF_CPP}"] + ["-C", ROOT])
+    return os.path.join(ORACLE_DIR, "_ref")
+
+
 def build_all(verbose: bool = True) -> None:
     with cf.ThreadPoolExecutor(max_workers=2) as ex:
         f_oracle = ex.submit(build_oracle)
@@ -136,6 +153,9 @@ def build_all(verbose: bool = True) -> None:
     host = build_host()
     if verbose:
         print("built", host, flush=True)
+    ref = build_ref()
+    if verbose and ref:
+        print("built", ref, flush=True)
 
 
 if __name__ == "__main__":

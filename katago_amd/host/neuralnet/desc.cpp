@@ -1180,6 +1180,11 @@ void ModelDesc::loadFromMemory(const string& data, bool binaryFloats, ModelDesc&
 }
 
 void ModelDesc::loadFromFileMaybeGZipped(const string& fileName, ModelDesc& descBuf, const string& expectedSha256) {
+  loadFromFileMaybeGZipped(fileName, descBuf, expectedSha256, true);
+}
+
+void ModelDesc::loadFromFileMaybeGZipped(const string& fileName, ModelDesc& descBuf, const string& expectedSha256,
+                                         bool applyLoadTimeTransforms) {
   try {
     string raw;
     readWholeFile(fileName, raw);
@@ -1216,7 +1221,7 @@ void ModelDesc::loadFromFileMaybeGZipped(const string& fileName, ModelDesc& desc
     else {
       throw StringError("Model file should end with .txt, .bin, .txt.gz, .bin.gz, or possibly just .gz.");
     }
-    descBuf.transformToReduceActivations();
+    if(applyLoadTimeTransforms) descBuf.transformToReduceActivations();
   }
   catch(const StringError& e) {
     throw StringError("Error loading or parsing model file " + fileName + ": " + e.what());

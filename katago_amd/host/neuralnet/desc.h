@@ -444,6 +444,11 @@ struct ModelDesc {
   // Loads .txt/.bin/.txt.gz/.bin.gz/.gz, verifying sha256 if expectedSha256 is
   // nonempty, then applies transformToReduceActivations().
   static void loadFromFileMaybeGZipped(const std::string& fileName, ModelDesc& descBuf, const std::string& expectedSha256);
+  // The same without transformToReduceActivations when applyLoadTimeTransforms
+  // is false (no counterpart in the reference, which always applies it): lets
+  // tests check that the transform leaves a net's outputs unchanged.
+  static void loadFromFileMaybeGZipped(const std::string& fileName, ModelDesc& descBuf, const std::string& expectedSha256,
+                                       bool applyLoadTimeTransforms);
   // Same, from an in-memory (already decompressed) model file.
   static void loadFromMemory(const std::string& data, bool binaryFloats, ModelDesc& descBuf);
 };

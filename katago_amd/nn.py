@@ -147,7 +147,10 @@ class LoadedModel:
             self._ptr = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # at interpreter exit the library may already be gone
+            pass
 
 
 class ComputeContext:
@@ -175,7 +178,10 @@ class ComputeContext:
             self._ptr = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # at interpreter exit the library may already be gone
+            pass
 
 
 class ComputeHandle:
@@ -266,7 +272,10 @@ class ComputeHandle:
             self._ptr = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # at interpreter exit the library may already be gone
+            pass
 
 
 class Evaluator:
@@ -344,7 +353,10 @@ class Evaluator:
             self._ptr = None
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # at interpreter exit the library may already be gone
+            pass
 
 
 TEST_CONV, TEST_BATCHNORM, TEST_RESIDUAL, TEST_GPOOL = 0, 1, 2, 3
@@ -443,7 +455,10 @@ class DeviceModel:
             self._ptr = ctypes.c_void_p()
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # at interpreter exit the library may already be gone
+            pass
 
 
 class DeviceHandle:
@@ -512,7 +527,10 @@ class DeviceHandle:
             self._ptr = ctypes.c_void_p()
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # at interpreter exit the library may already be gone
+            pass
 
 
 POST_ENABLED, POST_WHITE_TO_MOVE, POST_NO_RESULT_DISABLED, POST_PASSING_HACKS = 1, 2, 4, 8

@@ -748,9 +748,16 @@ struct OracleModel {
 extern "C" {
 
 void* oracle_load_model(const char* path, int nn_x, int nn_y, char* err, int errlen) {
+  return oracle_load_model_ex(path, nn_x, nn_y, 1, err, errlen);
+}
+
+// apply_transforms = 0 skips transformToReduceActivations (desc.cpp:2631 in
+// the reference, which always applies it): the net is evaluated with its BN
+// scales where the file has them, for the transform's invariance test.
+void* oracle_load_model_ex(const char* path, int nn_x, int nn_y, int apply_transforms, char* err, int errlen) {
   try {
     std::unique_ptr<OracleModel> m(new OracleModel());
-    ModelDesc::loadFromFileMaybeGZipped(path, m->desc, "");
+    ModelDesc::loadFromFileMaybeGZipped(path, m->desc, "", apply_transforms != 0);
     m->nnX = nn_x;
     m->nnY = nn_y;
     m->model.reset(new Model(m->desc, nn_x, nn_y));

@@ -38,6 +38,7 @@ extern "C" {
 /* Loads a model file (ModelDesc::loadFromFileMaybeGZipped, with
  * transformToReduceActivations, no scale8) for boards of nn_x by nn_y. */
 void* oracle_load_model(const char* path, int nn_x, int nn_y, char* err, int errlen);
+void* oracle_load_model_ex(const char* path, int nn_x, int nn_y, int apply_transforms, char* err, int errlen);
 void oracle_free_model(void* model);
 
 /* NeuralNet::getOutput for n rows (same row layout as kgn_get_output). */

@@ -23,6 +23,8 @@ def lib() -> ctypes.CDLL:
         c = ctypes
         l.oracle_load_model.restype = c.c_void_p
         l.oracle_load_model.argtypes = [c.c_char_p, c.c_int, c.c_int, c.c_char_p, c.c_int]
+        l.oracle_load_model_ex.restype = c.c_void_p
+        l.oracle_load_model_ex.argtypes = [c.c_char_p, c.c_int, c.c_int, c.c_int, c.c_char_p, c.c_int]
         l.oracle_free_model.argtypes = [c.c_void_p]
         l.oracle_forward.argtypes = [c.c_void_p, c.c_int] + [c.c_void_p] * 8 + [c.c_char_p, c.c_int]
         l.oracle_test_evaluate.argtypes = [c.c_int, c.c_char_p, c.c_int, c.c_int, c.c_int, c.c_void_p, c.c_void_p,
@@ -35,10 +37,11 @@ def lib() -> ctypes.CDLL:
 
 
 class OracleModel:
-    def __init__(self, path: str, nn_x: int = 19, nn_y: int = 19):
+    def __init__(self, path: str, nn_x: int = 19, nn_y: int = 19, load_time_transforms: bool = True):
+        """load_time_transforms=False skips transformToReduceActivations."""
         err = ctypes.create_string_buffer(4096)
         self.nn_x, self.nn_y = nn_x, nn_y
-        self._ptr = lib().oracle_load_model(path.encode(), nn_x, nn_y, err, len(err))
+        self._ptr = lib().oracle_load_model_ex(path.encode(), nn_x, nn_y, int(load_time_transforms), err, len(err))
         if not self._ptr:
             raise RuntimeError(err.value.decode())
 

@@ -46,7 +46,11 @@ def raw_score_fields(score, model_version: int):
         return s[0], s[1], s[2], s[3], s[4], s[5]
     if model_version >= 8:
         return s[0], s[1], s[2], s[3], 0.0, 0.0
-    return s[0], s[1], s[0], 0.0, 0.0, 0.0
+    if model_version >= 4:
+        return s[0], s[1], s[0], 0.0, 0.0, 0.0
+    # Version 3 has one score channel; its square stands in for the second
+    # moment (eigenbackend.cpp:2596-2604).
+    return s[0], s[0] * s[0], s[0], 0.0, 0.0, 0.0
 
 
 def postprocess_row(policy, value, score, ownership, legal, *, nn_x: int, nn_y: int, board_x: int, board_y: int,
