@@ -18,15 +18,29 @@
  *    testnn.cpp:683-920 KAT.
  *  - poolRowsValueHead (:179-197), NestedBottleneckResidualBlock
  *    (:1254-1303), Trunk/PolicyHead/ValueHead/Model (:1897-2205) and the
- *    getOutput row handling (:2433-2616): an independent float64 numpy
- *    re-derivation built from torch.nn.functional.conv2d on small nets, plus
- *    invariants (batch independence, off-board inputs not affecting on-board
- *    outputs, symmetry bookkeeping against the reference's symmetry golden
- *    vectors in tests/results/runOutputTests.txt).
+ *    getOutput row handling (:2433-2616), with the model versions' score
+ *    channel routing: the whole-network outputs the reference's own tests
+ *    recorded (tests/test_whole_net_golden.py: runNNOnTinyBoardTest.txt,
+ *    model version 8, 5x5 board in a 6x6 tensor, symmetry 3;
+ *    runNNSymmetriesTest.txt, version 5, 9x13 board, all eight symmetries;
+ *    tinymodel.cpp, versions 9 and 11, ReLU and Mish nets, 19x19 and 13x6
+ *    boards), on input rows written by KataGo's own featurizer
+ *    (oracle/_ref), through the evaluator's post-processing; plus a float64
+ *    re-derivation (tests/torch_reference.py) and invariants (batch
+ *    independence, off-board inputs, the reference's symmetry golden vectors
+ *    of tests/results/runOutputTests.txt).
+ *  - The model parser and load-time transforms the oracle shares with the
+ *    backend (katago_amd/host/neuralnet/desc.cpp): every weight bitwise equal
+ *    to KataGo's own desc.cpp compiled from source (oracle/_ref/ref_modeldesc,
+ *    tests/test_parser_vs_reference.py, model versions 3 to 17), and
+ *    transformToReduceActivations leaving outputs unchanged to fp32 rounding
+ *    (tests/test_load_transforms.py).
  *  - Transformer attention / FFN blocks and the RMSNorm trunk tip
- *    (:867-1022, :1307-1707): parity unpinned by the reference (its
- *    gpu_error_reference_files are not committed); checked only against
- *    torch's scaled_dot_product_attention / RMSNorm / silu on small shapes.
+ *    (:867-1022, :1307-1707): no output of the reference pins them (its
+ *    gpu_error_reference_files are not committed); checked against a float64
+ *    re-derivation using torch's scaled_dot_product_attention, RMSNorm and
+ *    silu on small nets and on the reference's three in-repo transformer nets,
+ *    whose weights the parser reads bitwise as KataGo does.
  */
 #ifndef KATAGO_AMD_EIGEN_ORACLE_H
 #define KATAGO_AMD_EIGEN_ORACLE_H
@@ -38,6 +52,7 @@ extern "C" {
 /* Loads a model file (ModelDesc::loadFromFileMaybeGZipped, with
  * transformToReduceActivations, no scale8) for boards of nn_x by nn_y. */
 void* oracle_load_model(const char* path, int nn_x, int nn_y, char* err, int errlen);
+/* The same; apply_transforms = 0 skips transformToReduceActivations. */
 void* oracle_load_model_ex(const char* path, int nn_x, int nn_y, int apply_transforms, char* err, int errlen);
 void oracle_free_model(void* model);
 
