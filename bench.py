@@ -192,6 +192,71 @@ def latency(h, call, lm, cfg, steps=200):
             "forwards": steps, "what": "one board per forward, host wall clock from launch to synchronize"}
 
 
+def _fixture_positions(batch):
+    """Positions of KataGo's own random games (tests/golden/featurize_golden.json.gz)
+    in 19x19 tensors, repeated up to `batch`."""
+    import gzip
+    with gzip.open(os.path.join(ROOT, "tests", "golden", "featurize_golden.json.gz"), "rt") as f:
+        fixtures = [fx for fx in json.load(f)["positions"] if fx["nnx"] == 19 and fx["nny"] == 19]
+    return [fixtures[i % len(fixtures)] for i in range(batch)]
+
+
+def featurize_rate(batch, seconds=2.0):
+    """Rows/s of the featurizer (kgn_featurize: chains, ladders on three
+    boards, pass-alive area, history and rule features of NNInputs::fillRowV7)
+    on one thread and on the box's CPU share."""
+    from katago_amd import nn
+    pos = nn.Positions(_fixture_positions(batch))
+    out = {}
+    for threads in (1, BOX_CPU_SHARE):
+        nn.featurize(pos, 19, 19, num_threads=threads)
+        rows, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            nn.featurize(pos, 19, 19, num_threads=threads)
+            rows += batch
+        out[f"threads_{threads}"] = round(rows / (time.perf_counter() - t0), 1)
+    out["unit"] = "rows/s"
+    out["what"] = (f"{batch}-row batches of 19x19 positions from seeded random games (tests/golden/featurize_golden.json.gz), "
+                   "NHWC rows identical to KataGo's NNInputs::fillRowV7")
+    return out
+
+
+def featurize_serve_rate(lm, cfg, batch, rounds=30):
+    """Positions in, network outputs out: one thread featurizes the next batch
+    (kgn_featurize on BOX_CPU_SHARE - 1 threads) while another runs the
+    current one through getOutput (pinned staging, H2D, forward, D2H)."""
+    import queue
+    from katago_amd import nn
+    pos = nn.Positions(_fixture_positions(batch))
+    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=cfg.fp16, auto_tune=False)
+    h = nn.ComputeHandle(ctx, max_batch=batch)
+    q = queue.Queue(maxsize=2)
+    h.get_output(*nn.featurize(pos, 19, 19))  # warm up (graph capture)
+
+    def produce():
+        for _ in range(rounds):
+            q.put(nn.featurize(pos, 19, 19, num_threads=max(1, BOX_CPU_SHARE - 1)))
+        q.put(None)
+
+    t = threading.Thread(target=produce)
+    t0 = time.perf_counter()
+    t.start()
+    rows = 0
+    while True:
+        item = q.get()
+        if item is None:
+            break
+        h.get_output(*item)
+        rows += batch
+    t.join()
+    secs = time.perf_counter() - t0
+    h.close()
+    ctx.close()
+    return {"value": round(rows / secs, 1), "unit": "evals/s", "batches": rounds,
+            "path": "positions -> kgn_featurize (host) -> getOutput (pinned staging, H2D, forward, D2H) -> rows, "
+                    "featurizing overlapped with the device"}
+
+
 def serve_rate(lm, cfg, batch, server_threads=2, rounds=40):
     """Evals/s with rows coming from host memory through the batching
     evaluator (NNEvaluator's serve loop): 2*batch native client threads keep
@@ -369,6 +434,9 @@ def main():
         result["latency"] = latency(h, call, lm, cfg)
     if not args.no_serve and batch > 1:
         result["pcie_inclusive"] = serve_rate(lm, cfg, batch)
+        if cfg.arch.num_input == 22 and cfg.arch.num_global == 19:  # the inputs of fillRowV7
+            result["featurize"] = featurize_rate(batch)
+            result["featurize_plus_serve"] = featurize_serve_rate(lm, cfg, batch)
     if not args.no_cpu:
         print("bench: timing CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(path)

@@ -50,6 +50,7 @@ HOST_SOURCES = [
     "host/neuralnet/hipbackend.cpp",
     "host/neuralnet/nneval.cpp",
     "host/neuralnet/capi.cpp",
+    "host/neuralnet/featurize.cpp",
 ]
 ORACLE_SOURCES = [
     os.path.join(ORACLE_DIR, "eigen_oracle.cpp"),

@@ -578,3 +578,86 @@ class DeviceBuffer:
 
     def __del__(self):
         self.free()
+
+
+# ---------------------------------------------------------------------------
+# Position featurizer (include/katago_featurize.h).
+
+class KgnPosition(ctypes.Structure):
+    """kgn_position."""
+    _fields_ = [("x_size", ctypes.c_int32), ("y_size", ctypes.c_int32), ("next_player", ctypes.c_int32),
+                ("colors", ctypes.c_void_p * 3), ("ko_point", ctypes.c_int32 * 3),
+                ("chain_head", ctypes.c_void_p * 3), ("chain_next", ctypes.c_void_p * 3),
+                ("super_ko_banned", ctypes.c_void_p), ("ko_recap_blocked", ctypes.c_void_p),
+                ("second_encore_start_colors", ctypes.c_void_p),
+                ("num_moves", ctypes.c_int32), ("move_point", ctypes.c_int32 * 5), ("move_player", ctypes.c_int32 * 5),
+                ("num_approx_valid_turns_this_phase", ctypes.c_int32), ("encore_phase", ctypes.c_int32),
+                ("ko_rule", ctypes.c_int32), ("scoring_rule", ctypes.c_int32), ("tax_rule", ctypes.c_int32),
+                ("multi_stone_suicide_legal", ctypes.c_int32), ("has_button", ctypes.c_int32),
+                ("self_komi", ctypes.c_float),
+                ("pass_would_end_game", ctypes.c_uint8), ("pass_would_end_phase", ctypes.c_uint8),
+                ("suppress_end_game_from_friendly_pass", ctypes.c_uint8), ("is_game_finished", ctypes.c_uint8),
+                ("is_past_normal_phase_end", ctypes.c_uint8), ("conservative_pass_and_is_root", ctypes.c_uint8),
+                ("enable_passing_hacks", ctypes.c_uint8), ("playout_doubling_advantage", ctypes.c_double),
+                ("max_history", ctypes.c_int32)]
+
+
+_POSITION_SCALARS = ["num_approx_valid_turns_this_phase", "encore_phase", "ko_rule", "scoring_rule", "tax_rule",
+                     "multi_stone_suicide_legal", "has_button", "self_komi", "pass_would_end_game", "pass_would_end_phase",
+                     "suppress_end_game_from_friendly_pass", "is_game_finished", "is_past_normal_phase_end",
+                     "conservative_pass_and_is_root", "enable_passing_hacks", "playout_doubling_advantage", "max_history"]
+
+
+class Positions:
+    """An array of kgn_position built from dicts with the struct's field
+    names (colors, chain_head and chain_next as lists of three per-point
+    lists); keeps the arrays the structs point into alive."""
+
+    def __init__(self, dicts, with_chain_order: bool = True):
+        self.n = len(dicts)
+        self.array = (KgnPosition * max(self.n, 1))()
+        self._keep = []
+        for i, d in enumerate(dicts):
+            p = self.array[i]
+            p.x_size, p.y_size, p.next_player = d["x_size"], d["y_size"], d["next_player"]
+            for k in range(3):
+                p.colors[k] = self._ptr(d["colors"][k], np.int8)
+                p.ko_point[k] = d["ko_point"][k]
+                if with_chain_order and "chain_head" in d:
+                    p.chain_head[k] = self._ptr(d["chain_head"][k], np.int16)
+                    p.chain_next[k] = self._ptr(d["chain_next"][k], np.int16)
+            p.super_ko_banned = self._ptr(d.get("super_ko_banned"), np.uint8)
+            p.ko_recap_blocked = self._ptr(d.get("ko_recap_blocked"), np.uint8)
+            p.second_encore_start_colors = self._ptr(d.get("second_encore_start_colors"), np.int8)
+            p.num_moves = d["num_moves"]
+            for k in range(5):
+                p.move_point[k] = d["move_point"][k]
+                p.move_player[k] = d["move_player"][k]
+            for f in _POSITION_SCALARS:
+                if f in d:
+                    setattr(p, f, d[f])
+
+    def _ptr(self, values, dtype):
+        if values is None:
+            return None
+        a = np.ascontiguousarray(values, dtype=dtype)
+        self._keep.append(a)
+        return a.ctypes.data
+
+
+def featurize(positions: Positions, nn_x: int = 19, nn_y: int = 19, use_nhwc: bool = True, num_threads: int = 0):
+    """kgn_featurize: returns spatial [n, nn_y*nn_x*22] (NHWC or NCHW per
+    row) and global [n, 19] float32 arrays."""
+    lib = host_library()
+    lib.kgn_featurize.restype = ctypes.c_int32
+    lib.kgn_featurize.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_char_p, ctypes.c_int32]
+    n = positions.n
+    spatial = np.zeros((n, nn_y * nn_x * 22), np.float32)
+    glob = np.zeros((n, 19), np.float32)
+    err = _errbuf()
+    rc = lib.kgn_featurize(ctypes.addressof(positions.array), n, nn_x, nn_y, int(use_nhwc), spatial.ctypes.data,
+                           glob.ctypes.data, num_threads, err, len(err))
+    if rc != 0:
+        _raise(err)
+    return spatial, glob

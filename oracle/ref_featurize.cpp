@@ -12,6 +12,12 @@
 //   <ySize lines of the board as Board::parseBoard reads it>
 // and, for random positions reached by play:
 //   game <name> <seed> <xSize> <ySize> <nnXLen> <nnYLen> <numMoves> <inputsVersion> <rules>
+// and, to check this repository's featurizer (include/katago_featurize.h,
+// linked in through katago_amd/host/neuralnet/featurizeadapter.cpp) against
+// KataGo's own fillRowV7 on every position of a random game:
+//   compare <name> <seed> <xSize> <ySize> <nnXLen> <nnYLen> <numMoves> <rules> <fixtureEvery>
+// which prints a summary line and, every fixtureEvery positions, the
+// position with KataGo's rows as a fixture line.
 // Output on stdout: one JSON object per position and line.
 #include <cstdio>
 #include <iostream>
@@ -25,6 +31,7 @@
 #include "../game/boardhistory.h"
 #include "../game/rules.h"
 #include "../neuralnet/nninputs.h"
+#include "featurizeadapter.h"
 
 using std::string;
 using std::vector;
@@ -103,6 +110,115 @@ void emit(const string& name, const Board& board, const BoardHistory& hist, Play
   std::cout << out.str() << std::endl;
 }
 
+void bits(std::ostream& out, const vector<float>& v) {
+  // 0/1 values as a hex string, four values per digit, first value in the
+  // high bit.
+  static const char* hex = "0123456789abcdef";
+  out << "\"";
+  for(size_t i = 0; i < v.size(); i += 4) {
+    int d = 0;
+    for(int k = 0; k < 4; k++) d = d * 2 + (i + k < v.size() && v[i + k] != 0.0f ? 1 : 0);
+    out << hex[d];
+  }
+  out << "\"";
+}
+
+template<typename T>
+void ints(std::ostream& out, const T* v, int n) {
+  out << "[";
+  for(int i = 0; i < n; i++) out << (i ? "," : "") << (int)v[i];
+  out << "]";
+}
+
+void fixture(const string& name, const kgn_position& pos, int nnX, int nnY, const vector<float>& spatial,
+             const vector<float>& global) {
+  std::ostringstream out;
+  const int area = pos.x_size * pos.y_size;
+  out << "{\"fixture\":\"" << name << "\",\"nnx\":" << nnX << ",\"nny\":" << nnY << ",\"x_size\":" << pos.x_size
+      << ",\"y_size\":" << pos.y_size << ",\"next_player\":" << pos.next_player << ",\"colors\":[";
+  for(int k = 0; k < 3; k++) {
+    out << (k ? "," : "");
+    ints(out, pos.colors[k], area);
+  }
+  out << "],\"chain_head\":[";
+  for(int k = 0; k < 3; k++) {
+    out << (k ? "," : "");
+    ints(out, pos.chain_head[k], area);
+  }
+  out << "],\"chain_next\":[";
+  for(int k = 0; k < 3; k++) {
+    out << (k ? "," : "");
+    ints(out, pos.chain_next[k], area);
+  }
+  out << "],\"ko_point\":";
+  ints(out, pos.ko_point, 3);
+  out << ",\"super_ko_banned\":";
+  ints(out, pos.super_ko_banned, area);
+  out << ",\"ko_recap_blocked\":";
+  ints(out, pos.ko_recap_blocked, area);
+  out << ",\"second_encore_start_colors\":";
+  ints(out, pos.second_encore_start_colors, area);
+  out << ",\"num_moves\":" << pos.num_moves << ",\"move_point\":";
+  ints(out, pos.move_point, 5);
+  out << ",\"move_player\":";
+  ints(out, pos.move_player, 5);
+  char komi[32];
+  snprintf(komi, sizeof(komi), "%.9g", pos.self_komi);
+  out << ",\"num_approx_valid_turns_this_phase\":" << pos.num_approx_valid_turns_this_phase
+      << ",\"encore_phase\":" << pos.encore_phase << ",\"ko_rule\":" << pos.ko_rule << ",\"scoring_rule\":" << pos.scoring_rule
+      << ",\"tax_rule\":" << pos.tax_rule << ",\"multi_stone_suicide_legal\":" << pos.multi_stone_suicide_legal
+      << ",\"has_button\":" << pos.has_button << ",\"self_komi\":" << komi
+      << ",\"pass_would_end_game\":" << (int)pos.pass_would_end_game << ",\"pass_would_end_phase\":" << (int)pos.pass_would_end_phase
+      << ",\"suppress_end_game_from_friendly_pass\":" << (int)pos.suppress_end_game_from_friendly_pass
+      << ",\"is_game_finished\":" << (int)pos.is_game_finished << ",\"is_past_normal_phase_end\":" << (int)pos.is_past_normal_phase_end
+      << ",\"max_history\":" << pos.max_history << ",\"conservative_pass_and_is_root\":" << (int)pos.conservative_pass_and_is_root
+      << ",\"enable_passing_hacks\":" << (int)pos.enable_passing_hacks
+      << ",\"playout_doubling_advantage\":" << pos.playout_doubling_advantage << ",\"spatial_nhwc_bits\":";
+  bits(out, spatial);
+  out << ",\"global\":";
+  floats(out, global);
+  out << "}";
+  std::cout << out.str() << std::endl;
+}
+
+// KataGo's fillRowV7 and this repository's featurizer on one position:
+// the number of differing spatial and global values.
+int compareOne(const string& name, const Board& board, const BoardHistory& hist, Player pla, int nnX, int nnY, bool emitFixture,
+               string& firstDiff, int variant) {
+  // Search-time parameters varied across positions (nninputs.h:52-63).
+  MiscNNInputParams params;
+  if(variant % 5 == 0) params.playoutDoublingAdvantage = (variant % 3 - 1) * 0.75;
+  if(variant % 7 == 0) params.conservativePassAndIsRoot = true;
+  if(variant % 11 == 0) params.enablePassingHacks = true;
+  if(variant % 13 == 0) params.maxHistory = variant % 4;
+  if(variant % 4 == 0) params.drawEquivalentWinsForWhite = 0.3;
+  const int C = NNInputs::NUM_FEATURES_SPATIAL_V7, G = NNInputs::NUM_FEATURES_GLOBAL_V7;
+  vector<float> refS((size_t)C * nnX * nnY), refG(G), mineS(refS.size()), mineG(G);
+  NNInputs::fillRowV7(board, hist, pla, params, nnX, nnY, true, refS.data(), refG.data());
+  kgn_position pos;
+  HipBackend::PositionStorage storage;
+  HipBackend::positionFromHistory(board, hist, pla, params, pos, storage);
+  char err[512];
+  if(kgn_featurize(&pos, 1, nnX, nnY, 1, mineS.data(), mineG.data(), 1, err, sizeof(err)) != 0)
+    throw StringError(string("kgn_featurize failed: ") + err);
+  int diffs = 0;
+  for(size_t i = 0; i < refS.size(); i++)
+    if(refS[i] != mineS[i]) {
+      if(diffs++ == 0 && firstDiff.empty()) {
+        const int c = (int)(i % C), p = (int)(i / C);
+        firstDiff = name + ": spatial feature " + std::to_string(c) + " at (" + std::to_string(p % nnX) + "," +
+                    std::to_string(p / nnX) + ") reference " + std::to_string(refS[i]) + " mine " + std::to_string(mineS[i]);
+      }
+    }
+  for(int i = 0; i < G; i++)
+    if(refG[i] != mineG[i]) {
+      if(diffs++ == 0 && firstDiff.empty())
+        firstDiff = name + ": global " + std::to_string(i) + " reference " + std::to_string(refG[i]) + " mine " + std::to_string(mineG[i]);
+    }
+  if(emitFixture) fixture(name, pos, nnX, nnY, refS, refG);
+  return diffs;
+}
+
 }  // namespace
 
 int main() {
@@ -145,6 +261,42 @@ int main() {
         pla = getOpp(pla);
       }
       emit(name, board, hist, pla, nnX, nnY, version);
+    }
+    else if(word == "compare") {
+      string name, rulesS;
+      uint64_t seed;
+      int xs, ys, nnX, nnY, moves, every;
+      std::cin >> name >> seed >> xs >> ys >> nnX >> nnY >> moves >> rulesS >> every;
+      Board board(xs, ys);
+      Player pla = P_BLACK;
+      BoardHistory hist(board, pla, rulesNamed(rulesS), 0);
+      Rand rand(seed);
+      int positions = 0, mismatched = 0;
+      string firstDiff;
+      for(int m = 0; m <= moves; m++) {
+        const string posName = name + "-" + std::to_string(m);
+        const int d = compareOne(posName, board, hist, pla, nnX, nnY, every > 0 && m % every == 0, firstDiff, (int)(seed + m));
+        positions++;
+        mismatched += d > 0;
+        if(m == moves || hist.isGameFinished) break;
+        vector<Loc> cands;
+        for(int y = 0; y < ys; y++)
+          for(int x = 0; x < xs; x++) {
+            Loc loc = Location::getLoc(x, y, xs);
+            if(hist.isLegal(board, loc, pla)) cands.push_back(loc);
+          }
+        // Mostly random legal moves, passes now and then, and two passes in a
+        // row at half, seven tenths and nine tenths of the game (which end the
+        // game under area rules and start the encore phases under territory
+        // rules).
+        const bool forcedPass = m == moves / 2 || m == moves / 2 + 1 || m == moves * 7 / 10 || m == moves * 7 / 10 + 1 ||
+                                m == moves * 9 / 10 || m == moves * 9 / 10 + 1;
+        Loc loc = forcedPass || cands.empty() || rand.nextUInt(30) == 0 ? Board::PASS_LOC : cands[rand.nextUInt((uint32_t)cands.size())];
+        hist.makeBoardMoveAssumeLegal(board, loc, pla, nullptr);
+        pla = getOpp(pla);
+      }
+      std::cout << "{\"summary\":\"" << name << "\",\"positions\":" << positions << ",\"mismatched\":" << mismatched
+                << ",\"first_diff\":\"" << firstDiff << "\"}" << std::endl;
     }
     else {
       std::cerr << "unknown record " << word << std::endl;
