@@ -160,7 +160,7 @@ def cpu_baseline(path, seconds_target=15.0):
                       f"({affinity} of the host's {host_cores}) capped at the box's CPU share of {BOX_CPU_SHARE} per GPU"}
 
 
-def latency(h, call, lm, cfg, steps=200):
+def latency(h, call, lm, cfg, batch=1, steps=200):
     """Batch-1 latency: each forward timed alone on the host clock (launch to
     synchronize), inputs resident in HBM; and the same through the host-memory
     entry point (featurized row in pageable host memory -> pinned staging ->
@@ -174,22 +174,45 @@ def latency(h, call, lm, cfg, steps=200):
         call()
         h.synchronize()
         lat.append(time.perf_counter() - t0)
-    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=cfg.fp16, auto_tune=False)
-    ch = nn.ComputeHandle(ctx, max_batch=1)
-    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, 1, board_sizes=cfg.board_sizes)
-    for _ in range(5):
-        ch.get_output(sp, gl)
-    host = []
-    for _ in range(steps):
-        t0 = time.perf_counter()
-        ch.get_output(sp, gl)
-        host.append(time.perf_counter() - t0)
-    ch.close()
-    ctx.close()
     q = lambda a, p: round(1000.0 * float(np.percentile(a, p)), 4)
-    return {"hbm_resident_ms": {"p50": q(lat, 50), "p90": q(lat, 90), "min": q(lat, 0)},
-            "pcie_inclusive_ms": {"p50": q(host, 50), "p90": q(host, 90), "min": q(host, 0)},
-            "forwards": steps, "what": "one board per forward, host wall clock from launch to synchronize"}
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, 1, board_sizes=cfg.board_sizes)
+
+    def host_path(low_latency):
+        ctx = nn.ComputeContext(lm, 19, 19, use_fp16=cfg.fp16, auto_tune=False, low_latency=low_latency)
+        ch = nn.ComputeHandle(ctx, max_batch=1)
+        for _ in range(5):
+            ch.get_output(sp, gl)
+        host = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            ch.get_output(sp, gl)
+            host.append(time.perf_counter() - t0)
+        ch.close()
+        ctx.close()
+        return {"p50": q(host, 50), "p90": q(host, 90), "min": q(host, 0)}
+
+    out = {"hbm_resident_ms": {"p50": q(lat, 50), "p90": q(lat, 90), "min": q(lat, 0)},
+           "pcie_inclusive_ms": host_path(False)}
+    if cfg.fp16 and batch <= 16:
+        # The same with hipLowLatency (split-K 3x3 convs): device-resident
+        # inputs on a one-row device handle, and the host-memory path.
+        h.set_low_latency(True)
+        for _ in range(5):
+            call()
+        h.synchronize()
+        fast = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            call()
+            h.synchronize()
+            fast.append(time.perf_counter() - t0)
+        h.set_low_latency(False)
+        out["low_latency"] = {"hbm_resident_ms": {"p50": q(fast, 50), "p90": q(fast, 90), "min": q(fast, 0)},
+                              "pcie_inclusive_ms": host_path(True),
+                              "what": "hipLowLatency: split-K 3x3 convolutions (up to 8 workgroups per board and 64 "
+                                      "output channels, fp32 partial sums added in a fixed order)"}
+    out.update({"forwards": steps, "what": "one board per forward, host wall clock from launch to synchronize"})
+    return out
 
 
 def _fixture_positions(batch):
@@ -290,6 +313,7 @@ def main():
     ap.add_argument("--no-autotune", action="store_true", help="keep the built-in kernel choices")
     ap.add_argument("--batch", type=int, default=0, help="boards per forward instead of the config's (not the headline line)")
     ap.add_argument("--latency", action="store_true", help="also time single forwards (always on at --batch 1)")
+    ap.add_argument("--no-latency", action="store_true", help="skip the single-forward timing even at --batch 1")
     ap.add_argument("--no-serve", action="store_true",
                     help="skip the PCIe-inclusive measurement through the batching evaluator")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -430,8 +454,8 @@ def main():
         result["roofline"]["vendor_gemm_sustained"] = vendor
         if vendor["tflops"]:
             result["roofline"]["frac_of_vendor_gemm"] = round(achieved / vendor["tflops"], 4)
-    if batch == 1 or args.latency:
-        result["latency"] = latency(h, call, lm, cfg)
+    if (batch == 1 or args.latency) and not args.no_latency:
+        result["latency"] = latency(h, call, lm, cfg, batch)
     if not args.no_serve and batch > 1:
         result["pcie_inclusive"] = serve_rate(lm, cfg, batch)
         if cfg.arch.num_input == 22 and cfg.arch.num_global == 19:  # the inputs of fillRowV7

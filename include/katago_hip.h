@@ -250,6 +250,20 @@ int kgh_handle_autotune(kgh_handle* handle, int32_t reps, char* report, int32_t 
 int kgh_handle_set_tuning(kgh_handle* handle, const char* table);
 int kgh_handle_get_tuning(kgh_handle* handle, char* buf, int32_t buflen);
 
+/* Low-latency mode for small batches (config key hipLowLatency of the
+ * NeuralNet backend; no counterpart in nninterface.h): every fp16 3x3 conv on
+ * 19x19 boards that the one-board kernel takes runs split-K, its 32-channel
+ * chunks spread over up to eight workgroups per (board, 64 output channels)
+ * whose fp32 partial sums a second kernel adds in a fixed order before the
+ * epilogue. At one board a forward uses ~18 workgroups per conv instead of 3.
+ * Results are deterministic and independent of the batch size within the
+ * mode, but not bitwise equal to the default kernels (other summation order;
+ * both stay within the fp16 tolerances of the oracle). Only for handles of
+ * max_batch <= KGH_LOW_LATENCY_MAX_BATCH; enabling allocates the partial-sum
+ * buffer (8 * max_batch * nn_x * nn_y * widest channel count floats). */
+#define KGH_LOW_LATENCY_MAX_BATCH 16
+int kgh_handle_set_low_latency(kgh_handle* handle, int32_t enabled);
+
 /* Per-launch timing of the convolution kernels, measured with HIP events on
  * the handle's stream. kgh_handle_set_profiling(h, 1) clears the records and
  * starts recording every conv launch of the following forwards;

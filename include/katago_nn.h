@@ -49,6 +49,13 @@ void kgn_free_context(void* context);
 void* kgn_create_context_ex(void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t use_fp16, const char* home_data_dir,
                             int32_t auto_tune, const char* tuner_file, char* err, int32_t errlen);
 
+/* createComputeContext with a ConfigParser holding the given "key = value"
+ * lines ('#' starts a comment), as they would appear in a KataGo config file:
+ * hipAutoTune, hipTunerFile, hipLowLatency (split-K 3x3 convolutions for
+ * handles of nnMaxBatchSize <= 16, see kgh_handle_set_low_latency). */
+void* kgn_create_context_cfg(void* loaded_model, int32_t nn_x, int32_t nn_y, int32_t use_fp16, const char* home_data_dir,
+                             const char* config, char* err, int32_t errlen);
+
 /* The handle's tuning table (text, as saved) into buf; returns where it came
  * from: 0 built-in choices, 1 a tuning file, 2 tuned at handle creation;
  * -1 on error (message in buf). */

@@ -541,6 +541,11 @@ struct kgh_handle {
   bool graphsEnabled = true;
   std::vector<GraphEntry> graphs;
 
+  // Low-latency mode (kgh_handle_set_low_latency): the 3x3 convs the split-K
+  // path takes run with their fp32 partial sums in splitWork.
+  bool lowLatency = false;
+  float* splitWork = nullptr;
+
   // Autotuned kernel variant per conv shape, keyed by (ky, kx, cinPad, cout,
   // M, gated epilogue, residual, masked residual); every conv launch of a
   // forward looks its shape up here (kgh_handle_autotune, kgh_handle_set_tuning).
@@ -631,6 +636,14 @@ struct Runner {
   }
 
   void conv(const ConvW& c, const T* x, int ldx, const ConvEpilogue<T>& e) {
+    if constexpr(std::is_same<T, half_t>::value) {
+      if(h != nullptr && h->lowLatency && kgh::convSplitKApplies(ldx, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, g, e)) {
+        ProfRec* rec = profStart(c);
+        kgh::launchConvSplitK((const half_t*)x, ldx, c.cinPad, c.cout, (const half_t*)c.wPrep, g, e, h->splitWork, s);
+        if(rec != nullptr) KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
+        return;
+      }
+    }
     int variant = CONV_AUTO;
     if(h != nullptr) {
       const kgh_handle::TuneKey key = {c.ky, c.kx, c.cinPad, c.cout, M, e.glu, e.residual != nullptr ? 1 : 0, e.maskResidualAdd};
@@ -661,21 +674,25 @@ struct Runner {
         return;
       }
     }
-    ProfRec* rec = nullptr;
-    if(h != nullptr && h->profiling) {
-      if(h->profUsed == h->prof.size()) {
-        ProfRec r;
-        KGH_HIP_CHECK(hipEventCreate(&r.start));
-        KGH_HIP_CHECK(hipEventCreate(&r.stop));
-        h->prof.push_back(r);
-      }
-      rec = &h->prof[h->profUsed++];
-      rec->kind = (c.ky == 3 && c.kx == 3) ? 0 : (c.ky == 1 && c.kx == 1) ? 1 : 2;
-      rec->flops = 2.0 * M * (double)c.cin * c.cout * c.ky * c.kx;
-      KGH_HIP_CHECK(hipEventRecord(rec->start, s));
-    }
+    ProfRec* rec = profStart(c);
     kgh::launchConv<T>(x, ldx, c.cin, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, c.wDirect, g, e, s, nullptr, variant);
     if(rec != nullptr) KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
+  }
+
+  // Starts the profiling record of a conv launch (null when not profiling).
+  ProfRec* profStart(const ConvW& c) {
+    if(h == nullptr || !h->profiling) return nullptr;
+    if(h->profUsed == h->prof.size()) {
+      ProfRec r;
+      KGH_HIP_CHECK(hipEventCreate(&r.start));
+      KGH_HIP_CHECK(hipEventCreate(&r.stop));
+      h->prof.push_back(r);
+    }
+    ProfRec* rec = &h->prof[h->profUsed++];
+    rec->kind = (c.ky == 3 && c.kx == 3) ? 0 : (c.ky == 1 && c.kx == 1) ? 1 : 2;
+    rec->flops = 2.0 * M * (double)c.cin * c.cout * c.ky * c.kx;
+    KGH_HIP_CHECK(hipEventRecord(rec->start, s));
+    return rec;
   }
 
   void bnAct(const T* x, int ldx, T* y, int ldy, const BNAct& bn, const float* ncBias, int ldNC) {
@@ -1925,6 +1942,24 @@ int kgh_handle_set_tuning(kgh_handle* handle, const char* table) {
     }
     handle->tuned = t;
     handle->tuneShapes = shapes;
+    dropGraphs(handle);
+  });
+}
+
+int kgh_handle_set_low_latency(kgh_handle* handle, int32_t enabled) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(enabled && handle->maxBatch > KGH_LOW_LATENCY_MAX_BATCH)
+      invalid("low-latency mode takes handles of max_batch <= " + std::to_string(KGH_LOW_LATENCY_MAX_BATCH));
+    if(enabled && handle->splitWork == nullptr) {
+      // Up to eight splits of the widest activation of the net.
+      const Net& net = handle->model->net;
+      int maxC = std::max(net.tmpC, 1);
+      for(int c : net.depthC) maxC = std::max(maxC, c);
+      KGH_HIP_CHECK(hipSetDevice(handle->model->device));
+      handle->splitWork = handle->arena.allocN<float>((size_t)8 * handle->maxBatch * handle->H * handle->W * maxC);
+    }
+    handle->lowLatency = enabled != 0;
     dropGraphs(handle);
   });
 }

@@ -194,6 +194,18 @@ bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int 
 template<typename T>
 bool convMfmaSupported(int cinPad, int cout);
 
+// Split-K form of the one-board 3x3 kernel for small batches (the handle's
+// low-latency mode): the conv's 32-channel chunks are spread over up to eight
+// workgroups per (board, 64-column tile), whose fp32 partial sums
+// (convSplitKWorkFloats floats of work) are added in a fixed order by a second
+// kernel that applies the epilogue. Deterministic, but not bitwise equal to
+// the other kernels (different summation order).
+bool convSplitKApplies(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, BoardGeom g,
+                       const ConvEpilogue<half_t>& epi);
+size_t convSplitKWorkFloats(int cinPad, int cout, BoardGeom g);
+void launchConvSplitK(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                      const ConvEpilogue<half_t>& epi, float* work, hipStream_t stream);
+
 // Converts fp32 weights (oc, ic, y, x) to the kernel layout [tap][oc][cinPad]
 // of type T on device (zero-padded channels).
 template<typename T>

@@ -77,7 +77,7 @@ __device__ __forceinline__ void rowColTile(int colTiles, int& rowTile, int& colT
 // kind, so the per-element activation is selected at compile time instead of
 // branching on every element.
 template<typename F>
-__device__ __forceinline__ void withActKind(int act, bool used, F&& f) {
+__host__ __device__ __forceinline__ void withActKind(int act, bool used, F&& f) {
   switch(used ? act : KGH_ACT_IDENTITY) {
     case KGH_ACT_RELU: f(std::integral_constant<int, KGH_ACT_RELU>()); break;
     case KGH_ACT_MISH: f(std::integral_constant<int, KGH_ACT_MISH>()); break;
@@ -925,10 +925,15 @@ __device__ __attribute__((aligned(256))) half_t kZeroChannels[BW_MAX_CIN + 64];
 // Tap at which window load i (0..8) of a window wave is issued (taps 0..5).
 __host__ __device__ constexpr int winLoadTap(int i) { return i * 6 / BW_WIN_PER; }
 
-template<int BN, int NB>
+// SPLIT: split-K for small batches. Workgroup (board, column tile, split s)
+// runs only the 32-channel chunks of split s (gridDim.y splits) and stores
+// its fp32 accumulators to work[s][m][cout] (board rows only); the residual
+// and the epilogue are left to splitKEpilogueKernel, which sums the splits in
+// order.
+template<int BN, int NB, bool SPLIT = false>
 __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
                                                                       int cout, const half_t* __restrict__ w, int batch,
-                                                                      ConvEpilogue<half_t> epi) {
+                                                                      ConvEpilogue<half_t> epi, float* __restrict__ work = nullptr) {
   // NB weight buffers, loaded LA = NB - 3 steps ahead: the DMA for step
   // s + LA goes to buffer (s - 3) mod NB, free once step s - 1's barrier is
   // passed. Nine buffers (six steps ahead) for 64-column tiles, whose small
@@ -986,7 +991,12 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   const int laneRow = lane & 31;
   const int kq = lane >> 5;
   const int cChunks = cinPad / 32;
-  const int steps = 9 * cChunks;
+  // This workgroup's chunks [cBegin, cEnd): all of them, or split
+  // blockIdx.y's share (the host makes every split non-empty).
+  const int perSplit = SPLIT ? (cChunks + (int)gridDim.y - 1) / (int)gridDim.y : cChunks;
+  const int cBegin = SPLIT ? (int)blockIdx.y * perSplit : 0;
+  const int cEnd = SPLIT ? min(cChunks, cBegin + perSplit) : cChunks;
+  const int steps = 9 * cEnd;
   const int tapStride = cout * cinPad;
 
   // Window load i of this wave fills LDS bytes [1024 j, 1024 j + 1024),
@@ -1050,7 +1060,7 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   // prologue DMA first, with the stage in win1, measured 2.4 us slower on
   // C2's residual convs.)
   floatx16 acc[RB][CB];
-  if(epi.residual != nullptr) {
+  if(!SPLIT && epi.residual != nullptr) {
     residualToAcc<half_t, RB, CB, 1>(acc, epi.residual, epi.ldRes, m0 + wm * BW_WTM, n0 + wn * WTN, mEnd, stage);
     __syncthreads();
   }
@@ -1062,14 +1072,14 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
 #pragma unroll
         for(int r = 0; r < 16; r++) acc[rb][cb][r] = 0.0f;
   }
-  // Prologue: weights of steps 0..2 and the window of chunk 0.
+  // Prologue: weights of the first LA steps and the window of the first chunk.
   if(loadsWeights) {
 #pragma unroll
-    for(int i = 0; i < LA; i++) loadWeights(wtBuf(i), i);
+    for(int i = 0; i < LA; i++) loadWeights(wtBuf(i), 9 * cBegin + i);
   }
   if(loadsWindow) {
 #pragma unroll
-    for(int i = 0; i < BW_WIN_PER; i++) loadWindow(win0, 0, i);
+    for(int i = 0; i < BW_WIN_PER; i++) loadWindow(win0, cBegin, i);
   }
   waitVmcnt<0>();
   barrierNoFence();
@@ -1105,7 +1115,7 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
     unsigned char* nxt = WP ? win0 : win1;
     // The last chunk re-loads itself into the idle window (never read), so
     // every step issues the same loads.
-    const int cNext = c + 1 < cChunks ? c + 1 : c;
+    const int cNext = c + 1 < cEnd ? c + 1 : c;
 #pragma unroll
     for(int t = 0; t < 9; t++) {
       const unsigned char* wCur = wtBuf(P + t);
@@ -1149,14 +1159,86 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
       }
     }
   };
-  for(int c = 0; c < cChunks; c += 2) {
+  // Buffer phase and window parity follow the chunk's position in this
+  // workgroup's range, so a split may start at any chunk.
+  for(int c = cBegin; c < cEnd; c += 2) {
     chunk(std::integral_constant<int, 0>(), std::integral_constant<int, 0>(), c);
-    if(c + 1 < cChunks) chunk(std::integral_constant<int, 9 % NB>(), std::integral_constant<int, 1>(), c + 1);
+    if(c + 1 < cEnd) chunk(std::integral_constant<int, 9 % NB>(), std::integral_constant<int, 1>(), c + 1);
   }
   waitVmcnt<0>();
   __syncthreads();
 
-  storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage, m0 + wm * BW_WTM, n0 + wn * WTN, mEnd, BW_HW, epi);
+  if constexpr(SPLIT) {
+    // Partial sums in the matrix-core C layout: per register, 32 lanes store
+    // 32 consecutive columns of one row.
+    const size_t M = (size_t)batch * BW_HW;
+    float* dst = work + (size_t)blockIdx.y * M * cout;
+#pragma unroll
+    for(int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for(int r = 0; r < 16; r++) {
+        const int i = wm * BW_WTM + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if(i < BW_HW) {
+#pragma unroll
+          for(int cb = 0; cb < CB; cb++) dst[(size_t)(m0 + i) * cout + n0 + wn * WTN + cb * 32 + laneRow] = acc[rb][cb][r];
+        }
+      }
+  }
+  else {
+    storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage, m0 + wm * BW_WTM, n0 + wn * WTN, mEnd, BW_HW, epi);
+  }
+}
+
+// Sums split-K partials work[s][m][c] over s = 0, 1, ... in order, then
+// applies the epilogue contract to the sum; eight channels per thread.
+template<int ACT>
+__global__ __launch_bounds__(256) void splitKEpilogueKernel(const float* __restrict__ work, int splits, int M, int HW, int cout,
+                                                            ConvEpilogue<half_t> epi) {
+  const int groups = cout / 8;
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if(idx >= (long)M * groups) return;
+  const int m = (int)(idx / groups);
+  const int c0 = (int)(idx - (long)m * groups) * 8;
+  float v[8];
+#pragma unroll
+  for(int k = 0; k < 8; k++) v[k] = 0.0f;
+  for(int s = 0; s < splits; s++) {
+    const float4* p = (const float4*)(work + ((size_t)s * M + m) * cout + c0);
+    const float4 a = p[0], b = p[1];
+    v[0] += a.x;
+    v[1] += a.y;
+    v[2] += a.z;
+    v[3] += a.w;
+    v[4] += b.x;
+    v[5] += b.y;
+    v[6] += b.z;
+    v[7] += b.w;
+  }
+  if(epi.ncBias != nullptr) {
+    const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
+#pragma unroll
+    for(int k = 0; k < 8; k++) v[k] += nb[k];
+  }
+  const float msk = epi.mask[m];
+  if(epi.residual != nullptr) {
+    const uint4 raw = *(const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0);
+    const half_t* rv = (const half_t*)&raw;
+#pragma unroll
+    for(int k = 0; k < 8; k++) v[k] = epi.maskResidualAdd ? (float)rv[k] + v[k] * msk : (float)rv[k] + v[k];
+  }
+  if(c0 < epi.rawEnd) {
+    half_t o[8];
+#pragma unroll
+    for(int k = 0; k < 8; k++) o[k] = (half_t)v[k];
+    *(uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0) = *(const uint4*)o;
+  }
+  if(epi.outAct != nullptr && c0 >= epi.actBegin) {
+    const int ca = c0 - epi.actBegin;
+    half_t o[8];
+#pragma unroll
+    for(int k = 0; k < 8; k++) o[k] = (half_t)(kgh_activate_fast(v[k] * epi.actScale[ca + k] + epi.actBias[ca + k], ACT) * msk);
+    *(uint4*)(epi.outAct + (size_t)m * epi.ldAct + ca) = *(const uint4*)o;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1432,6 +1514,16 @@ bool boardWindowFits(int cinStride, int cinPad, int cout, int bn, BoardGeom g, c
          !epi.maskResidualAdd && !epi.glu && cout % bn == 0 && M * cinStride < (1L << 31) && 9L * cout * cinPad < (1L << 31);
 }
 
+// Split-K at small batches: 64-column tiles, one workgroup per (board,
+// column tile, split); a split takes one or more whole 32-channel chunks.
+constexpr int SPLITK_BN = 64;
+constexpr int SPLITK_MAX_SPLITS = 8;
+int splitKCount(int cinPad) {
+  const int chunks = cinPad / 32;
+  const int perSplit = (chunks + SPLITK_MAX_SPLITS - 1) / SPLITK_MAX_SPLITS;
+  return (chunks + perSplit - 1) / perSplit;
+}
+
 // Shape conditions of the window kernel apart from batch size.
 bool tapWindowFits(int cinStride, int cinPad, int cout, int bn, BoardGeom g, const ConvEpilogue<half_t>& epi) {
   const long M = (long)g.batch * g.H * g.W;
@@ -1690,6 +1782,33 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
   long blocks = (total + threads - 1) / threads;
   hipLaunchKernelGGL(convDirectKernel<T>, dim3((unsigned)blocks), dim3(threads), 0, stream, x, cinStride, cin, cout, ky, kx,
                      wDirect, g, epi);
+  KGH_CHECK_LAUNCH();
+}
+
+bool convSplitKApplies(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, BoardGeom g,
+                       const ConvEpilogue<half_t>& epi) {
+  return ky == 3 && kx == 3 && cinPad >= 64 && mfmaPathOk<half_t>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
+         boardWindowFits(cinStride, cinPad, cout, SPLITK_BN, g, epi) && cout % 8 == 0;
+}
+
+size_t convSplitKWorkFloats(int cinPad, int cout, BoardGeom g) {
+  return (size_t)splitKCount(cinPad) * g.batch * g.H * g.W * cout;
+}
+
+void launchConvSplitK(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                      const ConvEpilogue<half_t>& epi, float* work, hipStream_t stream) {
+  if(!convSplitKApplies(cinStride, cinPad, cout, 3, 3, w, g, epi)) throw KghError(5, "conv: split-K does not apply to this shape");
+  const int splits = splitKCount(cinPad);
+  hipLaunchKernelGGL((convBoardWindowKernel<SPLITK_BN, 9, true>), dim3(g.batch * (cout / SPLITK_BN), splits), dim3(BW_THREADS), 0,
+                     stream, x, cinStride, cinPad, cout, w, g.batch, epi, work);
+  KGH_CHECK_LAUNCH();
+  const int M = g.batch * g.H * g.W;
+  const long threads = (long)M * (cout / 8);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  withActKind(epi.actKind, epi.outAct != nullptr, [&](auto actTag) {
+    hipLaunchKernelGGL((splitKEpilogueKernel<decltype(actTag)::value>), grid, dim3(256), 0, stream, work, splits, M, g.H * g.W, cout,
+                       epi);
+  });
   KGH_CHECK_LAUNCH();
 }
 

@@ -1,4 +1,5 @@
 // C shim over NeuralNet::* (include/katago_nn.h) for non-C++ callers.
+#include <sstream>
 #include <chrono>
 #include <cstring>
 #include <memory>
@@ -94,6 +95,38 @@ void* kgn_create_context_ex(void* m, int32_t nn_x, int32_t nn_y, int32_t use_fp1
     ConfigParser cfg;
     if(auto_tune >= 0) cfg.overrideKey("hipAutoTune", auto_tune ? "true" : "false");
     if(tuner_file != nullptr && tuner_file[0] != 0) cfg.overrideKey("hipTunerFile", tuner_file);
+    enabled_t mode = use_fp16 == 0 ? enabled_t::False : use_fp16 == 1 ? enabled_t::True : enabled_t::Auto;
+    return NeuralNet::createComputeContext({0}, nullptr, nn_x, nn_y, home_data_dir != nullptr ? home_data_dir : "", mode,
+                                           (const LoadedModel*)m, cfg);
+  }
+  catch(const std::exception& e) {
+    setErr(err, errlen, e.what());
+    return nullptr;
+  }
+}
+
+void* kgn_create_context_cfg(void* m, int32_t nn_x, int32_t nn_y, int32_t use_fp16, const char* home_data_dir, const char* config,
+                             char* err, int32_t errlen) {
+  try {
+    ConfigParser cfg;
+    // "key = value" lines, '#' comments, as in a KataGo config file.
+    std::istringstream in(config != nullptr ? config : "");
+    std::string line;
+    while(std::getline(in, line)) {
+      const size_t hash = line.find('#');
+      if(hash != std::string::npos) line.erase(hash);
+      const size_t eq = line.find('=');
+      auto trim = [](std::string s) {
+        const size_t b = s.find_first_not_of(" \t\r");
+        const size_t e = s.find_last_not_of(" \t\r");
+        return b == std::string::npos ? std::string() : s.substr(b, e - b + 1);
+      };
+      if(eq == std::string::npos) {
+        if(!trim(line).empty()) throw StringError("config line without '=': " + line);
+        continue;
+      }
+      cfg.overrideKey(trim(line.substr(0, eq)), trim(line.substr(eq + 1)));
+    }
     enabled_t mode = use_fp16 == 0 ? enabled_t::False : use_fp16 == 1 ? enabled_t::True : enabled_t::Auto;
     return NeuralNet::createComputeContext({0}, nullptr, nn_x, nn_y, home_data_dir != nullptr ? home_data_dir : "", mode,
                                            (const LoadedModel*)m, cfg);

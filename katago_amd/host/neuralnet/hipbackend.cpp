@@ -309,6 +309,9 @@ struct ComputeContext {
   // Autotuning (config keys hipAutoTune, hipTunerFile; the OpenCL backend's
   // openCLTunerFile is the model): tables live in <home data dir>/hiptuning.
   bool autoTune = true;
+  // hipLowLatency: handles of at most KGH_LOW_LATENCY_MAX_BATCH rows run the
+  // split-K 3x3 convs (kgh_handle_set_low_latency), for batch-1 searches.
+  bool lowLatency = false;
   std::string tunerFile;  // explicit tuning file, else a per-(gpu, board, batch, dtype, architecture) name
   std::string tunerDir;
   uint64_t archHash = 0;  // of the flattened layer table (shapes, not weights)
@@ -467,6 +470,7 @@ ComputeContext* NeuralNet::createComputeContext(const vector<int>& gpuIdxs, Logg
   ComputeContext* c = new ComputeContext(nnXLen, nnYLen, useFP16Mode);
   if(cfg.contains("hipAutoTune")) c->autoTune = cfg.getBool("hipAutoTune");
   if(cfg.contains("hipTunerFile")) c->tunerFile = cfg.getString("hipTunerFile");
+  if(cfg.contains("hipLowLatency")) c->lowLatency = cfg.getBool("hipLowLatency");
   string home = homeDataDirOverride;
   if(home.empty()) {
     const char* env = getenv("HOME");
@@ -540,6 +544,8 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
   h->postParams.shortterm_score_error_multiplier = pp.shorttermScoreErrorMultiplier;
 
   maybeAutoTune(*h, logger, serverThreadIdx);
+  const bool lowLatency = context->lowLatency && maxBatchSize <= KGH_LOW_LATENCY_MAX_BATCH;
+  if(lowLatency) checkKgh(kgh_handle_set_low_latency(h->handle, 1), "kgh_handle_set_low_latency");
 
   if(logger != nullptr) {
     char buf[512] = {0};
@@ -549,6 +555,10 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
     logger->write(prefix + "Model version " + Global::intToString(desc.modelVersion) + " useFP16 = " + (h->useFP16 ? "true" : "false") +
                   " useNHWC = true");
     logger->write(prefix + "Model name: " + desc.name + " (" + desc.getShortInfoString() + ")");
+    if(context->lowLatency)
+      logger->write(prefix + (lowLatency ? "Low-latency (split-K) 3x3 convolutions enabled"
+                                         : "hipLowLatency ignored: nnMaxBatchSize above " +
+                                             Global::intToString(KGH_LOW_LATENCY_MAX_BATCH)));
   }
   return h.release();
 }

@@ -72,6 +72,9 @@ def host_library() -> ctypes.CDLL:
         lib.kgn_create_context.restype = c.c_void_p
         lib.kgn_create_context.argtypes = [c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_char_p, c.c_int32]
         lib.kgn_free_context.argtypes = [c.c_void_p]
+        lib.kgn_create_context_cfg.restype = c.c_void_p
+        lib.kgn_create_context_cfg.argtypes = [c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_char_p, c.c_char_p, c.c_char_p,
+                                               c.c_int32]
         lib.kgn_create_context_ex.restype = c.c_void_p
         lib.kgn_create_context_ex.argtypes = [c.c_void_p, c.c_int32, c.c_int32, c.c_int32, c.c_char_p, c.c_int32, c.c_char_p,
                                               c.c_char_p, c.c_int32]
@@ -157,18 +160,25 @@ class ComputeContext:
     """NeuralNet::createComputeContext. use_fp16: True, False or None (auto).
     auto_tune: None keeps the backend default (on), True/False sets
     hipAutoTune; home_data_dir is homeDataDirOverride (tuning tables under
-    <dir>/hiptuning); tuner_file sets hipTunerFile."""
+    <dir>/hiptuning); tuner_file sets hipTunerFile; low_latency sets
+    hipLowLatency (split-K 3x3 convs for handles of max_batch <= 16)."""
 
     def __init__(self, model: LoadedModel, nn_x: int = 19, nn_y: int = 19, use_fp16=None, auto_tune=None,
-                 home_data_dir: str = "", tuner_file: str = ""):
+                 home_data_dir: str = "", tuner_file: str = "", low_latency=None):
         lib = host_library()
         err = _errbuf()
         mode = 2 if use_fp16 is None else (1 if use_fp16 else 0)
         self.model = model
         self.nn_x, self.nn_y = nn_x, nn_y
-        tune = -1 if auto_tune is None else int(bool(auto_tune))
-        self._ptr = lib.kgn_create_context_ex(model._ptr, nn_x, nn_y, mode, home_data_dir.encode(), tune, tuner_file.encode(),
-                                              err, len(err))
+        cfg = []
+        if auto_tune is not None:
+            cfg.append(f"hipAutoTune = {'true' if auto_tune else 'false'}")
+        if tuner_file:
+            cfg.append(f"hipTunerFile = {tuner_file}")
+        if low_latency is not None:
+            cfg.append(f"hipLowLatency = {'true' if low_latency else 'false'}")
+        self._ptr = lib.kgn_create_context_cfg(model._ptr, nn_x, nn_y, mode, home_data_dir.encode(), "\n".join(cfg).encode(),
+                                               err, len(err))
         if not self._ptr:
             _raise(err)
 
@@ -513,6 +523,12 @@ class DeviceHandle:
     def set_graphs(self, on: bool):
         """Enables (default) or disables HIP graph replay of repeated forwards."""
         hip_check(hip_library().kgh_handle_set_graphs(self._ptr, int(on)))
+
+    def set_low_latency(self, on: bool):
+        """kgh_handle_set_low_latency: split-K 3x3 convs (max_batch <= 16)."""
+        lib = hip_library()
+        lib.kgh_handle_set_low_latency.argtypes = [ctypes.c_void_p, ctypes.c_int32]
+        hip_check(lib.kgh_handle_set_low_latency(self._ptr, int(on)))
 
     def profile(self, kind: int):
         ms = ctypes.c_double()
