@@ -314,6 +314,8 @@ def main():
     ap.add_argument("--batch", type=int, default=0, help="boards per forward instead of the config's (not the headline line)")
     ap.add_argument("--latency", action="store_true", help="also time single forwards (always on at --batch 1)")
     ap.add_argument("--no-latency", action="store_true", help="skip the single-forward timing even at --batch 1")
+    ap.add_argument("--low-latency", action="store_true",
+                    help="run the timed forwards in the handle's low-latency mode (split-K 3x3 convs; batch <= 16)")
     ap.add_argument("--no-serve", action="store_true",
                     help="skip the PCIe-inclusive measurement through the batching evaluator")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -351,6 +353,8 @@ def main():
     lm = nn.LoadedModel(path)
     dm = nn.DeviceModel(lm, use_fp16=cfg.fp16)
     h = nn.DeviceHandle(dm, batch)
+    if args.low_latency:
+        h.set_low_latency(True)
     # Tile choices as a backend handle makes them at creation (the on-device
     # autotuner); the table goes to stderr.
     tuning = "" if args.no_autotune else h.autotune()
@@ -434,7 +438,8 @@ def main():
         "config": {"workload": f"C{args.config}: {name} {'fp16' if cfg.fp16 else 'fp32'} boards {boards} in 19x19, batch {batch}, "
                                f"symmetry 0, inputs resident in HBM",
                    "global_batch": batch, "board": "19x19", "parallelism": "none (1 GPU)",
-                   "autotuned_shapes": len([l for l in tuning.splitlines() if l.strip()])},
+                   "autotuned_shapes": len([l for l in tuning.splitlines() if l.strip()]),
+                   **({"low_latency": True} if args.low_latency else {})},
         "mfma_frac_end_to_end": round(value * flops_per_eval / (peak * 1e12), 4),
         "gflop_per_eval": round(flops_per_eval / 1e9, 3),
         "conv_frac": {"achieved": round(conv_frac, 2), "peak": peak, "unit": "TFLOP/s",

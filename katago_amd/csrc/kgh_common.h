@@ -197,9 +197,9 @@ bool convMfmaSupported(int cinPad, int cout);
 // Split-K form of the one-board 3x3 kernel for small batches (the handle's
 // low-latency mode): the conv's 32-channel chunks are spread over up to eight
 // workgroups per (board, 64-column tile), whose fp32 partial sums
-// (convSplitKWorkFloats floats of work) are added in a fixed order by a second
-// kernel that applies the epilogue. Deterministic, but not bitwise equal to
-// the other kernels (different summation order).
+// (convSplitKWorkFloats floats of work) a second kernel adds in a fixed order
+// before applying the epilogue. Deterministic, but not bitwise equal to the
+// other kernels (different summation order).
 bool convSplitKApplies(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, BoardGeom g,
                        const ConvEpilogue<half_t>& epi);
 size_t convSplitKWorkFloats(int cinPad, int cout, BoardGeom g);

@@ -918,6 +918,9 @@ constexpr int BW_BM = 384;
 constexpr int BW_WTM = BW_BM / BW_ROW_WAVES;           // 96 rows per wave
 constexpr int BW_MAX_CIN = 1024;
 
+constexpr int SPLITK_BN = 64;
+constexpr int SPLITK_MAX_SPLITS = 8;
+
 // Zero source of the window's border and gap slots (zero-initialised at load;
 // never written). Long enough for every chunk offset up to BW_MAX_CIN.
 __device__ __attribute__((aligned(256))) half_t kZeroChannels[BW_MAX_CIN + 64];
@@ -925,11 +928,69 @@ __device__ __attribute__((aligned(256))) half_t kZeroChannels[BW_MAX_CIN + 64];
 // Tap at which window load i (0..8) of a window wave is issued (taps 0..5).
 __host__ __device__ constexpr int winLoadTap(int i) { return i * 6 / BW_WIN_PER; }
 
+// Sums split-K partials work[s][m][c0..c0+7] over s = 0, 1, ... in order
+// (all loads issued first), then applies the epilogue contract to the sums.
+template<int ACT>
+__device__ __forceinline__ void splitKEpilogue8(const float* __restrict__ work, int splits, int M, int HW, int cout,
+                                                const ConvEpilogue<half_t>& epi, int m, int c0) {
+  float4 part[2 * SPLITK_MAX_SPLITS];
+#pragma unroll
+  for(int s = 0; s < SPLITK_MAX_SPLITS; s++)
+    if(s < splits) {
+      const float4* p = (const float4*)(work + ((size_t)s * M + m) * cout + c0);
+      part[2 * s] = p[0];
+      part[2 * s + 1] = p[1];
+    }
+  float v[8];
+#pragma unroll
+  for(int k = 0; k < 8; k++) v[k] = 0.0f;
+#pragma unroll
+  for(int s = 0; s < SPLITK_MAX_SPLITS; s++)
+    if(s < splits) {
+      const float4 a = part[2 * s], b = part[2 * s + 1];
+      v[0] += a.x;
+      v[1] += a.y;
+      v[2] += a.z;
+      v[3] += a.w;
+      v[4] += b.x;
+      v[5] += b.y;
+      v[6] += b.z;
+      v[7] += b.w;
+    }
+  if(epi.ncBias != nullptr) {
+    const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
+#pragma unroll
+    for(int k = 0; k < 8; k++) v[k] += nb[k];
+  }
+  const float msk = epi.mask[m];
+  if(epi.residual != nullptr) {
+    const uint4 raw = *(const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0);
+    const half_t* rv = (const half_t*)&raw;
+#pragma unroll
+    for(int k = 0; k < 8; k++) v[k] = epi.maskResidualAdd ? (float)rv[k] + v[k] * msk : (float)rv[k] + v[k];
+  }
+  if(c0 < epi.rawEnd) {
+    half_t o[8];
+#pragma unroll
+    for(int k = 0; k < 8; k++) o[k] = (half_t)v[k];
+    *(uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0) = *(const uint4*)o;
+  }
+  if(epi.outAct != nullptr && c0 >= epi.actBegin) {
+    const int ca = c0 - epi.actBegin;
+    half_t o[8];
+#pragma unroll
+    for(int k = 0; k < 8; k++) o[k] = (half_t)(kgh_activate_fast(v[k] * epi.actScale[ca + k] + epi.actBias[ca + k], ACT) * msk);
+    *(uint4*)(epi.outAct + (size_t)m * epi.ldAct + ca) = *(const uint4*)o;
+  }
+}
+
 // SPLIT: split-K for small batches. Workgroup (board, column tile, split s)
 // runs only the 32-channel chunks of split s (gridDim.y splits) and stores
 // its fp32 accumulators to work[s][m][cout] (board rows only); the residual
 // and the epilogue are left to splitKEpilogueKernel, which sums the splits in
-// order.
+// order. (Summing in the last split to finish instead, behind device-scope
+// fences, measured twice as slow: each fence writes back and invalidates the
+// XCD's whole L2.)
 template<int BN, int NB, bool SPLIT = false>
 __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
                                                                       int cout, const half_t* __restrict__ w, int batch,
@@ -1189,8 +1250,8 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   }
 }
 
-// Sums split-K partials work[s][m][c] over s = 0, 1, ... in order, then
-// applies the epilogue contract to the sum; eight channels per thread.
+
+
 template<int ACT>
 __global__ __launch_bounds__(256) void splitKEpilogueKernel(const float* __restrict__ work, int splits, int M, int HW, int cout,
                                                             ConvEpilogue<half_t> epi) {
@@ -1198,47 +1259,7 @@ __global__ __launch_bounds__(256) void splitKEpilogueKernel(const float* __restr
   const long idx = (long)blockIdx.x * 256 + threadIdx.x;
   if(idx >= (long)M * groups) return;
   const int m = (int)(idx / groups);
-  const int c0 = (int)(idx - (long)m * groups) * 8;
-  float v[8];
-#pragma unroll
-  for(int k = 0; k < 8; k++) v[k] = 0.0f;
-  for(int s = 0; s < splits; s++) {
-    const float4* p = (const float4*)(work + ((size_t)s * M + m) * cout + c0);
-    const float4 a = p[0], b = p[1];
-    v[0] += a.x;
-    v[1] += a.y;
-    v[2] += a.z;
-    v[3] += a.w;
-    v[4] += b.x;
-    v[5] += b.y;
-    v[6] += b.z;
-    v[7] += b.w;
-  }
-  if(epi.ncBias != nullptr) {
-    const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
-#pragma unroll
-    for(int k = 0; k < 8; k++) v[k] += nb[k];
-  }
-  const float msk = epi.mask[m];
-  if(epi.residual != nullptr) {
-    const uint4 raw = *(const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0);
-    const half_t* rv = (const half_t*)&raw;
-#pragma unroll
-    for(int k = 0; k < 8; k++) v[k] = epi.maskResidualAdd ? (float)rv[k] + v[k] * msk : (float)rv[k] + v[k];
-  }
-  if(c0 < epi.rawEnd) {
-    half_t o[8];
-#pragma unroll
-    for(int k = 0; k < 8; k++) o[k] = (half_t)v[k];
-    *(uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0) = *(const uint4*)o;
-  }
-  if(epi.outAct != nullptr && c0 >= epi.actBegin) {
-    const int ca = c0 - epi.actBegin;
-    half_t o[8];
-#pragma unroll
-    for(int k = 0; k < 8; k++) o[k] = (half_t)(kgh_activate_fast(v[k] * epi.actScale[ca + k] + epi.actBias[ca + k], ACT) * msk);
-    *(uint4*)(epi.outAct + (size_t)m * epi.ldAct + ca) = *(const uint4*)o;
-  }
+  splitKEpilogue8<ACT>(work, splits, M, HW, cout, epi, m, (int)(idx - (long)m * groups) * 8);
 }
 
 // ---------------------------------------------------------------------------
@@ -1516,8 +1537,6 @@ bool boardWindowFits(int cinStride, int cinPad, int cout, int bn, BoardGeom g, c
 
 // Split-K at small batches: 64-column tiles, one workgroup per (board,
 // column tile, split); a split takes one or more whole 32-channel chunks.
-constexpr int SPLITK_BN = 64;
-constexpr int SPLITK_MAX_SPLITS = 8;
 int splitKCount(int cinPad) {
   const int chunks = cinPad / 32;
   const int perSplit = (chunks + SPLITK_MAX_SPLITS - 1) / SPLITK_MAX_SPLITS;
