@@ -124,7 +124,9 @@ __global__ void rowMatmulKernel(const float* __restrict__ in, int ldIn, int cin,
 // reference's poolRowsGPool, eigenbackend.cpp:152-177) over the positions of
 // board n, into LDS sums[C] and maxs[C]. Every thread of the block takes
 // part; thread t moves 16-byte channel groups of the positions
-// p = t / CG (mod threads / CG). red holds 2 * blockDim.x * VEC floats.
+// p = t / CG (mod threads / CG), then the threads' partials are reduced
+// within each wavefront by xor shuffles and across wavefronts in order.
+// red holds 2 * blockDim.x * VEC floats.
 // Requires C and ld multiples of the vector width and 16-byte rows.
 template<typename T, int U = 12>
 __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float* __restrict__ mask, int n, int HW, float* sums,
@@ -138,6 +140,9 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
     const int PG = nt / cgN;
     const int cgl = t % cgN;
     const int pg = t / cgN;
+    // Wavefront reduction when a wave holds whole position groups of every
+    // channel group (cgN divides 64); else partials through LDS.
+    const bool waveReduce = 64 % cgN == 0 && nt % 64 == 0;
     float sm[VEC], mx[VEC];
 #pragma unroll
     for(int j = 0; j < VEC; j++) {
@@ -174,18 +179,53 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
           }
         }
       }
+      if(waveReduce) {
+        // The lanes of a wave that share this channel group sit cgN apart:
+        // xor shuffles over those strides leave the wave's sum and maximum
+        // in lanes 0..cgN-1, which store them by wave.
 #pragma unroll
-      for(int j = 0; j < VEC; j++) {
-        red[(pg * cgN + cgl) * VEC + j] = sm[j];
-        red[(nt + pg * cgN + cgl) * VEC + j] = mx[j];
+        for(int j = 0; j < VEC; j++)
+          for(int off = cgN; off < 64; off <<= 1) {
+            sm[j] += __shfl_xor(sm[j], off);
+            mx[j] = fmaxf(mx[j], __shfl_xor(mx[j], off));
+          }
+        const int lane = t & 63;
+        if(lane < cgN) {
+#pragma unroll
+          for(int j = 0; j < VEC; j++) {
+            red[((t >> 6) * cgN + lane) * VEC + j] = sm[j];
+            red[(nt + (t >> 6) * cgN + lane) * VEC + j] = mx[j];
+          }
+        }
+      }
+      else {
+#pragma unroll
+        for(int j = 0; j < VEC; j++) {
+          red[(pg * cgN + cgl) * VEC + j] = sm[j];
+          red[(nt + pg * cgN + cgl) * VEC + j] = mx[j];
+        }
       }
     }
     __syncthreads();
+    const int CV = cgN * VEC;
+    if(waveReduce) {
+      // The waves' totals, in wave order.
+      for(int c = t; c < CV; c += nt) {
+        float a = 0.0f, b = -1.0f;
+        for(int w = 0; w < (nt >> 6); w++) {
+          a += red[w * CV + c];
+          b = fmaxf(b, red[nt * VEC + w * CV + c]);
+        }
+        sums[cg0 * VEC + c] = a;
+        maxs[cg0 * VEC + c] = b;
+      }
+      __syncthreads();
+      continue;
+    }
     // The PG partials of a channel in K consecutive runs, one thread each,
     // then the K run totals in order. K >= 2 needs K * CV <= blockDim, so
     // the run totals fit red2 (2 * blockDim floats); with K = 1 the partials
     // are summed directly.
-    const int CV = cgN * VEC;
     const int K = min(8, nt / CV);
     if(K >= 2) {
       const int L = (PG + K - 1) / K;
@@ -227,6 +267,32 @@ __device__ void poolBoardVec(const T* __restrict__ g, int ld, int C, const float
   }
 }
 
+// out[co] = sum_i pooled[i] * W[i][co] over cin inputs, as four consecutive
+// segments of the inputs (one thread each, all their weight loads in
+// flight) added in order: the same order at any block size, so the fused
+// gpool kernel and the pooling launch agree bitwise. part holds
+// POOL_MATVEC_SEGS * cout floats of LDS; out may be LDS or global memory.
+constexpr int POOL_MATVEC_SEGS = 4;
+__device__ void pooledMatvec(const float* pooled, int cin, const float* __restrict__ W, int cout, float* part, float* out) {
+  const int seg = (cin + POOL_MATVEC_SEGS - 1) / POOL_MATVEC_SEGS;
+  for(int item = threadIdx.x; item < POOL_MATVEC_SEGS * cout; item += blockDim.x) {
+    const int k = item / cout;
+    const int co = item - k * cout;
+    const int i1 = min(cin, (k + 1) * seg);
+    float a = 0.0f;
+#pragma unroll 16
+    for(int i = k * seg; i < i1; i++) a += pooled[i] * W[(size_t)i * cout + co];
+    part[item] = a;
+  }
+  __syncthreads();
+  for(int co = threadIdx.x; co < cout; co += blockDim.x) {
+    float acc = 0.0f;
+#pragma unroll
+    for(int k = 0; k < POOL_MATVEC_SEGS; k++) acc += part[k * cout + co];
+    out[co] = acc;
+  }
+}
+
 // poolKernel with 16-byte loads spread over all threads (see poolBoardVec).
 // Launched with POOL_THREADS threads (the bound lets the unrolled loads keep
 // their registers).
@@ -255,16 +321,7 @@ __global__ __launch_bounds__(POOL_THREADS) void poolVecKernel(const T* __restric
   __syncthreads();
   if(pooledOut != nullptr)
     for(int i = threadIdx.x; i < 3 * C; i += blockDim.x) pooledOut[(size_t)n * ldPooled + i] = pooled[i];
-  if(Wt != nullptr) {
-    for(int co = threadIdx.x; co < cout; co += blockDim.x) {
-      float acc = 0.0f;
-      // Unrolled so that 32 weight loads are in flight at once (the sum order
-      // is unchanged): the loop is a chain of L2 round trips otherwise.
-#pragma unroll 32
-      for(int i = 0; i < 3 * C; i++) acc += pooled[i] * Wt[(size_t)i * cout + co];
-      out[(size_t)n * ldOut + co] = acc;
-    }
-  }
+  if(Wt != nullptr) pooledMatvec(pooled, 3 * C, Wt, cout, red, out + (size_t)n * ldOut);
   (void)VEC;
 }
 
@@ -296,12 +353,7 @@ __global__ __launch_bounds__(GPOOL_ACT_THREADS) void gpoolBiasActKernel(GpoolBia
     pooled[c + 2 * C] = maxs[c];
   }
   __syncthreads();
-  for(int co = threadIdx.x; co < a.cout; co += blockDim.x) {
-    float acc = 0.0f;
-#pragma unroll 32
-    for(int i = 0; i < 3 * C; i++) acc += pooled[i] * a.Wt[(size_t)i * a.cout + co];
-    nb[co] = acc;
-  }
+  pooledMatvec(pooled, 3 * C, a.Wt, a.cout, red, nb);
   __syncthreads();
   // Twelve 16-byte rows in flight per thread (one round at C2's 361 x 128).
   const int CG = a.cout / VEC;
@@ -827,8 +879,10 @@ bool gpoolBiasActApplies(const GpoolBiasActArgs<T>& a) {
   const bool actOk = a.act == KGH_ACT_IDENTITY || a.act == KGH_ACT_RELU || a.act == KGH_ACT_MISH || a.act == KGH_ACT_SILU ||
                      a.act == KGH_ACT_MISH_SCALE8;
   const size_t smem = (size_t)(5 * a.C + a.cout + 2 * GPOOL_ACT_THREADS * VEC + 2 * GPOOL_ACT_THREADS) * sizeof(float);
-  return aligned && actOk && a.C % VEC == 0 && a.ldG % VEC == 0 && a.cout % VEC == 0 && a.ldX % VEC == 0 && a.ldY % VEC == 0 &&
-         a.Wt != nullptr && smem <= 64 * 1024;
+  // The matvec partials reuse the pooling scratch (2 * threads * (VEC + 1) floats).
+  const bool partsFit = POOL_MATVEC_SEGS * a.cout <= 2 * GPOOL_ACT_THREADS * (VEC + 1);
+  return aligned && actOk && partsFit && a.C % VEC == 0 && a.ldG % VEC == 0 && a.cout % VEC == 0 && a.ldX % VEC == 0 &&
+         a.ldY % VEC == 0 && a.Wt != nullptr && smem <= 64 * 1024;
 }
 
 template<typename T>
@@ -877,7 +931,8 @@ template<typename T>
 void launchPool(const T* g, int ldG, int C, const float* mask, const float* maskSum, int batch, int HW, bool valueMode,
                 float* pooledOut, int ldPooled, const float* Wt, int cout, float* out, int ldOut, hipStream_t stream) {
   constexpr int VEC = 16 / (int)sizeof(T);
-  if(C % VEC == 0 && ldG % VEC == 0 && ((uintptr_t)g & 15) == 0) {
+  const bool partsFit = Wt == nullptr || POOL_MATVEC_SEGS * cout <= 2 * POOL_THREADS * (VEC + 1);
+  if(C % VEC == 0 && ldG % VEC == 0 && ((uintptr_t)g & 15) == 0 && partsFit) {
     const int threads = POOL_THREADS;
     const size_t smem = (size_t)(5 * C + 2 * threads * VEC + 2 * threads) * sizeof(float);
     if(valueMode)
