@@ -168,6 +168,7 @@ enum ConvVariant {
   CONV_DMA1H_192,  // 1x1 fp16 DMA kernel with 192-row tiles, two workgroups per CU
   CONV_DMA1H_128,
   CONV_DMA1H_64,
+  CONV_BOARD_HALF_64,  // the one-board kernel on half a board per workgroup (two per CU), 64 output channels per tile
   CONV_VARIANT_COUNT
 };
 

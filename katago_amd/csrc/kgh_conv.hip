@@ -925,8 +925,6 @@ constexpr int SPLITK_MAX_SPLITS = 8;
 // never written). Long enough for every chunk offset up to BW_MAX_CIN.
 __device__ __attribute__((aligned(256))) half_t kZeroChannels[BW_MAX_CIN + 64];
 
-// Tap at which window load i (0..8) of a window wave is issued (taps 0..5).
-__host__ __device__ constexpr int winLoadTap(int i) { return i * 6 / BW_WIN_PER; }
 
 // Sums split-K partials work[s][m][c0..c0+7] over s = 0, 1, ... in order
 // (all loads issued first), then applies the epilogue contract to the sums.
@@ -991,10 +989,16 @@ __device__ __forceinline__ void splitKEpilogue8(const float* __restrict__ work, 
 // order. (Summing in the last split to finish instead, behind device-scope
 // fences, measured twice as slow: each fence writes back and invalidates the
 // XCD's whole L2.)
-template<int BN, int NB, bool SPLIT = false>
-__global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
-                                                                      int cout, const half_t* __restrict__ w, int batch,
-                                                                      ConvEpilogue<half_t> epi, float* __restrict__ work = nullptr) {
+//
+// RW = 2: half a board per workgroup (rows 0..191 or 192..383 of the board's
+// 384, with a window of the 13 padded rows they reach), 2 row waves and 2
+// column waves, two workgroups per CU: twice the workgroups at small and
+// middle batches. Every output sums the same products in the same order as
+// with RW = 4, so the two are bitwise equal.
+template<int BN, int NB, bool SPLIT = false, int RW = BW_ROW_WAVES>
+__global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoardWindowKernel(
+    const half_t* __restrict__ x, int cinStride, int cinPad, int cout, const half_t* __restrict__ w, int batch,
+    ConvEpilogue<half_t> epi, float* __restrict__ work = nullptr) {
   // NB weight buffers, loaded LA = NB - 3 steps ahead: the DMA for step
   // s + LA goes to buffer (s - 3) mod NB, free once step s - 1's barrier is
   // passed. Nine buffers (six steps ahead) for 64-column tiles, whose small
@@ -1013,8 +1017,14 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   constexpr int RB = BW_WTM / 32;
   constexpr int CB = WTN / 32;
   static_assert(WTN % 32 == 0, "wave tile must be a multiple of 32 columns");
-  constexpr int B_PER = BN / 16 / 4;
-  static_assert(B_PER * 64 == BN, "weights split evenly over four waves");
+  static_assert(RW == BW_ROW_WAVES || RW == 2, "a whole board or half of one");
+  constexpr int B_PER = BN / 16 / RW;
+  static_assert(B_PER * 16 * RW == BN, "weights split evenly over the weight waves");
+  // Window: all 21 padded rows, or the 13 that half a board's taps reach.
+  constexpr int WROWS = RW == BW_ROW_WAVES ? BW_PSIDE : 13;
+  constexpr int WIN_PER = RW == BW_ROW_WAVES ? BW_WIN_PER : 11;
+  constexpr int WIN_BYTES = RW * WIN_PER * 1024;
+  static_assert(WIN_BYTES >= WROWS * BW_PSIDE * BW_ROW_BYTES, "window covers the rows");
   // Separate arrays, each addressed at compile time, so the compiler never
   // makes a fragment read wait for DMA into another buffer. The weight
   // buffers are declared first so that they sit in the low 64 KB, where
@@ -1028,8 +1038,8 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   __shared__ __attribute__((aligned(1024))) unsigned char wt6[NB > 6 ? BN * 64 : 64];
   __shared__ __attribute__((aligned(1024))) unsigned char wt7[NB > 6 ? BN * 64 : 64];
   __shared__ __attribute__((aligned(1024))) unsigned char wt8[NB > 6 ? BN * 64 : 64];
-  __shared__ __attribute__((aligned(1024))) unsigned char win0[BW_WIN_BYTES];
-  __shared__ __attribute__((aligned(1024))) unsigned char win1[BW_WIN_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char win0[WIN_BYTES];
+  __shared__ __attribute__((aligned(1024))) unsigned char win1[WIN_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1037,15 +1047,20 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   // The accumulator stage of the residual load and the epilogue (32 x
   // CONV_STAGE_LD floats per wave) lives in win0 while the windows are idle.
   constexpr int STAGE_BYTES = 32 * CONV_STAGE_LD * 4;
-  static_assert(2 * BW_ROW_WAVES * STAGE_BYTES <= BW_WIN_BYTES, "stage fits in a window");
+  static_assert(2 * RW * STAGE_BYTES <= WIN_BYTES, "stage fits in a window");
   float* stage = (float*)(win0 + wave * STAGE_BYTES);
-  const int wm = wave & 3;   // row block of 96
-  const int wn = wave >> 2;  // column half
-  const int loader = wave & 3;
-  const bool loadsWeights = wave < 4;
-  const bool loadsWindow = wave >= 4;
-  int board, colTile;
-  rowColTile(cout / BN, board, colTile);
+  const int wm = wave % RW;  // row block of 96
+  const int wn = wave / RW;  // column half
+  const int loader = wave % RW;
+  const bool loadsWeights = wave < RW;
+  const bool loadsWindow = wave >= RW;
+  int rowTile, colTile;
+  rowColTile(cout / BN, rowTile, colTile);
+  const int board = RW == BW_ROW_WAVES ? rowTile : rowTile >> 1;
+  // First of this workgroup's rows in the board, and the padded row at
+  // which its window starts (one above the first row's board row).
+  const int rowBase = RW == BW_ROW_WAVES ? 0 : (rowTile & 1) * 96 * RW;
+  const int py0 = rowBase / BW_SIDE;
   const int m0 = board * BW_HW;
   const int mEnd = m0 + BW_HW;
   const int n0 = colTile * BN;
@@ -1061,23 +1076,23 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   const int tapStride = cout * cinPad;
 
   // Window load i of this wave fills LDS bytes [1024 j, 1024 j + 1024),
-  // j = wave + 4 i: lane l writes slot q = 64 j + l, which is 16-byte group
-  // q % 5 of window position q / 5. Element offsets into x are 32-bit: the
-  // host keeps tensors below 2^31 elements.
-  const half_t* winPtr[BW_WIN_PER];
+  // j = wave + RW i: lane l writes slot q = 64 j + l, which is 16-byte group
+  // q % 5 of window position q / 5 (padded row py0 + q / 5 / 21). Element
+  // offsets into x are 32-bit: the host keeps tensors below 2^31 elements.
+  const half_t* winPtr[WIN_PER];
 #pragma unroll
-  for(int i = 0; i < BW_WIN_PER; i++) {
-    const int q = 64 * (loader + BW_ROW_WAVES * i) + lane;
+  for(int i = 0; i < WIN_PER; i++) {
+    const int q = 64 * (loader + RW * i) + lane;
     const int pos = q / 5;
     const int grp = q - 5 * pos;
-    const int py = pos / BW_PSIDE;
-    const int px = pos - BW_PSIDE * py;
-    const bool onBoard = grp < 4 && py >= 1 && py <= BW_SIDE && px >= 1 && px <= BW_SIDE;
+    const int wy = pos / BW_PSIDE;
+    const int py = py0 + wy;
+    const int px = pos - BW_PSIDE * wy;
+    const bool onBoard = grp < 4 && wy < WROWS && py >= 1 && py <= BW_SIDE && px >= 1 && px <= BW_SIDE;
     winPtr[i] = onBoard ? x + ((m0 + (py - 1) * BW_SIDE + (px - 1)) * cinStride + grp * 8) : kZeroChannels;
   }
   auto loadWindow = [&](unsigned char* dst, int c, int i) {
-    __builtin_amdgcn_global_load_lds((const void*)(winPtr[i] + c * 32), (lds_void_t*)(dst + (loader + BW_ROW_WAVES * i) * 1024),
-                                     16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(winPtr[i] + c * 32), (lds_void_t*)(dst + (loader + RW * i) * 1024), 16, 0, 0);
   };
   // Weight wave-load i of this wave covers rows 16 (wave * B_PER + i) .. +15
   // of the swizzled 64-byte-row weight buffer. Steps past the end re-read the
@@ -1101,12 +1116,13 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   };
 
   // Byte offset of the lane's A rows at tap (dy, dx) = (-1, -1); rows past
-  // the board's 361 positions read position 0 and are discarded.
+  // the board's 361 positions read the window's first board position and
+  // are discarded.
   int aBase[RB];
 #pragma unroll
   for(int rb = 0; rb < RB; rb++) {
-    const int i = wm * BW_WTM + rb * 32 + laneRow;
-    const int pos = i < BW_HW ? (i / BW_SIDE + 1) * BW_PSIDE + (i % BW_SIDE + 1) : BW_PSIDE + 1;
+    const int i = rowBase + wm * BW_WTM + rb * 32 + laneRow;
+    const int pos = i < BW_HW ? (i / BW_SIDE + 1 - py0) * BW_PSIDE + (i % BW_SIDE + 1) : BW_PSIDE + 1;
     aBase[rb] = (pos - BW_PSIDE - 1) * BW_ROW_BYTES + kq * 16;
   }
   // Weight fragment of column block cb, half step ks: the swizzle term of
@@ -1122,7 +1138,7 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   // C2's residual convs.)
   floatx16 acc[RB][CB];
   if(!SPLIT && epi.residual != nullptr) {
-    residualToAcc<half_t, RB, CB, 1>(acc, epi.residual, epi.ldRes, m0 + wm * BW_WTM, n0 + wn * WTN, mEnd, stage);
+    residualToAcc<half_t, RB, CB, 1>(acc, epi.residual, epi.ldRes, m0 + rowBase + wm * BW_WTM, n0 + wn * WTN, mEnd, stage);
     __syncthreads();
   }
   else {
@@ -1140,7 +1156,7 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
   }
   if(loadsWindow) {
 #pragma unroll
-    for(int i = 0; i < BW_WIN_PER; i++) loadWindow(win0, cBegin, i);
+    for(int i = 0; i < WIN_PER; i++) loadWindow(win0, cBegin, i);
   }
   waitVmcnt<0>();
   barrierNoFence();
@@ -1183,8 +1199,8 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
       if(loadsWeights) loadWeights(wtBuf(P + t + LA), 9 * c + t + LA);
       if(loadsWindow) {
 #pragma unroll
-        for(int i = 0; i < BW_WIN_PER; i++)
-          if(winLoadTap(i) == t) loadWindow(nxt, cNext, i);
+        for(int i = 0; i < WIN_PER; i++)
+          if(i * 6 / WIN_PER == t) loadWindow(nxt, cNext, i);
       }
       half8_t a0[RB], b0[CB];
 #pragma unroll
@@ -1238,7 +1254,7 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
     for(int rb = 0; rb < RB; rb++)
 #pragma unroll
       for(int r = 0; r < 16; r++) {
-        const int i = wm * BW_WTM + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int i = rowBase + wm * BW_WTM + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
         if(i < BW_HW) {
 #pragma unroll
           for(int cb = 0; cb < CB; cb++) dst[(size_t)(m0 + i) * cout + n0 + wn * WTN + cb * 32 + laneRow] = acc[rb][cb][r];
@@ -1246,7 +1262,7 @@ __global__ __launch_bounds__(BW_THREADS, 1) void convBoardWindowKernel(const hal
       }
   }
   else {
-    storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage, m0 + wm * BW_WTM, n0 + wn * WTN, mEnd, BW_HW, epi);
+    storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage, m0 + rowBase + wm * BW_WTM, n0 + wn * WTN, mEnd, BW_HW, epi);
   }
 }
 
@@ -1517,12 +1533,12 @@ void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const
   KGH_CHECK_LAUNCH();
 }
 
-template<int BN>
+template<int BN, int RW = BW_ROW_WAVES>
 void launchBoardWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                        const ConvEpilogue<half_t>& epi, hipStream_t stream) {
-  dim3 grid(g.batch * (cout / BN));
-  hipLaunchKernelGGL((convBoardWindowKernel<BN, BN == 64 ? 9 : 6>), grid, dim3(BW_THREADS), 0, stream, x, cinStride, cinPad, cout, w,
-                     g.batch, epi);
+  dim3 grid(g.batch * (RW == BW_ROW_WAVES ? 1 : 2) * (cout / BN));
+  hipLaunchKernelGGL((convBoardWindowKernel<BN, BN == 64 ? 9 : 6, false, RW>), grid, dim3(128 * RW), 0, stream, x, cinStride, cinPad,
+                     cout, w, g.batch, epi);
   KGH_CHECK_LAUNCH();
 }
 
@@ -1578,7 +1594,10 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
       return true;
     }
     if(cinPad >= 64) {
-      launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      // Half boards (two workgroups per CU) while the doubled count still
+      // fits the CUs' 512 slots in one round.
+      if((long)g.batch * (cout / 64) <= 256) launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
       return true;
     }
   }
@@ -1651,7 +1670,7 @@ bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g
       if(v == CONV_TW_64) return tapWindowFits(cinStride, cinPad, cout, 64, g, epi);
       if(v == CONV_BOARD_192) return boardWindowFits(cinStride, cinPad, cout, 192, g, epi);
       if(v == CONV_BOARD_128) return boardWindowFits(cinStride, cinPad, cout, 128, g, epi);
-      if(v == CONV_BOARD_64) return boardWindowFits(cinStride, cinPad, cout, 64, g, epi);
+      if(v == CONV_BOARD_64 || v == CONV_BOARD_HALF_64) return boardWindowFits(cinStride, cinPad, cout, 64, g, epi);
     }
     else {
       if(v == CONV_DMA1_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
@@ -1697,6 +1716,7 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
       case CONV_BOARD_192: launchBoardWindow<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_128: launchBoardWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_64: launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_BOARD_HALF_64: launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_192: launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_128: launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_64: launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
@@ -1746,7 +1766,7 @@ bool convMfmaSupported(int cinPad, int cout) {
 const char* convVariantName(int variant) {
   static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
                                 "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64",
-                                "dma1x1h_192", "dma1x1h_128", "dma1x1h_64"};
+                                "dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "boardhalf64"};
   return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
 }
 
