@@ -1551,7 +1551,7 @@ bool boardWindowFits(int cinStride, int cinPad, int cout, int bn, BoardGeom g, c
          !epi.maskResidualAdd && !epi.glu && cout % bn == 0 && M * cinStride < (1L << 31) && 9L * cout * cinPad < (1L << 31);
 }
 
-// Split-K at small batches: 64-column tiles, one workgroup per (board,
+// Split-K at small batches: 64-column tiles, one workgroup per (half board,
 // column tile, split); a split takes one or more whole 32-channel chunks.
 int splitKCount(int cinPad) {
   const int chunks = cinPad / 32;
@@ -1838,7 +1838,8 @@ void launchConvSplitK(const half_t* x, int cinStride, int cinPad, int cout, cons
                       const ConvEpilogue<half_t>& epi, float* work, hipStream_t stream) {
   if(!convSplitKApplies(cinStride, cinPad, cout, 3, 3, w, g, epi)) throw KghError(5, "conv: split-K does not apply to this shape");
   const int splits = splitKCount(cinPad);
-  hipLaunchKernelGGL((convBoardWindowKernel<SPLITK_BN, 9, true>), dim3(g.batch * (cout / SPLITK_BN), splits), dim3(BW_THREADS), 0,
+  // Half boards: at one board, 2 x 3 x 6 = 36 workgroups for a 192-channel conv.
+  hipLaunchKernelGGL((convBoardWindowKernel<SPLITK_BN, 9, true, 2>), dim3(g.batch * 2 * (cout / SPLITK_BN), splits), dim3(128 * 2), 0,
                      stream, x, cinStride, cinPad, cout, w, g.batch, epi, work);
   KGH_CHECK_LAUNCH();
   const int M = g.batch * g.H * g.W;
