@@ -931,6 +931,22 @@ __device__ __attribute__((aligned(256))) half_t kZeroChannels[BW_MAX_CIN + 64];
 template<int ACT>
 __device__ __forceinline__ void splitKEpilogue8(const float* __restrict__ work, int splits, int M, int HW, int cout,
                                                 const ConvEpilogue<half_t>& epi, int m, int c0) {
+  // Every load first (partials, residual, mask, per-channel parameters): one
+  // memory round trip per thread.
+  const bool hasRes = epi.residual != nullptr;
+  const bool hasAct = epi.outAct != nullptr && c0 >= epi.actBegin;
+  const int ca = hasAct ? c0 - epi.actBegin : 0;
+  const uint4 raw = hasRes ? *(const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0) : make_uint4(0, 0, 0, 0);
+  const float msk = epi.mask[m];
+  // (The parameter arrays are only 4-byte aligned: scalar loads.)
+  float s8[8], b8[8];
+  if(hasAct) {
+#pragma unroll
+    for(int k = 0; k < 8; k++) {
+      s8[k] = epi.actScale[ca + k];
+      b8[k] = epi.actBias[ca + k];
+    }
+  }
   float4 part[2 * SPLITK_MAX_SPLITS];
 #pragma unroll
   for(int s = 0; s < SPLITK_MAX_SPLITS; s++)
@@ -960,9 +976,7 @@ __device__ __forceinline__ void splitKEpilogue8(const float* __restrict__ work, 
 #pragma unroll
     for(int k = 0; k < 8; k++) v[k] += nb[k];
   }
-  const float msk = epi.mask[m];
-  if(epi.residual != nullptr) {
-    const uint4 raw = *(const uint4*)(epi.residual + (size_t)m * epi.ldRes + c0);
+  if(hasRes) {
     const half_t* rv = (const half_t*)&raw;
 #pragma unroll
     for(int k = 0; k < 8; k++) v[k] = epi.maskResidualAdd ? (float)rv[k] + v[k] * msk : (float)rv[k] + v[k];
@@ -973,11 +987,10 @@ __device__ __forceinline__ void splitKEpilogue8(const float* __restrict__ work, 
     for(int k = 0; k < 8; k++) o[k] = (half_t)v[k];
     *(uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0) = *(const uint4*)o;
   }
-  if(epi.outAct != nullptr && c0 >= epi.actBegin) {
-    const int ca = c0 - epi.actBegin;
+  if(hasAct) {
     half_t o[8];
 #pragma unroll
-    for(int k = 0; k < 8; k++) o[k] = (half_t)(kgh_activate_fast(v[k] * epi.actScale[ca + k] + epi.actBias[ca + k], ACT) * msk);
+    for(int k = 0; k < 8; k++) o[k] = (half_t)(kgh_activate_fast(v[k] * s8[k] + b8[k], ACT) * msk);
     *(uint4*)(epi.outAct + (size_t)m * epi.ldAct + ca) = *(const uint4*)o;
   }
 }
