@@ -128,6 +128,11 @@ struct Block {
   int ropeIndex = -1;
   bool learnableRope = false;
   ConvW qkv, proj;
+  // qkv with the RMSNorm gain folded into its input rows (weights * g[cin]),
+  // for a trunk whose producer records row sums of squares (see
+  // ConvEpilogue); empty when C is not a multiple of 32.
+  ConvW qkvNorm;
+  std::vector<float> normHost;  // g on the host, while the block is built
 };
 
 struct HeadConv {
@@ -309,6 +314,16 @@ struct Builder {
     if(l.i[0] != blk.C) invalid(std::string(what) + ": channel mismatch");
     blk.normEps = l.f[0];
     blk.normW = dev(l, 0, blk.C, what);
+    blk.normHost.assign(host(l, 0), host(l, 0) + blk.C);
+  }
+  // The RMSNorm-folded copy of a transformer block's input GEMM: weights
+  // [cout][cin] with row cin scaled by the norm's gain.
+  void foldNorm(Block& blk, std::vector<float> w, int cout) {
+    if(blk.C % 32 != 0) return;
+    for(int o = 0; o < cout; o++)
+      for(int i = 0; i < blk.C; i++) w[(size_t)o * blk.C + i] *= blk.normHost[i];
+    blk.qkvNorm = makeConv(upload(w), 1, 1, blk.C, cout, false);
+    blk.normHost.clear();
   }
 
   Block block(Net& net, int depth, int streamC) {
@@ -414,6 +429,7 @@ struct Builder {
       appendTransposed(wqkv, host(v, 0), streamC, vC);
       appendTransposed(wo, host(o, 0), aC, streamC);
       blk.qkv = makeConv(upload(wqkv), 1, 1, streamC, qC + kC + vC, false);
+      foldNorm(blk, wqkv, qC + kC + vC);
       blk.proj = makeConv(upload(wo), 1, 1, aC, streamC, false);
       net.tmpC = std::max(net.tmpC, std::max(streamC, std::max(qC + kC + vC, aC)));
     }
@@ -443,6 +459,7 @@ struct Builder {
       }
       appendTransposed(w2, host(l2, 0), F, streamC);
       blk.qkv = makeConv(upload(wg), 1, 1, streamC, 2 * F, false);
+      foldNorm(blk, wg, 2 * F);
       blk.proj = makeConv(upload(w2), 1, 1, F, streamC, false);
       net.tmpC = std::max(net.tmpC, std::max(streamC, F));
     }
@@ -491,6 +508,7 @@ struct kgh_handle {
   void* tmp2 = nullptr;
   void* tmp3 = nullptr;
   float* nbias = nullptr;
+  float* rowSq = nullptr;  // per row and 32-channel block: sums of squares of the trunk (folded RMSNorm)
   void* p1 = nullptr;
   void* gv = nullptr;
   float* g1Bias = nullptr;
@@ -611,6 +629,7 @@ struct Runner {
   T* tmp2;
   T* tmp3;
   float* nbias;
+  float* rowSq = nullptr;  // see kgh_handle::rowSq; null: no folded RMSNorm
 
   ConvEpilogue<T> epi() const {
     ConvEpilogue<T> e;
@@ -706,12 +725,51 @@ struct Runner {
   // holds act(tail(R[depth])) * mask, and R[depth] holds the raw stream only
   // if rawLive (nothing reads it after an inner stack, or after a trunk
   // whose tip BN is applied in the last epilogue, so that store is skipped).
-  void runStack(const std::vector<Block>& blocks, int depth, const BNAct* tail, bool rawLive = true) {
+  //
+  // sqIn: the stream's producer recorded row sums of squares for a folded
+  // RMSNorm of blocks[0]; each block's final conv records them when the block
+  // after it folds its norm.
+  void runStack(const std::vector<Block>& blocks, int depth, const BNAct* tail, bool rawLive = true, bool sqIn = false) {
     for(size_t i = 0; i < blocks.size(); i++) {
       const bool last = i + 1 == blocks.size();
       const BNAct* next = !last ? (isConvKind(blocks[i + 1]) ? &blocks[i + 1].preBN : nullptr) : tail;
-      runBlock(blocks[i], depth, next, !last || rawLive);
+      sqIn = runBlock(blocks[i], depth, next, !last || rawLive, sqIn, !last && normFolds(blocks[i + 1]));
     }
+  }
+
+  // A transformer block whose RMSNorm can fold into its input GEMM.
+  static bool normFolds(const Block& b) { return (b.kind == BK_ATTENTION || b.kind == BK_FFN) && b.qkvNorm.wPrep != nullptr; }
+
+  // Has e's conv record the row sums of squares of its raw output (the trunk,
+  // C channels) for the next block's folded RMSNorm when wanted and the
+  // shapes allow; returns whether it will.
+  bool recordSq(ConvEpilogue<T>& e, const ConvW& c, int ldx, int C, bool want) {
+    if(!want || rowSq == nullptr || e.outRaw == nullptr || e.rawEnd < C || C % 32 != 0) return false;
+    ConvEpilogue<T> t = e;
+    t.sumSqOut = rowSq;
+    t.ldSq = C / 32;
+    if(!kgh::convNormFoldOk<T>(ldx, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, t)) return false;
+    e = t;
+    return true;
+  }
+
+  // A transformer block's input GEMM (x = the trunk Rd): with the producer's
+  // row sums, on the norm-folded weights with the row scale in the epilogue;
+  // else after an RMSNorm launch into xn.
+  void normedInputConv(const Block& b, T* Rd, int C, T* xn, ConvEpilogue<T> e, bool sqIn) {
+    if(sqIn) {
+      ConvEpilogue<T> t = e;
+      t.rowNormIn = rowSq;
+      t.ldNorm = C / 32;
+      t.normC = C;
+      t.normEps = b.normEps;
+      if(kgh::convNormFoldOk<T>(C, b.qkvNorm.cinPad, b.qkvNorm.cout, 1, 1, b.qkvNorm.wPrep, t)) {
+        conv(b.qkvNorm, Rd, C, t);
+        return;
+      }
+    }
+    kgh::launchRmsNorm<T>(Rd, C, xn, C, C, b.normW, nullptr, b.normEps, KGH_ACT_IDENTITY, mask, M, s);
+    conv(b.qkv, xn, C, e);
   }
 
   // The residual update's raw output is dropped when nothing reads it (the
@@ -722,7 +780,10 @@ struct Runner {
     e.rawEnd = 0;
   }
 
-  void runBlock(const Block& b, int depth, const BNAct* next, bool rawNeeded = true) {
+  // Returns whether the block's final conv recorded row sums of squares
+  // (wantSq: the next block folds its RMSNorm).
+  bool runBlock(const Block& b, int depth, const BNAct* next, bool rawNeeded = true, bool sqIn = false, bool wantSq = false) {
+    bool sqOut = false;
     T* Rd = R[depth];
     T* Ad = A[depth];
     const int C = (b.kind == BK_ATTENTION || b.kind == BK_FFN) ? b.C : b.preBN.C;
@@ -740,6 +801,7 @@ struct Runner {
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
       dropDeadRaw(e2, rawNeeded);
+      sqOut = recordSq(e2, b.conv2, b.conv1.cout, C, wantSq);
       conv(b.conv2, tmp1, b.conv1.cout, e2);
     }
     else if(b.kind == BK_GPOOL) {
@@ -804,6 +866,7 @@ struct Runner {
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
       dropDeadRaw(e2, rawNeeded);
+      sqOut = recordSq(e2, b.conv2, b.regC, C, wantSq);
       conv(b.conv2, tmp3, b.regC, e2);
     }
     else if(b.kind == BK_NBT) {
@@ -826,6 +889,7 @@ struct Runner {
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
       dropDeadRaw(e2, rawNeeded);
+      sqOut = recordSq(e2, b.conv2, midC, C, wantSq);
       conv(b.conv2, Am, midC, e2);
     }
     else if(b.kind == BK_ATTENTION) {
@@ -835,12 +899,11 @@ struct Runner {
       T* xn = tmp1;
       T* qkv = tmp2;
       T* att = tmp3;
-      kgh::launchRmsNorm<T>(Rd, C, xn, C, C, b.normW, nullptr, b.normEps, KGH_ACT_IDENTITY, mask, M, s);
       ConvEpilogue<T> e1 = epi();
       e1.outRaw = qkv;
       e1.ldRaw = qkvC;
       e1.rawEnd = INT_MAX;
-      conv(b.qkv, xn, C, e1);
+      normedInputConv(b, Rd, C, xn, e1, sqIn);
       const float* cosT = nullptr;
       const float* sinT = nullptr;
       if(b.ropeIndex >= 0) {
@@ -859,6 +922,7 @@ struct Runner {
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
       dropDeadRaw(e2, rawNeeded);
+      sqOut = recordSq(e2, b.proj, aC, C, wantSq);
       conv(b.proj, att, aC, e2);
     }
     else if(b.kind == BK_FFN) {
@@ -866,14 +930,13 @@ struct Runner {
       const int F = b.ffnC;
       T* xn = tmp1;
       T* hid = tmp2;
-      kgh::launchRmsNorm<T>(Rd, C, xn, C, C, b.normW, nullptr, b.normEps, KGH_ACT_IDENTITY, mask, M, s);
       ConvEpilogue<T> e1 = epi();
       e1.outAct = hid;
       e1.ldAct = F;
       e1.actBegin = 0;
       e1.actKind = KGH_ACT_SILU;
       e1.glu = 1;
-      conv(b.qkv, xn, C, e1);
+      normedInputConv(b, Rd, C, xn, e1, sqIn);
       ConvEpilogue<T> e2 = epi();
       e2.residual = Rd;
       e2.ldRes = C;
@@ -883,11 +946,13 @@ struct Runner {
       e2.rawEnd = C;
       setAct(e2, next, Ad, C);
       dropDeadRaw(e2, rawNeeded);
+      sqOut = recordSq(e2, b.proj, F, C, wantSq);
       conv(b.proj, hid, F, e2);
     }
     else {
       throw KghError(KGH_ERR_INTERNAL, "unknown block kind");
     }
+    return sqOut;
   }
 };
 
@@ -899,6 +964,7 @@ Runner<T> makeRunner(const Net& net, kgh_handle* h, int batch) {
     r.R.push_back((T*)h->R[d]);
     r.A.push_back((T*)h->A[d]);
   }
+  r.rowSq = h->rowSq;
   return r;
 }
 
@@ -914,6 +980,7 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
                        net.trunkC, n, s);
 
   // Stem: R0 = conv(x) + globalBias[n]; A0 = first block's preBN activation.
+  bool stemSq = false;
   {
     ConvEpilogue<T> e = r.epi();
     e.ncBias = h->gbias;
@@ -923,9 +990,10 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
     e.rawEnd = net.trunkC;
     const BNAct* first = Runner<T>::isConvKind(net.blocks[0]) ? &net.blocks[0].preBN : nullptr;
     Runner<T>::setAct(e, first, r.A[0], net.trunkC);
+    stemSq = r.recordSq(e, net.initialConv, net.inputCPad, net.trunkC, Runner<T>::normFolds(net.blocks[0]));
     r.conv(net.initialConv, (const T*)h->x0, net.inputCPad, e);
   }
-  r.runStack(net.blocks, 0, net.tipKind == 0 ? &net.tipBN : nullptr, net.tipKind != 0);
+  r.runStack(net.blocks, 0, net.tipKind == 0 ? &net.tipBN : nullptr, net.tipKind != 0, stemSq);
   if(net.tipKind != 0) {
     // Trunk-tip RMSNorm + activation into A[0], the heads' input.
     if(net.tipSpatial)
@@ -1304,6 +1372,9 @@ size_t carveActivations(kgh_handle* h, int maxBatch, int nn_x, int nn_y, Take&& 
   h->tmp2 = get(M * tmpC * es);
   h->tmp3 = get(M * tmpC * es);
   h->nbias = getF(B * tmpC);
+  int maxC = 1;
+  for(int c : net.depthC) maxC = std::max(maxC, c);
+  h->rowSq = getF(M * (size_t)((maxC + 31) / 32));
   h->p1 = get(M * net.p1C * es);
   h->gv = get(M * (net.g1C + net.v1C) * es);
   h->g1Bias = getF(B * net.p1C);

@@ -102,6 +102,14 @@ template<typename T> __device__ __forceinline__ T kgh_from_float(float v) { retu
 // BN + activation + mask, residual accumulation, the per-(n,c) bias of the
 // global-input matmul, the raw/activated split of a combined regular+gpool
 // convolution, and the gated linear unit.
+//
+// A transformer block's RMSNorm (y = mask ? x * g / sqrt(mean(x^2) + eps) : 0)
+// folds into the GEMM that consumes y: g scales that GEMM's weight rows, the
+// producer of x records, per row and 32-column block, the sum of squares of
+// the raw values it stores (sumSqOut, ldSq floats per row, needs rawEnd a
+// multiple of 32), and the consumer first scales its accumulators by
+//   mask[m] / sqrt(sum_b rowNormIn[m*ldNorm + b] / normC + normEps)
+// (matrix-core kernels only).
 template<typename T>
 struct ConvEpilogue {
   T* outRaw;
@@ -120,7 +128,55 @@ struct ConvEpilogue {
   const float* ncBias;
   int ldNC;
   int glu;
+  float* sumSqOut;
+  int ldSq;
+  const float* rowNormIn;
+  int ldNorm;
+  int normC;
+  float normEps;
 };
+
+// The consumer row scale of a folded RMSNorm (see ConvEpilogue): the block
+// sums added in order, then 1 / sqrt(mean + eps) as the RMSNorm kernel
+// computes it, times the mask.
+template<typename T>
+__device__ __forceinline__ float kgh_row_norm_from_sum(const ConvEpilogue<T>& e, float ss, float msk) {
+  return msk * (1.0f / sqrtf(ss / (float)e.normC + e.normEps));
+}
+
+template<typename T>
+__device__ __forceinline__ float kgh_row_norm_scale(const ConvEpilogue<T>& e, int m, float msk) {
+  const float* p = e.rowNormIn + (size_t)m * e.ldNorm;
+  float ss = 0.0f;
+  for(int b = 0; b < e.ldNorm; b++) ss += p[b];
+  return kgh_row_norm_from_sum(e, ss, msk);
+}
+
+// Most block sums per row a folded RMSNorm takes (C <= 1024).
+constexpr int KGH_NORM_MAX_BLOCKS = 32;
+
+// The same scale in two parts, so that a kernel can issue every load of a row
+// (its block sums and mask) before other work and add them later. ldNorm is
+// at least 1; the entries past ldNorm are +0 and the sum is never negative,
+// so adding them leaves it unchanged, and starting the sum from q[0] equals
+// starting it from 0. (Both keep the compiler from placing an add, and a
+// wait for its load, beside the loads.)
+template<typename T>
+__device__ __forceinline__ void kgh_row_norm_load(const ConvEpilogue<T>& e, int m, float (&q)[KGH_NORM_MAX_BLOCKS], float& msk) {
+  const float* p = e.rowNormIn + (size_t)m * e.ldNorm;
+  q[0] = p[0];
+#pragma unroll
+  for(int b = 1; b < KGH_NORM_MAX_BLOCKS; b++) q[b] = b < e.ldNorm ? p[b] : 0.0f;
+  msk = e.mask[m];
+}
+
+template<typename T>
+__device__ __forceinline__ float kgh_row_norm_finish(const ConvEpilogue<T>& e, const float (&q)[KGH_NORM_MAX_BLOCKS], float msk) {
+  float ss = q[0];
+#pragma unroll
+  for(int b = 1; b < KGH_NORM_MAX_BLOCKS; b++) ss += q[b];
+  return kgh_row_norm_from_sum(e, ss, msk);
+}
 
 template<typename T>
 __device__ __forceinline__ void kgh_epilogue_store(const ConvEpilogue<T>& e, int m, int n, int c, float acc) {
@@ -194,6 +250,12 @@ bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int 
 
 template<typename T>
 bool convMfmaSupported(int cinPad, int cout);
+
+// Whether launchConv takes the epilogue's folded-RMSNorm fields for this
+// shape (a matrix-core kernel; raw split on 32 columns; no residual where the
+// accumulators are scaled).
+template<typename T>
+bool convNormFoldOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi);
 
 // Split-K form of the one-board 3x3 kernel for small batches (the handle's
 // low-latency mode): the conv's 32-channel chunks are spread over up to eight

@@ -87,6 +87,22 @@ __host__ __device__ __forceinline__ void withActKind(int act, bool used, F&& f) 
   }
 }
 
+// Sum of squares of the 16 stored values of this lane, added to its partner
+// lane's (the other 16 columns of the same row and 32-column block), stored
+// once per block: the producer side of a folded RMSNorm (see ConvEpilogue).
+// Both lanes of a pair take this path together (rawEnd is a multiple of 32).
+template<typename T>
+__device__ __forceinline__ void storeBlockSumSq(const ConvEpilogue<T>& epi, int m, int c0, const T (&o)[16]) {
+  float ss = 0.0f;
+#pragma unroll
+  for(int j = 0; j < 16; j++) {
+    const float f = kgh_to_float(o[j]);
+    ss += f * f;
+  }
+  ss += __shfl_xor(ss, 1);
+  if((c0 & 16) == 0) epi.sumSqOut[(size_t)m * epi.ldSq + (c0 >> 5)] = ss;
+}
+
 template<typename T, int BN, int WM, int ACT>
 __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / WM / 32][BN / (4 / WM) / 32], unsigned char* smem,
                                                      int m0, int n0, int M, int HW, const ConvEpilogue<T>& epi) {
@@ -144,6 +160,11 @@ __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / W
           v[4 * q + 3] = t.w;
         }
         const float msk = epi.mask[m];
+        if(epi.rowNormIn != nullptr) {
+          const float sc = kgh_row_norm_scale(epi, m, msk);
+#pragma unroll
+          for(int j = 0; j < 16; j++) v[j] *= sc;
+        }
         if(epi.ncBias != nullptr) {
           const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
 #pragma unroll
@@ -167,6 +188,7 @@ __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / W
           uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
 #pragma unroll
           for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
+          if(epi.sumSqOut != nullptr) storeBlockSumSq(epi, m, c0, o);
         }
         if(actCols && epi.glu) {
           T o[8];
@@ -495,9 +517,11 @@ __device__ __forceinline__ void barrierNoFence() {
 // and only the outputs touch memory here. The stage is private to the wave and a wave's LDS operations execute in order, so no
 // workgroup barrier is needed; the empty asm statements only keep the
 // compiler from reordering the stage accesses.
+// nscLds: the folded-RMSNorm row scales of the wave's rows (row r of the
+// wave at nscLds[r]) when the kernel computed them, else null (computed here).
 template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, int ACT>
 __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
-                                                     const ConvEpilogue<T>& epi) {
+                                                     const ConvEpilogue<T>& epi, const float* nscLds) {
   constexpr int VEC = 16 / (int)sizeof(T);
   constexpr int RV = 16 / VEC;  // 16-byte vectors per lane per block
   const int lane = threadIdx.x & 63;
@@ -505,10 +529,12 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
   const int half = lane & 1;   // which 16-channel half of the 32 columns
   const int lrow = lane >> 1;  // 0..31
   float msk[RB];
+  float nsc[RB];  // folded RMSNorm row scales, once per row
 #pragma unroll
   for(int rb = 0; rb < RB; rb++) {
     const int m = mBase + rb * 32 + lrow;
     msk[rb] = m < M ? epi.mask[m] : 0.0f;
+    nsc[rb] = epi.rowNormIn == nullptr || m >= M ? 0.0f : nscLds != nullptr ? nscLds[rb * 32 + lrow] : kgh_row_norm_scale(epi, m, msk[rb]);
   }
 #pragma unroll
   for(int cb = 0; cb < CB; cb++) {
@@ -541,6 +567,10 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
       }
       const int m = mBase + rb * 32 + lrow;
       if(m < M) {
+        if(epi.rowNormIn != nullptr) {
+#pragma unroll
+          for(int j = 0; j < 16; j++) v[j] *= nsc[rb];
+        }
         if(epi.ncBias != nullptr) {
           const float* nb = epi.ncBias + (size_t)(m / HW) * epi.ldNC + c0;
 #pragma unroll
@@ -564,6 +594,7 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
           uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
 #pragma unroll
           for(int q = 0; q < RV; q++) dst[q] = ((const uint4*)o)[q];
+          if(epi.sumSqOut != nullptr) storeBlockSumSq(epi, m, c0, o);
         }
         if constexpr(GLU) {
           if(actCols) {
@@ -595,14 +626,14 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
 constexpr int KGH_ACT_DYNAMIC = -1;
 template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, bool ACT_FIXED = true>
 __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
-                                                  const ConvEpilogue<T>& epi) {
+                                                  const ConvEpilogue<T>& epi, const float* nscLds = nullptr) {
   if constexpr(ACT_FIXED) {
     withActKind(epi.actKind, epi.outAct != nullptr, [&](auto actTag) {
-      storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, GLU, decltype(actTag)::value>(acc, stage, mBase, nBase, M, HW, epi);
+      storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, GLU, decltype(actTag)::value>(acc, stage, mBase, nBase, M, HW, epi, nscLds);
     });
   }
   else {
-    storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, GLU, KGH_ACT_DYNAMIC>(acc, stage, mBase, nBase, M, HW, epi);
+    storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, GLU, KGH_ACT_DYNAMIC>(acc, stage, mBase, nBase, M, HW, epi, nscLds);
   }
 }
 
@@ -1331,6 +1362,7 @@ __global__ __launch_bounds__(BM / 48 * 64, BM == 384 ? 1 : 2) void conv1x1DmaKer
   __shared__ __attribute__((aligned(1024))) unsigned char b1s[BN * 64];
   __shared__ __attribute__((aligned(1024))) unsigned char b2s[BN * 64];
   __shared__ __attribute__((aligned(16))) float stageArr[BM == 384 ? 8 * 32 * CONV_STAGE_LD : 4];
+  __shared__ float rowScale[BM];  // folded-RMSNorm row scales of the tile
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1406,6 +1438,14 @@ __global__ __launch_bounds__(BM / 48 * 64, BM == 384 ? 1 : 2) void conv1x1DmaKer
   }
 
   const bool resInAcc = epi.residual != nullptr && !epi.maskResidualAdd;
+  // A folded RMSNorm's row scales (no residual then): thread t < BM issues
+  // row m0 + t's block sums and mask before the first DMA and finishes the
+  // scale into LDS once the first step has landed, so the epilogue reads
+  // one LDS value per row.
+  const bool rowNorm = epi.rowNormIn != nullptr;
+  const bool normRow = rowNorm && tid < BM && m0 + tid < M;
+  float nq[KGH_NORM_MAX_BLOCKS], nMask = 0.0f;
+  if(normRow) kgh_row_norm_load(epi, m0 + tid, nq, nMask);
   floatx16 acc[RB][CB];
   // BM = 384: the first two steps' DMA overlaps the residual load. BM = 192:
   // the stage shares the A buffers, so the residual is loaded first.
@@ -1430,6 +1470,8 @@ __global__ __launch_bounds__(BM / 48 * 64, BM == 384 ? 1 : 2) void conv1x1DmaKer
     load(1, 1);
   }
   waitStep();
+  // Visible to the epilogue after the barriers of the step loop.
+  if(rowNorm && tid < BM) rowScale[tid] = normRow ? kgh_row_norm_finish(epi, nq, nMask) : 0.0f;
   barrierNoFence();
 
   auto step = [&](auto pTag, int st) {
@@ -1462,7 +1504,7 @@ __global__ __launch_bounds__(BM / 48 * 64, BM == 384 ? 1 : 2) void conv1x1DmaKer
 
   ConvEpilogue<half_t> e = epi;
   if(resInAcc) e.residual = nullptr;
-  storeWaveEpilogue<half_t, RB, CB, false, GLU>(acc, stage, m0 + wm * WTM, n0 + wn * WTN, M, HW, e);
+  storeWaveEpilogue<half_t, RB, CB, false, GLU>(acc, stage, m0 + wm * WTM, n0 + wn * WTN, M, HW, e, rowScale + wm * WTM);
 }
 
 // Direct convolution: one thread per output element. Used for shapes the
@@ -1808,8 +1850,16 @@ bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int 
 }
 
 template<typename T>
+bool convNormFoldOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi) {
+  return mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) && (epi.sumSqOut == nullptr || epi.rawEnd % 32 == 0) &&
+         (epi.rowNormIn == nullptr || (epi.residual == nullptr && epi.ldNorm >= 1 && epi.ldNorm <= KGH_NORM_MAX_BLOCKS));
+}
+
+template<typename T>
 void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky, int kx, const void* wPrepared,
                 const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma, int variant) {
+  if((epi.sumSqOut != nullptr || epi.rowNormIn != nullptr) && !convNormFoldOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi))
+    throw KghError(5, "conv: a folded RMSNorm needs the matrix-core kernels");
   bool done = false;
   if(variant != CONV_AUTO && convVariantApplies<T>(variant, x, cinStride, cinPad, cout, ky, kx, wPrepared, g, epi)) {
     launchVariant<T>(variant, ky, x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
@@ -1839,7 +1889,8 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
 
 bool convSplitKApplies(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, BoardGeom g,
                        const ConvEpilogue<half_t>& epi) {
-  return ky == 3 && kx == 3 && cinPad >= 64 && mfmaPathOk<half_t>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
+  return ky == 3 && kx == 3 && cinPad >= 64 && epi.sumSqOut == nullptr && epi.rowNormIn == nullptr &&
+         mfmaPathOk<half_t>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
          boardWindowFits(cinStride, cinPad, cout, SPLITK_BN, g, epi) && cout % 8 == 0;
 }
 
@@ -1887,6 +1938,8 @@ void launchConvertToFloat(const T* src, float* dst, size_t n, hipStream_t stream
   KGH_CHECK_LAUNCH();
 }
 
+template bool convNormFoldOk<float>(int, int, int, int, int, const void*, const ConvEpilogue<float>&);
+template bool convNormFoldOk<half_t>(int, int, int, int, int, const void*, const ConvEpilogue<half_t>&);
 template bool convMfmaSupported<float>(int, int);
 template bool convMfmaSupported<half_t>(int, int);
 template void launchConv<float>(const float*, int, int, int, int, int, int, const void*, const float*, BoardGeom,

@@ -13,8 +13,16 @@ import pytest
 
 from katago_amd import modelgen, nn
 
+def _variant_count():
+    """CONV_VARIANT_COUNT: the entries of ConvVariant in kgh_common.h."""
+    import re
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "katago_amd", "csrc", "kgh_common.h")
+    body = re.search(r"enum ConvVariant \{(.*?)CONV_VARIANT_COUNT", open(path).read(), re.S).group(1)
+    return len(re.findall(r"^\s*(CONV_\w+)", body, re.M))
+
+
 # Kernel variant ids 0..VARIANTS-1 (ConvVariant in kgh_common.h).
-VARIANTS = 19
+VARIANTS = _variant_count()
 
 pytestmark = pytest.mark.gpu
 
