@@ -91,15 +91,28 @@ __host__ __device__ __forceinline__ void withActKind(int act, bool used, F&& f) 
 // lane's (the other 16 columns of the same row and 32-column block), stored
 // once per block: the producer side of a folded RMSNorm (see ConvEpilogue).
 // Both lanes of a pair take this path together (rawEnd is a multiple of 32).
+// fp16 values square exactly in fp32; the pairs go through the packed dot
+// product (one instruction per two values, no conversions).
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 template<typename T>
 __device__ __forceinline__ void storeBlockSumSq(const ConvEpilogue<T>& epi, int m, int c0, const T (&o)[16]) {
   float ss = 0.0f;
+  if constexpr(std::is_same<T, half_t>::value) {
 #pragma unroll
-  for(int j = 0; j < 16; j++) {
-    const float f = kgh_to_float(o[j]);
-    ss += f * f;
+    for(int j = 0; j < 8; j++) {
+      const half2_t h = {o[2 * j], o[2 * j + 1]};
+      ss = __builtin_amdgcn_fdot2(h, h, ss, false);
+    }
   }
-  ss += __shfl_xor(ss, 1);
+  else {
+#pragma unroll
+    for(int j = 0; j < 16; j++) {
+      const float f = kgh_to_float(o[j]);
+      ss += f * f;
+    }
+  }
+  // Partner lane by a DPP quad permutation [1,0,3,2] (no LDS round trip).
+  ss += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ss), 0xB1, 0xF, 0xF, false));
   if((c0 & 16) == 0) epi.sumSqOut[(size_t)m * epi.ldSq + (c0 >> 5)] = ss;
 }
 
