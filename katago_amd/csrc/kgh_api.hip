@@ -543,7 +543,7 @@ struct kgh_handle {
   float* dPost = nullptr;
   int* dErr = nullptr;
 
-  std::vector<const float*> ropeCos, ropeSin;  // per RopeSpec of the model: [table][pair][H*W]
+  std::vector<const float*> ropeCos, ropeSin;  // per RopeSpec of the model: [table][H*W][pair]
 
   bool profiling = false;
   std::vector<ProfRec> prof;
@@ -1507,7 +1507,7 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     const size_t M = (size_t)max_batch * nn_x * nn_y;
     DeviceArena& a = h->arena;
     carveActivations(h.get(), max_batch, nn_x, nn_y, [&](size_t bytes) { return a.alloc(bytes); });
-    // Rotary tables per attention block, [table][pair][y * nn_x + x]: the
+    // Rotary tables per attention block, [table][y * nn_x + x][pair]: the
     // angle formulas of TransformerAttentionDesc::computeRopeCosSin
     // (desc.cpp:1212-1275).
     for(const RopeSpec& rs : net.ropes) {
@@ -1529,7 +1529,7 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
                 const float freq = 1.0f / powf(rs.theta, (float)(2 * q) / (float)(rs.dq / 2));
                 angle = (float)(p < halfPairs ? y : x) * freq;
               }
-              const size_t idx = ((size_t)tb * pairs + p) * HW + (size_t)y * nn_x + x;
+              const size_t idx = ((size_t)tb * HW + (size_t)y * nn_x + x) * pairs + p;
               cs[idx] = cosf(angle);
               sn[idx] = sinf(angle);
             }

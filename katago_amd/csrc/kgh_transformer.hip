@@ -173,8 +173,8 @@ __global__ void rmsNormApplyKernel(const T* __restrict__ x, int ldX, T* __restri
 }
 
 // Rotary embedding in place on the Q and K parts of a QKV row: one thread
-// per (row, head, pair). Tables are [table][pair][HW] with table = the kv
-// head for learnable tables, else 0.
+// per (row, head, pair). Tables are [table][HW][pair] (a position's pairs
+// contiguous) with table = the kv head for learnable tables, else 0.
 template<typename T>
 __global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, const float* __restrict__ cosT,
                            const float* __restrict__ sinT, int learnable, int HW, int M) {
@@ -189,8 +189,8 @@ __global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, c
   int table = 0;
   if(learnable) table = head < H ? head * KV / H : head - H;
   const int xy = row % HW;
-  const float cs = cosT[((size_t)table * pairs + p) * HW + xy];
-  const float sn = sinT[((size_t)table * pairs + p) * HW + xy];
+  const float cs = cosT[((size_t)table * HW + xy) * pairs + p];
+  const float sn = sinT[((size_t)table * HW + xy) * pairs + p];
   T* e = qkv + (size_t)row * ld + head * dq + 2 * p;
   const float x0 = kgh_to_float(e[0]), x1 = kgh_to_float(e[1]);
   e[0] = kgh_from_float<T>(x0 * cs - x1 * sn);
@@ -212,7 +212,7 @@ constexpr int FA_THREADS = 768;
 constexpr int FA_MAX_KEYS = 384;
 
 // With cosT non-null the rotary embedding is applied here, to K rows as they
-// are staged and to Q fragments as they are loaded (tables [table][pair][HW],
+// are staged and to Q fragments as they are loaded (tables [table][HW][pair],
 // table = kv head when learnable, else 0): each rotated value is rounded to
 // fp16 once, exactly as when a separate pass rotates Q and K in place.
 template<int DQ, int DV>
@@ -238,7 +238,13 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
   // Stage K rows (16-byte groups), V^T (8 dims of one key per thread) and the
   // key mask; keys past HW and dims past DV are zero.
   constexpr int PAIRS = DQ / 2;
-  for(int i = tid; i < FA_MAX_KEYS * (DQ / 8); i += FA_THREADS) {
+  constexpr int K_ITERS = FA_MAX_KEYS * (DQ / 8) / FA_THREADS;
+  constexpr int V_ITERS = FA_MAX_KEYS * (DVP / 8) / FA_THREADS;
+  static_assert(K_ITERS * FA_THREADS == FA_MAX_KEYS * (DQ / 8) && V_ITERS * FA_THREADS == FA_MAX_KEYS * (DVP / 8),
+                "staging loops without a remainder");
+#pragma unroll
+  for(int it = 0; it < K_ITERS; it++) {
+    const int i = tid + it * FA_THREADS;
     const int key = i / (DQ / 8);
     const int g = i - key * (DQ / 8);
     half_t v[8];
@@ -246,20 +252,24 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
     if(key < HW) {
       *(uint4*)v = *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8);
       if(cosT != nullptr) {
-        const size_t tb = (size_t)(learnable ? kvh : 0) * PAIRS;
+        // The group's four pairs are contiguous in the tables: one 16-byte
+        // load each.
+        const size_t ti = ((size_t)(learnable ? kvh : 0) * HW + key) * PAIRS + g * 4;
+        const float4 c4 = *(const float4*)(cosT + ti), s4 = *(const float4*)(sinT + ti);
+        const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
         for(int q = 0; q < 4; q++) {
-          const size_t ti = (tb + g * 4 + q) * HW + key;
-          const float c = cosT[ti], sn = sinT[ti];
           const float x0 = (float)v[2 * q], x1 = (float)v[2 * q + 1];
-          v[2 * q] = (half_t)(x0 * c - x1 * sn);
-          v[2 * q + 1] = (half_t)(x0 * sn + x1 * c);
+          v[2 * q] = (half_t)(x0 * cc[q] - x1 * ss[q]);
+          v[2 * q + 1] = (half_t)(x0 * ss[q] + x1 * cc[q]);
         }
       }
     }
     *(uint4*)&Ks[key * KLD + g * 8] = *(const uint4*)v;
   }
-  for(int i = tid; i < FA_MAX_KEYS * (DVP / 8); i += FA_THREADS) {
+#pragma unroll
+  for(int it = 0; it < V_ITERS; it++) {
+    const int i = tid + it * FA_THREADS;
     const int key = i / (DVP / 8);
     const int g = i - key * (DVP / 8);
     half_t v[8];
@@ -285,14 +295,14 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
   for(int ks = 0; ks < DQ / 16; ks++) {
     qf[ks] = *(const half8_t*)(qkv + (rowBase + qRow) * ld + h * DQ + ks * 16 + kq * 8);
     if(cosT != nullptr) {
-      const size_t tb = (size_t)(learnable ? h * KV / H : 0) * PAIRS;
+      const size_t ti = ((size_t)(learnable ? h * KV / H : 0) * HW + qRow) * PAIRS + (ks * 16 + kq * 8) / 2;
+      const float4 c4 = *(const float4*)(cosT + ti), s4 = *(const float4*)(sinT + ti);
+      const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
       for(int q = 0; q < 4; q++) {
-        const size_t ti = (tb + (ks * 16 + kq * 8) / 2 + q) * HW + qRow;
-        const float c = cosT[ti], sn = sinT[ti];
         const float x0 = (float)qf[ks][2 * q], x1 = (float)qf[ks][2 * q + 1];
-        qf[ks][2 * q] = (half_t)(x0 * c - x1 * sn);
-        qf[ks][2 * q + 1] = (half_t)(x0 * sn + x1 * c);
+        qf[ks][2 * q] = (half_t)(x0 * cc[q] - x1 * ss[q]);
+        qf[ks][2 * q + 1] = (half_t)(x0 * ss[q] + x1 * cc[q]);
       }
     }
   }

@@ -118,3 +118,26 @@ def test_half_height_1x1_variants_give_identical_bits_on_nbt(model_dir, variant)
     out = _forward(tuned, sp, gl)
     for k in out:
         assert np.array_equal(out[k], ref[k]), k
+
+
+def test_every_kernel_variant_gives_identical_bits_on_transformer(model_dir):
+    """C4's transformer net with every shape pinned to each variant in turn:
+    the 1x1 DMA kernels (384- and 192-row tiles) against the built-in tile
+    kernel at 12 boards, on the [Q|K|V] and SwiGLU GEMMs that scale their
+    rows by the folded RMSNorm, and on the output projection and linear2 with
+    their masked residual that record the next norm's sums of squares."""
+    cfg = modelgen.configs()[4]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    n = 12
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, n, board_sizes=(19, 13))
+    tuned = nn.ComputeHandle(nn.ComputeContext(lm, use_fp16=True, auto_tune=True, tuner_file=str(model_dir) + "/t_c4.txt"),
+                             max_batch=n)
+    shapes = [l.split()[:8] for l in tuned.tuning()[1].splitlines() if l.strip()]
+    assert any(k[0] == "1" and k[5] == "1" for k in shapes)  # the SwiGLU GEMM
+    assert any(k[0] == "1" and k[7] == "1" for k in shapes)  # a masked residual
+    ref = _forward(nn.ComputeHandle(nn.ComputeContext(lm, use_fp16=True, auto_tune=False), max_batch=n), sp, gl)
+    for v in range(1, VARIANTS):
+        tuned.set_tuning("".join(" ".join(k) + f" {v}\n" for k in shapes))
+        out = _forward(tuned, sp, gl)
+        for k in out:
+            assert np.array_equal(out[k], ref[k]), (v, k)
