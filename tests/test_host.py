@@ -178,3 +178,15 @@ def test_hot_kernels_keep_everything_in_registers():
                 seen.add(h)
                 assert u["scratch"] == 0 and u["vgpr_spill"] == 0, (name, u)
     assert seen == set(hot), set(hot) - seen
+
+
+def test_context_config_text_rejects_a_line_without_equals(model_dir):
+    """kgn_create_context_cfg reads KataGo config lines ("key = value", '#'
+    comments, blank lines); a line with no '=' is an error, reported before
+    any device work."""
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, modelgen.configs()[0]))
+    lib = nn.host_library()
+    err = nn._errbuf()
+    ptr = lib.kgn_create_context_cfg(lm._ptr, 19, 19, 1, b"", b"# tuning\n\nhipAutoTune = false\nhipLowLatency\n", err, len(err))
+    assert not ptr
+    assert "without '='" in err.value.decode() and "hipLowLatency" in err.value.decode()
