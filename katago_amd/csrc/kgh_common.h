@@ -225,6 +225,8 @@ enum ConvVariant {
   CONV_DMA1H_128,
   CONV_DMA1H_64,
   CONV_BOARD_HALF_64,  // the one-board kernel on half a board per workgroup (two per CU), 64 output channels per tile
+  CONV_ALLK1_64,  // 1x1 fp16 kernel for small row counts: 64-row tiles, every input channel in LDS at once
+  CONV_ALLK1_32,
   CONV_VARIANT_COUNT
 };
 

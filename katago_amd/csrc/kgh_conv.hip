@@ -1520,6 +1520,103 @@ __global__ __launch_bounds__(BM / 48 * 64, BM == 384 ? 1 : 2) void conv1x1DmaKer
   storeWaveEpilogue<half_t, RB, CB, false, GLU>(acc, stage, m0 + wm * WTM, n0 + wn * WTN, M, HW, e, rowScale + wm * WTM);
 }
 
+// ---------------------------------------------------------------------------
+// 1x1 fp16 convolution for small row counts (a few boards): 64-row x BN
+// tiles, two waves per 32 output channels, each a 32 x 32 block. The whole
+// K dimension (up to 384 input channels, twelve 32-channel steps) is DMA'd
+// into LDS at once, in the DMA kernels' swizzled 64-byte rows, so a tile
+// waits on one memory round trip instead of one per step; the matrix work
+// then runs the steps in the same order as every other kernel.
+constexpr int SMALL1_BM = 64;
+constexpr int SMALL1_MAX_STEPS = 12;
+
+template<int BN, bool GLU>
+__global__ __launch_bounds__(BN / 32 * 128, 2) void conv1x1AllKKernel(const half_t* __restrict__ x, int cinStride, int cinPad,
+                                                                      int cout, const half_t* __restrict__ w, BoardGeom g,
+                                                                      ConvEpilogue<half_t> epi) {
+  constexpr int BM = SMALL1_BM;
+  constexpr int WAVES = 2 * (BN / 32);
+  constexpr int A_LOADS = BM / 16;               // wave-loads of A rows per step
+  constexpr int B_LOADS = BN / 16;
+  constexpr int LOADS = A_LOADS + B_LOADS;
+  constexpr int PER_WAVE = LOADS / WAVES;        // 3 (BN = 32) or 2 (BN = 64)
+  static_assert(PER_WAVE * WAVES == LOADS, "a step's loads split evenly over the waves");
+  static_assert(PER_WAVE * SMALL1_MAX_STEPS < 64, "every load of a wave fits the vmcnt counter");
+  constexpr int STEP_BYTES = (BM + BN) * 64;
+  __shared__ __attribute__((aligned(1024))) unsigned char buf[SMALL1_MAX_STEPS * STEP_BYTES];
+  __shared__ __attribute__((aligned(16))) float stageArr[WAVES * 32 * CONV_STAGE_LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1;   // row block of 32
+  const int wn = wave >> 1;  // column block of 32
+  const int HW = g.H * g.W;
+  const int M = g.batch * HW;
+  int rowTile, colTile;
+  rowColTile(cout / BN, rowTile, colTile);
+  const int m0 = rowTile * BM;
+  const int n0 = colTile * BN;
+  float* stage = stageArr + wave * 32 * CONV_STAGE_LD;
+  const int laneRow = lane & 31;
+  const int kq = lane >> 5;
+  const int steps = cinPad / 32;
+
+  // Every step's operands: wave-load j of a step (j < A_LOADS: A rows 16 j..,
+  // else weight rows 16 (j - A_LOADS)..) is issued by wave j % WAVES. Rows
+  // past M read row M - 1 and are never stored.
+  const int dRow = lane >> 2;
+  const int dGroup = dmaLogicalGroup(lane);
+  for(int st = 0; st < steps; st++) {
+    unsigned char* dst = buf + st * STEP_BYTES;
+#pragma unroll
+    for(int i = 0; i < PER_WAVE; i++) {
+      const int j = wave + WAVES * i;
+      const half_t* src;
+      if(j < A_LOADS) {
+        int gm = m0 + 16 * j + dRow;
+        gm = gm < M ? gm : M - 1;
+        src = x + (size_t)gm * cinStride + st * 32 + dGroup * 8;
+      }
+      else {
+        src = w + (size_t)(n0 + 16 * (j - A_LOADS) + dRow) * cinPad + st * 32 + dGroup * 8;
+      }
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void_t*)(dst + j * 1024), 16, 0, 0);
+    }
+  }
+  // The residual (if any) starts the accumulators, as in the other kernels;
+  // its loads overlap the DMA (the stage is not a DMA target).
+  const bool resInAcc = epi.residual != nullptr && !epi.maskResidualAdd;
+  floatx16 acc[1][1];
+  if(resInAcc) {
+    residualToAcc<half_t, 1, 1>(acc, epi.residual, epi.ldRes, m0 + wm * 32, n0 + wn * 32, M, stage);
+  }
+  else {
+#pragma unroll
+    for(int r = 0; r < 16; r++) acc[0][0][r] = 0.0f;
+  }
+  waitVmcnt<0>();
+  __syncthreads();
+
+  const int aOff0 = swizzled(wm * 32 + laneRow, kq);
+  const int aOff1 = swizzled(wm * 32 + laneRow, 2 + kq);
+  const int bOff0 = BM * 64 + swizzled(wn * 32 + laneRow, kq);
+  const int bOff1 = BM * 64 + swizzled(wn * 32 + laneRow, 2 + kq);
+  for(int st = 0; st < steps; st++) {
+    const unsigned char* src = buf + st * STEP_BYTES;
+    const half8_t a0 = *(const half8_t*)(src + aOff0);
+    const half8_t b0 = *(const half8_t*)(src + bOff0);
+    const half8_t a1 = *(const half8_t*)(src + aOff1);
+    const half8_t b1 = *(const half8_t*)(src + bOff1);
+    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[0][0], 0, 0, 0);
+    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, acc[0][0], 0, 0, 0);
+  }
+
+  ConvEpilogue<half_t> e = epi;
+  if(resInAcc) e.residual = nullptr;
+  storeWaveEpilogue<half_t, 1, 1, false, GLU>(acc, stage, m0 + wm * 32, n0 + wn * 32, M, HW, e);
+}
+
 // Direct convolution: one thread per output element. Used for shapes the
 // matrix-core kernel does not take (tiny channel counts, 5x5, dilation-free
 // odd kernels), in particular the layer-level known-answer tests.
@@ -1695,6 +1792,22 @@ bool dma1x1Fits(int cinStride, int cinPad, int cout, int bn, BoardGeom g) {
   return cinPad % 32 == 0 && cinStride % 8 == 0 && cout % bn == 0 && M * cinStride < (1L << 31) && (long)cout * cinPad < (1L << 31);
 }
 
+// The whole-K 1x1 kernel: at most twelve 32-channel steps (384 input
+// channels) held in LDS.
+bool allK1x1Fits(int cinStride, int cinPad, int cout, int bn, BoardGeom g) {
+  return dma1x1Fits(cinStride, cinPad, cout, bn, g) && cinPad <= 32 * SMALL1_MAX_STEPS;
+}
+
+template<int BN>
+void launch1x1AllK(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                   const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  const int M = g.batch * g.H * g.W;
+  dim3 grid((M + SMALL1_BM - 1) / SMALL1_BM * (cout / BN)), block(BN / 32 * 128);
+  if(epi.glu) hipLaunchKernelGGL((conv1x1AllKKernel<BN, true>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  else hipLaunchKernelGGL((conv1x1AllKKernel<BN, false>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  KGH_CHECK_LAUNCH();
+}
+
 // The 1x1 DMA kernel: fp16, 32-channel steps, enough 384-row x BN tiles
 // (about 128 or more), 32-bit element offsets.
 template<typename T>
@@ -1710,9 +1823,21 @@ bool dispatch1x1Dma<half_t>(const half_t* x, int cinStride, int cinPad, int cout
   // Too few 384-row tiles to fill most CUs: from 24 tiles of 192 rows, the
   // 192-row kernel with 64-column tiles (two workgroups per CU; the tuner
   // picks it for b18c384nbt's 1x1 convs at 16 to 64 boards, 12-20 us vs
-  // 18-24 us on the 128-row tile kernel); below that, the tile kernel.
+  // 18-24 us on the 128-row tile kernel). Below that, the whole-K kernel
+  // (one memory round trip per tile; C2's net at 1-8 boards: forwards
+  // 0.09-0.12 ms shorter than on the 128-row tile kernel), with 32-column
+  // tiles while 64-column ones would give fewer than 64 workgroups; else
+  // the tile kernel.
   if((M + TW_BM - 1) / TW_BM * (cout / 64) < 3 * 128) {
-    if(M < 24L * 192 || cout % 64 != 0) return false;
+    if(M < 24L * 192) {
+      if(!allK1x1Fits(cinStride, cinPad, cout, 32, g)) return false;
+      if(cout % 64 == 0 && (M + SMALL1_BM - 1) / SMALL1_BM * (cout / 64) >= 64)
+        launch1x1AllK<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      else
+        launch1x1AllK<32>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      return true;
+    }
+    if(cout % 64 != 0) return false;
     launch1x1Dma<64, 192>(x, cinStride, cinPad, cout, w, g, epi, stream);
     return true;
   }
@@ -1747,6 +1872,8 @@ bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g
       if(v == CONV_DMA1H_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
       if(v == CONV_DMA1H_128) return dma1x1Fits(cinStride, cinPad, cout, 128, g);
       if(v == CONV_DMA1H_64) return dma1x1Fits(cinStride, cinPad, cout, 64, g);
+      if(v == CONV_ALLK1_64) return allK1x1Fits(cinStride, cinPad, cout, 64, g);
+      if(v == CONV_ALLK1_32) return allK1x1Fits(cinStride, cinPad, cout, 32, g);
     }
   }
   else {
@@ -1785,6 +1912,8 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
       case CONV_BOARD_128: launchBoardWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_64: launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_HALF_64: launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_ALLK1_64: launch1x1AllK<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_ALLK1_32: launch1x1AllK<32>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_192: launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_128: launch1x1Dma<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_64: launch1x1Dma<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
@@ -1834,7 +1963,7 @@ bool convMfmaSupported(int cinPad, int cout) {
 const char* convVariantName(int variant) {
   static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
                                 "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64",
-                                "dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "boardhalf64"};
+                                "dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "boardhalf64", "allk1x1_64", "allk1x1_32"};
   return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
 }
 

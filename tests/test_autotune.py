@@ -100,11 +100,12 @@ def test_every_kernel_variant_gives_identical_bits(model_dir, fp16):
             assert np.array_equal(out[k], ref[k]), (v, k)
 
 
-@pytest.mark.parametrize("variant", [16, 17, 18], ids=["dma1x1h_192", "dma1x1h_128", "dma1x1h_64"])
+@pytest.mark.parametrize("variant", [16, 17, 18, 20, 21], ids=["dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "allk1x1_64", "allk1x1_32"])
 def test_half_height_1x1_variants_give_identical_bits_on_nbt(model_dir, variant):
-    """The 192-row 1x1 kernels on C2's nested-bottleneck shapes, including
-    the post 1x1 conv whose residual is loaded into the accumulators through
-    the stage that shares the A buffers: bitwise the built-in outputs."""
+    """The 192-row 1x1 kernels and the whole-K small-batch 1x1 kernels on
+    C2's nested-bottleneck shapes, including the post 1x1 conv whose residual
+    is loaded into the accumulators (through the stage that shares the A
+    buffers in the 192-row kernel): bitwise the built-in outputs."""
     cfg = modelgen.configs()[2]
     lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
     n = 12  # batches of 8 boards or fewer are not tuned
