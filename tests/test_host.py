@@ -169,8 +169,9 @@ def test_hot_kernels_keep_everything_in_registers():
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "katago_amd", "lib", "kernel_resources.json")
     with open(path) as f:
         usage = json.load(f)
-    hot = ("convBoardWindowKernel", "convTapWindowKernel", "conv1x1DmaKernel", "convMfmaKernel", "flashAttentionKernel", "poolVecKernel", "headVectorKernel",
-           "bnActVecKernel", "rmsNormRowKernel", "headSpatialKernel")
+    hot = ("convBoardWindowKernel", "convTapWindowKernel", "conv1x1DmaKernel", "conv1x1AllKKernel", "convMfmaKernel", "flashAttentionKernel",
+           "poolVecKernel", "headVectorKernel", "bnActVecKernel", "rmsNormRowKernel", "headSpatialKernel", "gpoolBiasActKernel",
+           "splitKEpilogueKernel")
     seen = set()
     for name, u in usage.items():
         for h in hot:
