@@ -903,14 +903,29 @@ struct Runner {
       e1.outRaw = qkv;
       e1.ldRaw = qkvC;
       e1.rawEnd = INT_MAX;
-      normedInputConv(b, Rd, C, xn, e1, sqIn);
       const float* cosT = nullptr;
       const float* sinT = nullptr;
       if(b.ropeIndex >= 0) {
         if(h == nullptr) throw KghError(KGH_ERR_INTERNAL, "rotary embedding needs a handle");
         cosT = h->ropeCos[b.ropeIndex];
         sinT = h->ropeSin[b.ropeIndex];
+        // Rotate Q and K in the GEMM's epilogue where it can; attention then
+        // reads them as stored.
+        ConvEpilogue<T> t = e1;
+        t.ropeCos = cosT;
+        t.ropeSin = sinT;
+        t.ropeEnd = qC + kC;
+        t.ropeQC = qC;
+        t.ropeDq = b.dq;
+        t.ropeGroup = b.heads / b.kvHeads;
+        t.ropeLearnable = b.learnableRope ? 1 : 0;
+        if(b.heads % b.kvHeads == 0 && kgh::convRopeOk<T>(C, b.qkv.cinPad, b.qkv.cout, 1, 1, b.qkv.wPrep, t)) {
+          e1 = t;
+          cosT = nullptr;
+          sinT = nullptr;
+        }
       }
+      normedInputConv(b, Rd, C, xn, e1, sqIn);
       kgh::launchAttention<T>(qkv, qkvC, qC, qC + kC, b.heads, b.kvHeads, b.dq, b.dv, mask, HW, g.batch, att, aC, cosT, sinT,
                               b.learnableRope, s);
       ConvEpilogue<T> e2 = epi();

@@ -110,6 +110,15 @@ template<typename T> __device__ __forceinline__ T kgh_from_float(float v) { retu
 // multiple of 32), and the consumer first scales its accumulators by
 //   mask[m] / sqrt(sum_b rowNormIn[m*ldNorm + b] / normC + normEps)
 // (matrix-core kernels only).
+//
+// An attention block's [Q|K|V] GEMM can also apply the rotary embedding: the
+// raw columns below ropeEnd (the query heads, then the key heads, ropeDq
+// wide, queries below ropeQC) are rounded to T, then each pair (2p, 2p+1) of
+// a head is rotated by the angle of table t at position m % (H*W), with
+//   ropeCos/ropeSin [t][H*W][ropeDq/2], t = 0, or with ropeLearnable the kv
+//   head (query head h -> h / ropeGroup),
+// and rounded again: exactly what a separate pass over the stored Q and K
+// computes (matrix-core kernels only; ropeDq and ropeQC multiples of 16).
 template<typename T>
 struct ConvEpilogue {
   T* outRaw;
@@ -134,7 +143,43 @@ struct ConvEpilogue {
   int ldNorm;
   int normC;
   float normEps;
+  const float* ropeCos;
+  const float* ropeSin;
+  int ropeEnd;
+  int ropeQC;
+  int ropeDq;
+  int ropeGroup;
+  int ropeLearnable;
 };
+
+// One rotated pair, as the rotary-embedding kernels compute it.
+__device__ __forceinline__ void kgh_rope_pair(float x0, float x1, float c, float s, float& y0, float& y1) {
+  y0 = x0 * c - x1 * s;
+  y1 = x0 * s + x1 * c;
+}
+
+// The rotary embedding of one lane's 16 stored channels c0.. of row m (see
+// ConvEpilogue): c0 is a multiple of 16, so the 8 pairs lie in one head and
+// their table entries are contiguous.
+template<typename T>
+__device__ __forceinline__ void kgh_rope_stored(const ConvEpilogue<T>& e, int m, int HW, int c0, T (&o)[16]) {
+  const int head = c0 / e.ropeDq;
+  const int pairs = e.ropeDq >> 1;
+  const int table = !e.ropeLearnable ? 0 : c0 < e.ropeQC ? head / e.ropeGroup : head - e.ropeQC / e.ropeDq;
+  const size_t ti = ((size_t)table * HW + (m % HW)) * pairs + ((c0 - head * e.ropeDq) >> 1);
+  float cs[8], sn[8];
+  *(float4*)&cs[0] = *(const float4*)(e.ropeCos + ti);
+  *(float4*)&cs[4] = *(const float4*)(e.ropeCos + ti + 4);
+  *(float4*)&sn[0] = *(const float4*)(e.ropeSin + ti);
+  *(float4*)&sn[4] = *(const float4*)(e.ropeSin + ti + 4);
+#pragma unroll
+  for(int q = 0; q < 8; q++) {
+    float y0, y1;
+    kgh_rope_pair(kgh_to_float(o[2 * q]), kgh_to_float(o[2 * q + 1]), cs[q], sn[q], y0, y1);
+    o[2 * q] = kgh_from_float<T>(y0);
+    o[2 * q + 1] = kgh_from_float<T>(y1);
+  }
+}
 
 // The consumer row scale of a folded RMSNorm (see ConvEpilogue): the block
 // sums added in order, then 1 / sqrt(mean + eps) as the RMSNorm kernel
@@ -256,6 +301,9 @@ bool convMfmaSupported(int cinPad, int cout);
 // Whether launchConv takes the epilogue's folded-RMSNorm fields for this
 // shape (a matrix-core kernel; raw split on 32 columns; no residual where the
 // accumulators are scaled).
+// Whether epi's rotary embedding (see ConvEpilogue) can run in this conv.
+template<typename T>
+bool convRopeOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi);
 template<typename T>
 bool convNormFoldOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi);
 

@@ -116,7 +116,9 @@ __device__ __forceinline__ void storeBlockSumSq(const ConvEpilogue<T>& epi, int 
   if((c0 & 16) == 0) epi.sumSqOut[(size_t)m * epi.ldSq + (c0 >> 5)] = ss;
 }
 
-template<typename T, int BN, int WM, int ACT>
+// ROPE: the rotary-embedding mode of ConvEpilogue (raw outputs only, no
+// activated output), instantiated only in kernels that take 1x1 convs.
+template<typename T, int BN, int WM, int ACT, bool ROPE = false>
 __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / WM / 32][BN / (4 / WM) / 32], unsigned char* smem,
                                                      int m0, int n0, int M, int HW, const ConvEpilogue<T>& epi) {
   // Epilogue. For each 32-column block the wave writes its accumulators to
@@ -148,7 +150,7 @@ __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / W
 
     const int c0 = n0 + wn * WTN + cb * 32 + half * 16;  // first of this lane's 16 channels
     const bool rawCols = c0 < epi.rawEnd;                // the split points are multiples of 16
-    const bool actCols = epi.outAct != nullptr && c0 >= epi.actBegin;
+    const bool actCols = !ROPE && epi.outAct != nullptr && c0 >= epi.actBegin;
     float aS[16], aB[16];
     if(actCols && !epi.glu) {
 #pragma unroll
@@ -198,6 +200,9 @@ __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / W
           T o[16];
 #pragma unroll
           for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(v[j]);
+          if constexpr(ROPE) {
+            if(c0 < epi.ropeEnd) kgh_rope_stored(epi, m, HW, c0, o);
+          }
           uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
 #pragma unroll
           for(int q = 0; q < 16 / VEC; q++) dst[q] = ((const uint4*)o)[q];
@@ -225,9 +230,15 @@ __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / W
   }
 }
 
-template<typename T, int BN, int WM>
+template<typename T, int BN, int WM, bool ALLOW_ROPE = false>
 __device__ __forceinline__ void storeTileEpilogue(floatx16 (&acc)[CONV_BM / WM / 32][BN / (4 / WM) / 32], unsigned char* smem,
                                                   int m0, int n0, int M, int HW, const ConvEpilogue<T>& epi) {
+  if constexpr(ALLOW_ROPE) {
+    if(epi.ropeEnd > 0) {
+      storeTileEpilogueAct<T, BN, WM, KGH_ACT_IDENTITY, true>(acc, smem, m0, n0, M, HW, epi);
+      return;
+    }
+  }
   withActKind(epi.actKind, epi.outAct != nullptr, [&](auto actTag) {
     storeTileEpilogueAct<T, BN, WM, decltype(actTag)::value>(acc, smem, m0, n0, M, HW, epi);
   });
@@ -454,7 +465,9 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
 
   ConvEpilogue<T> e = epi;
   if(resInAcc) e.residual = nullptr;
-  storeTileEpilogue<T, BN, WM>(acc, smem, m0, n0, M, HW, e);
+  // (The 192-column tile has no registers to spare for the rotary mode;
+  // the dispatch keeps such epilogues off it.)
+  storeTileEpilogue<T, BN, WM, KS == 1 && BN != 192>(acc, smem, m0, n0, M, HW, e);
 }
 
 // ---------------------------------------------------------------------------
@@ -532,7 +545,7 @@ __device__ __forceinline__ void barrierNoFence() {
 // compiler from reordering the stage accesses.
 // nscLds: the folded-RMSNorm row scales of the wave's rows (row r of the
 // wave at nscLds[r]) when the kernel computed them, else null (computed here).
-template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, int ACT>
+template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, int ACT, bool ROPE = false>
 __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
                                                      const ConvEpilogue<T>& epi, const float* nscLds) {
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -553,7 +566,7 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
   for(int cb = 0; cb < CB; cb++) {
     const int c0 = nBase + cb * 32 + half * 16;  // first of this lane's 16 channels
     const bool rawCols = c0 < epi.rawEnd;        // the split points are multiples of 16
-    const bool actCols = epi.outAct != nullptr && c0 >= epi.actBegin;
+    const bool actCols = !ROPE && epi.outAct != nullptr && c0 >= epi.actBegin;
     float aS[16], aB[16];
     if(actCols && !epi.glu) {
 #pragma unroll
@@ -604,6 +617,9 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
           T o[16];
 #pragma unroll
           for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(v[j]);
+          if constexpr(ROPE) {
+            if(c0 < epi.ropeEnd) kgh_rope_stored(epi, m, HW, c0, o);
+          }
           uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
 #pragma unroll
           for(int q = 0; q < RV; q++) dst[q] = ((const uint4*)o)[q];
@@ -637,9 +653,15 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
 // branch on the kind); kernels with no registers to spare keep one body that
 // selects the activation at run time (KGH_ACT_DYNAMIC).
 constexpr int KGH_ACT_DYNAMIC = -1;
-template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, bool ACT_FIXED = true>
+template<typename T, int RB, int CB, bool RES_IN_ACC, bool GLU, bool ACT_FIXED = true, bool ALLOW_ROPE = false>
 __device__ __forceinline__ void storeWaveEpilogue(floatx16 (&acc)[RB][CB], float* stage, int mBase, int nBase, int M, int HW,
                                                   const ConvEpilogue<T>& epi, const float* nscLds = nullptr) {
+  if constexpr(ALLOW_ROPE && !GLU) {
+    if(epi.ropeEnd > 0) {
+      storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, false, KGH_ACT_IDENTITY, true>(acc, stage, mBase, nBase, M, HW, epi, nscLds);
+      return;
+    }
+  }
   if constexpr(ACT_FIXED) {
     withActKind(epi.actKind, epi.outAct != nullptr, [&](auto actTag) {
       storeWaveEpilogueAct<T, RB, CB, RES_IN_ACC, GLU, decltype(actTag)::value>(acc, stage, mBase, nBase, M, HW, epi, nscLds);
@@ -1517,7 +1539,7 @@ __global__ __launch_bounds__(BM / 48 * 64, BM == 384 ? 1 : 2) void conv1x1DmaKer
 
   ConvEpilogue<half_t> e = epi;
   if(resInAcc) e.residual = nullptr;
-  storeWaveEpilogue<half_t, RB, CB, false, GLU>(acc, stage, m0 + wm * WTM, n0 + wn * WTN, M, HW, e, rowScale + wm * WTM);
+  storeWaveEpilogue<half_t, RB, CB, false, GLU, true, true>(acc, stage, m0 + wm * WTM, n0 + wn * WTN, M, HW, e, rowScale + wm * WTM);
 }
 
 // ---------------------------------------------------------------------------
@@ -1614,7 +1636,7 @@ __global__ __launch_bounds__(BN / 32 * 128, 2) void conv1x1AllKKernel(const half
 
   ConvEpilogue<half_t> e = epi;
   if(resInAcc) e.residual = nullptr;
-  storeWaveEpilogue<half_t, 1, 1, false, GLU>(acc, stage, m0 + wm * 32, n0 + wn * 32, M, HW, e);
+  storeWaveEpilogue<half_t, 1, 1, false, GLU, true, true>(acc, stage, m0 + wm * 32, n0 + wn * 32, M, HW, e);
 }
 
 // Direct convolution: one thread per output element. Used for shapes the
@@ -1854,7 +1876,7 @@ template<typename T>
 bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g, const ConvEpilogue<T>& epi) {
   if(v >= CONV_TILE_192 && v <= CONV_TILE_32) {
     static const int bn[] = {192, 128, 96, 64, 32};
-    return cout % bn[v - CONV_TILE_192] == 0;
+    return cout % bn[v - CONV_TILE_192] == 0 && !(v == CONV_TILE_192 && epi.ropeEnd > 0);
   }
   if constexpr(std::is_same<T, half_t>::value) {
     if(ky == 3) {
@@ -1937,7 +1959,7 @@ bool dispatchMfmaTile(const T* x, int cinStride, int cinPad, int cout, const T* 
   const long rowTiles = ((long)g.batch * g.H * g.W + CONV_BM - 1) / CONV_BM;
   int bn = 0;
   for(int cand : bns) {
-    if(cout % cand != 0) continue;
+    if(cout % cand != 0 || (cand == 192 && epi.ropeEnd > 0)) continue;
     bn = cand;
     if(rowTiles * (cout / cand) >= 3L * 256) break;
   }
@@ -1992,6 +2014,13 @@ bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int 
 }
 
 template<typename T>
+bool convRopeOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi) {
+  return ky == 1 && kx == 1 && epi.outAct == nullptr && !epi.glu && mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
+         epi.ropeDq > 0 && epi.ropeDq % 16 == 0 &&
+         epi.ropeQC % 16 == 0 && epi.ropeEnd % 16 == 0 && epi.ropeGroup > 0 && epi.ropeCos != nullptr && epi.ropeSin != nullptr;
+}
+
+template<typename T>
 bool convNormFoldOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi) {
   return mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) && (epi.sumSqOut == nullptr || epi.rawEnd % 32 == 0) &&
          (epi.rowNormIn == nullptr || (epi.residual == nullptr && epi.ldNorm >= 1 && epi.ldNorm <= KGH_NORM_MAX_BLOCKS));
@@ -2002,6 +2031,8 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
                 const float* wDirect, BoardGeom g, const ConvEpilogue<T>& epi, hipStream_t stream, bool* usedMfma, int variant) {
   if((epi.sumSqOut != nullptr || epi.rowNormIn != nullptr) && !convNormFoldOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi))
     throw KghError(5, "conv: a folded RMSNorm needs the matrix-core kernels");
+  if(epi.ropeEnd > 0 && !convRopeOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi))
+    throw KghError(5, "conv: a rotary embedding in the epilogue needs the matrix-core kernels and head dims multiples of 16");
   bool done = false;
   if(variant != CONV_AUTO && convVariantApplies<T>(variant, x, cinStride, cinPad, cout, ky, kx, wPrepared, g, epi)) {
     launchVariant<T>(variant, ky, x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
@@ -2031,7 +2062,7 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
 
 bool convSplitKApplies(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, BoardGeom g,
                        const ConvEpilogue<half_t>& epi) {
-  return ky == 3 && kx == 3 && cinPad >= 64 && epi.sumSqOut == nullptr && epi.rowNormIn == nullptr &&
+  return ky == 3 && kx == 3 && cinPad >= 64 && epi.sumSqOut == nullptr && epi.rowNormIn == nullptr && epi.ropeEnd == 0 &&
          mfmaPathOk<half_t>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
          boardWindowFits(cinStride, cinPad, cout, SPLITK_BN, g, epi) && cout % 8 == 0;
 }
@@ -2080,6 +2111,8 @@ void launchConvertToFloat(const T* src, float* dst, size_t n, hipStream_t stream
   KGH_CHECK_LAUNCH();
 }
 
+template bool convRopeOk<float>(int, int, int, int, int, const void*, const ConvEpilogue<float>&);
+template bool convRopeOk<half_t>(int, int, int, int, int, const void*, const ConvEpilogue<half_t>&);
 template bool convNormFoldOk<float>(int, int, int, int, int, const void*, const ConvEpilogue<float>&);
 template bool convNormFoldOk<half_t>(int, int, int, int, int, const void*, const ConvEpilogue<half_t>&);
 template bool convMfmaSupported<float>(int, int);

@@ -192,9 +192,10 @@ __global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, c
   const float cs = cosT[((size_t)table * HW + xy) * pairs + p];
   const float sn = sinT[((size_t)table * HW + xy) * pairs + p];
   T* e = qkv + (size_t)row * ld + head * dq + 2 * p;
-  const float x0 = kgh_to_float(e[0]), x1 = kgh_to_float(e[1]);
-  e[0] = kgh_from_float<T>(x0 * cs - x1 * sn);
-  e[1] = kgh_from_float<T>(x0 * sn + x1 * cs);
+  float y0, y1;
+  kgh_rope_pair(kgh_to_float(e[0]), kgh_to_float(e[1]), cs, sn, y0, y1);
+  e[0] = kgh_from_float<T>(y0);
+  e[1] = kgh_from_float<T>(y1);
 }
 
 // ---------------------------------------------------------------------------
@@ -259,9 +260,10 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
         const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
         for(int q = 0; q < 4; q++) {
-          const float x0 = (float)v[2 * q], x1 = (float)v[2 * q + 1];
-          v[2 * q] = (half_t)(x0 * cc[q] - x1 * ss[q]);
-          v[2 * q + 1] = (half_t)(x0 * ss[q] + x1 * cc[q]);
+          float y0, y1;
+          kgh_rope_pair((float)v[2 * q], (float)v[2 * q + 1], cc[q], ss[q], y0, y1);
+          v[2 * q] = (half_t)y0;
+          v[2 * q + 1] = (half_t)y1;
         }
       }
     }
@@ -300,9 +302,10 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
       const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
       for(int q = 0; q < 4; q++) {
-        const float x0 = (float)qf[ks][2 * q], x1 = (float)qf[ks][2 * q + 1];
-        qf[ks][2 * q] = (half_t)(x0 * cc[q] - x1 * ss[q]);
-        qf[ks][2 * q + 1] = (half_t)(x0 * ss[q] + x1 * cc[q]);
+        float y0, y1;
+        kgh_rope_pair((float)qf[ks][2 * q], (float)qf[ks][2 * q + 1], cc[q], ss[q], y0, y1);
+        qf[ks][2 * q] = (half_t)y0;
+        qf[ks][2 * q + 1] = (half_t)y1;
       }
     }
   }
