@@ -917,6 +917,8 @@ struct Runner {
         t.ropeEnd = qC + kC;
         t.ropeQC = qC;
         t.ropeDq = b.dq;
+        t.ropeDqShift = 0;
+        while((1 << t.ropeDqShift) < b.dq) t.ropeDqShift++;
         t.ropeGroup = b.heads / b.kvHeads;
         t.ropeLearnable = b.learnableRope ? 1 : 0;
         if(b.heads % b.kvHeads == 0 && kgh::convRopeOk<T>(C, b.qkv.cinPad, b.qkv.cout, 1, 1, b.qkv.wPrep, t)) {

@@ -118,7 +118,8 @@ template<typename T> __device__ __forceinline__ T kgh_from_float(float v) { retu
 //   ropeCos/ropeSin [t][H*W][ropeDq/2], t = 0, or with ropeLearnable the kv
 //   head (query head h -> h / ropeGroup),
 // and rounded again: exactly what a separate pass over the stored Q and K
-// computes (matrix-core kernels only; ropeDq and ropeQC multiples of 16).
+// computes (1x1 matrix-core kernels only; ropeDq = 1 << ropeDqShift, at
+// least 16, and ropeQC a multiple of 16).
 template<typename T>
 struct ConvEpilogue {
   T* outRaw;
@@ -148,6 +149,7 @@ struct ConvEpilogue {
   int ropeEnd;
   int ropeQC;
   int ropeDq;
+  int ropeDqShift;
   int ropeGroup;
   int ropeLearnable;
 };
@@ -158,15 +160,15 @@ __device__ __forceinline__ void kgh_rope_pair(float x0, float x1, float c, float
   y1 = x0 * s + x1 * c;
 }
 
-// The rotary embedding of one lane's 16 stored channels c0.. of row m (see
-// ConvEpilogue): c0 is a multiple of 16, so the 8 pairs lie in one head and
-// their table entries are contiguous.
+// The rotary embedding of one lane's 16 stored channels c0.. of a row at
+// board position xy (see ConvEpilogue): c0 is a multiple of 16, so the 8
+// pairs lie in one head and their table entries are contiguous.
 template<typename T>
-__device__ __forceinline__ void kgh_rope_stored(const ConvEpilogue<T>& e, int m, int HW, int c0, T (&o)[16]) {
-  const int head = c0 / e.ropeDq;
+__device__ __forceinline__ void kgh_rope_stored(const ConvEpilogue<T>& e, int xy, int HW, int c0, T (&o)[16]) {
+  const int head = c0 >> e.ropeDqShift;
   const int pairs = e.ropeDq >> 1;
-  const int table = !e.ropeLearnable ? 0 : c0 < e.ropeQC ? head / e.ropeGroup : head - e.ropeQC / e.ropeDq;
-  const size_t ti = ((size_t)table * HW + (m % HW)) * pairs + ((c0 - head * e.ropeDq) >> 1);
+  const int table = !e.ropeLearnable ? 0 : c0 < e.ropeQC ? head / e.ropeGroup : head - (e.ropeQC >> e.ropeDqShift);
+  const size_t ti = ((size_t)table * HW + xy) * pairs + ((c0 & (e.ropeDq - 1)) >> 1);
   float cs[8], sn[8];
   *(float4*)&cs[0] = *(const float4*)(e.ropeCos + ti);
   *(float4*)&cs[4] = *(const float4*)(e.ropeCos + ti + 4);

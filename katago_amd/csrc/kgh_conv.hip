@@ -201,7 +201,7 @@ __device__ __forceinline__ void storeTileEpilogueAct(floatx16 (&acc)[CONV_BM / W
 #pragma unroll
           for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(v[j]);
           if constexpr(ROPE) {
-            if(c0 < epi.ropeEnd) kgh_rope_stored(epi, m, HW, c0, o);
+            if(c0 < epi.ropeEnd) kgh_rope_stored(epi, m % HW, HW, c0, o);
           }
           uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
 #pragma unroll
@@ -556,10 +556,12 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
   const int lrow = lane >> 1;  // 0..31
   float msk[RB];
   float nsc[RB];  // folded RMSNorm row scales, once per row
+  int xyR[RB];    // board positions of the rows (rotary mode)
 #pragma unroll
   for(int rb = 0; rb < RB; rb++) {
     const int m = mBase + rb * 32 + lrow;
     msk[rb] = m < M ? epi.mask[m] : 0.0f;
+    xyR[rb] = ROPE ? m % HW : 0;
     nsc[rb] = epi.rowNormIn == nullptr || m >= M ? 0.0f : nscLds != nullptr ? nscLds[rb * 32 + lrow] : kgh_row_norm_scale(epi, m, msk[rb]);
   }
 #pragma unroll
@@ -618,7 +620,7 @@ __device__ __forceinline__ void storeWaveEpilogueAct(floatx16 (&acc)[RB][CB], fl
 #pragma unroll
           for(int j = 0; j < 16; j++) o[j] = kgh_from_float<T>(v[j]);
           if constexpr(ROPE) {
-            if(c0 < epi.ropeEnd) kgh_rope_stored(epi, m, HW, c0, o);
+            if(c0 < epi.ropeEnd) kgh_rope_stored(epi, xyR[rb], HW, c0, o);
           }
           uint4* dst = (uint4*)(epi.outRaw + (size_t)m * epi.ldRaw + c0);
 #pragma unroll
@@ -2016,7 +2018,7 @@ bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int 
 template<typename T>
 bool convRopeOk(int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared, const ConvEpilogue<T>& epi) {
   return ky == 1 && kx == 1 && epi.outAct == nullptr && !epi.glu && mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
-         epi.ropeDq > 0 && epi.ropeDq % 16 == 0 &&
+         epi.ropeDq >= 16 && epi.ropeDq == (1 << epi.ropeDqShift) &&
          epi.ropeQC % 16 == 0 && epi.ropeEnd % 16 == 0 && epi.ropeGroup > 0 && epi.ropeCos != nullptr && epi.ropeSin != nullptr;
 }
 
