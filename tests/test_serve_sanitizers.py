@@ -1,6 +1,6 @@
 """The NNEvaluator batching server loop (nneval.cpp) built with
 ThreadSanitizer, and with AddressSanitizer + UndefinedBehaviorSanitizer,
-host code only (g++, no device code), and driven by tests/tsan/serve_stress.cpp:
+host code only (g++, no device code), and driven by tests/sanitize/serve_stress.cpp:
 three server threads in debugSkipNeuralNet mode, twelve client threads,
 servers killed and respawned between rounds. The reference's serve loop is
 nneval.cpp:342-420, 549-750."""
@@ -11,8 +11,8 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SOURCES = [
-    os.path.join(ROOT, "tests", "tsan", "serve_stress.cpp"),
-    os.path.join(ROOT, "tests", "tsan", "nninterface_stub.cpp"),
+    os.path.join(ROOT, "tests", "sanitize", "serve_stress.cpp"),
+    os.path.join(ROOT, "tests", "sanitize", "nninterface_stub.cpp"),
     os.path.join(ROOT, "katago_amd", "host", "neuralnet", "nneval.cpp"),
     os.path.join(ROOT, "katago_amd", "host", "core", "global.cpp"),
 ]
