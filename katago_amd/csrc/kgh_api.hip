@@ -992,9 +992,23 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
   hipStream_t s = h->stream;
   const int HW = h->H * h->W;
 
-  kgh::launchPackInputs<T>(dSpatial, dSym, n, h->H, h->W, net.inputC, (T*)h->x0, net.inputCPad, h->mask, h->maskSum, s);
-  kgh::launchRowMatmul(dGlobal, net.globalC, net.globalC, net.initialMatMul.w, net.trunkC, nullptr, KGH_ACT_IDENTITY, h->gbias,
-                       net.trunkC, n, s);
+  PrepareBoardsArgs<T> pa;
+  pa.spatial = dSpatial;
+  pa.sym = dSym;
+  pa.H = h->H;
+  pa.W = h->W;
+  pa.cin = net.inputC;
+  pa.x = (T*)h->x0;
+  pa.cinPad = net.inputCPad;
+  pa.mask = h->mask;
+  pa.maskSum = h->maskSum;
+  pa.global = dGlobal;
+  pa.ldGlobal = net.globalC;
+  pa.globalC = net.globalC;
+  pa.Wg = net.initialMatMul.w;
+  pa.cout = net.trunkC;
+  pa.gbias = h->gbias;
+  kgh::launchPrepareBoards<T>(pa, n, s);
 
   // Stem: R0 = conv(x) + globalBias[n]; A0 = first block's preBN activation.
   bool stemSq = false;

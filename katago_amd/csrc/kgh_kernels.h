@@ -122,11 +122,34 @@ struct PostArgs {
   int batch;
 };
 
+// Inputs of the per-board preparation kernel: spatial[batch][H*W][cin] fp32
+// rows and sym[batch] in; x[batch*H*W][cinPad], mask[batch*H*W],
+// maskSum[batch] and (when Wg is set) gbias[batch][cout] = global W out.
+template<typename T>
+struct PrepareBoardsArgs {
+  const float* spatial;
+  const int* sym;
+  int H;
+  int W;
+  int cin;
+  T* x;
+  int cinPad;
+  float* mask;
+  float* maskSum;
+  const float* global;
+  int ldGlobal;
+  int globalC;
+  const float* Wg;  // [globalC][cout], or null
+  int cout;
+  float* gbias;
+};
+
 namespace kgh {
 
+// Per-board input preparation (one launch): rows packed with the symmetry
+// applied, the on-board mask and its sum, and the stem's global-input bias.
 template<typename T>
-void launchPackInputs(const float* spatial, const int* sym, int batch, int H, int W, int cin, T* x, int cinPad, float* mask,
-                      float* maskSum, hipStream_t stream);
+void launchPrepareBoards(const PrepareBoardsArgs<T>& a, int batch, hipStream_t stream);
 
 void launchRowMatmul(const float* in, int ldIn, int cin, const float* Wt, int cout, const float* bias, int act, float* out,
                      int ldOut, int batch, hipStream_t stream);

@@ -32,60 +32,80 @@ __device__ __forceinline__ void symDest(int h, int w, int H, int W, int sym, boo
   }
 }
 
-// VEC_ROW: cin even, cinPad <= 64 and cinPad * sizeof(T) a multiple of 16.
+// The input rows of one board and what the trunk needs from them besides:
+// workgroup n packs board n's H*W rows (row p of the batch goes to the
+// symmetry's destination position, fp32 -> T, channels padded with zeros to
+// cinPad), records the on-board mask from plane 0 with its sum, and computes
+// the stem's global-input bias row gbias[n][co] = sum_i global[n][i] W[i][co]
+// (the four-accumulator order of rowMatmulKernel). One launch instead of
+// three. VEC_ROW: cin even, cinPad <= 64 and cinPad * sizeof(T) a multiple
+// of 16.
+constexpr int PREP_MAX_THREADS = 1024;
 template<typename T, bool VEC_ROW>
-__global__ void packInputsKernel(const float* __restrict__ spatial, const int* __restrict__ sym, int batch, int H, int W,
-                                 int cin, T* __restrict__ x, int cinPad, float* __restrict__ mask) {
-  int HW = H * W;
-  int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if(idx >= batch * HW) return;
-  int n = idx / HW;
-  int s = idx - n * HW;
-  int h = s / W;
-  int w = s - h * W;
-  int hd, wd;
-  symDest(h, w, H, W, sym[n], false, hd, wd);
-  int md = n * HW + hd * W + wd;
-  const float* src = spatial + (size_t)idx * cin;
-  T* dst = x + (size_t)md * cinPad;
-  if(VEC_ROW) {
-    // The padded row built in registers: float2 loads (rows start on 8-byte
-    // boundaries when cin is even), 16-byte stores (cinPad * sizeof(T) is a
-    // multiple of 16).
-    constexpr int MAXC = 64;
-    T row[MAXC];
+__global__ __launch_bounds__(PREP_MAX_THREADS) void prepareBoardsKernel(PrepareBoardsArgs<T> a) {
+  const int n = blockIdx.x;
+  const int HW = a.H * a.W;
+  const int nt = blockDim.x;
+  float onBoard = 0.0f;
+  for(int s = threadIdx.x; s < HW; s += nt) {
+    const int h = s / a.W;
+    const int w = s - h * a.W;
+    int hd, wd;
+    symDest(h, w, a.H, a.W, a.sym[n], false, hd, wd);
+    const int md = n * HW + hd * a.W + wd;
+    const float* src = a.spatial + ((size_t)n * HW + s) * a.cin;
+    T* dst = a.x + (size_t)md * a.cinPad;
+    if constexpr(VEC_ROW) {
+      // The padded row built in registers: float2 loads (rows start on
+      // 8-byte boundaries when cin is even), 16-byte stores.
+      constexpr int MAXC = 64;
+      T row[MAXC];
 #pragma unroll
-    for(int c2 = 0; c2 < MAXC / 2; c2++) {
-      float2 v = make_float2(0.0f, 0.0f);
-      if(2 * c2 < cin) v = *(const float2*)(src + 2 * c2);
-      row[2 * c2] = (T)v.x;
-      row[2 * c2 + 1] = (T)v.y;
+      for(int c2 = 0; c2 < MAXC / 2; c2++) {
+        float2 v = make_float2(0.0f, 0.0f);
+        if(2 * c2 < a.cin) v = *(const float2*)(src + 2 * c2);
+        row[2 * c2] = (T)v.x;
+        row[2 * c2 + 1] = (T)v.y;
+      }
+      constexpr int PER16 = 16 / (int)sizeof(T);
+#pragma unroll
+      for(int q = 0; q < MAXC / PER16; q++)
+        if(q * PER16 < a.cinPad) *(uint4*)(dst + q * PER16) = *(const uint4*)(row + q * PER16);
     }
-    constexpr int PER16 = 16 / (int)sizeof(T);
-#pragma unroll
-    for(int q = 0; q < MAXC / PER16; q++)
-      if(q * PER16 < cinPad) *(uint4*)(dst + q * PER16) = *(const uint4*)(row + q * PER16);
-    mask[md] = src[0];
+    else {
+      for(int c = 0; c < a.cin; c++) dst[c] = (T)src[c];
+      for(int c = a.cin; c < a.cinPad; c++) dst[c] = (T)0.0f;
+    }
+    a.mask[md] = src[0];
+    onBoard += src[0];
   }
-  else {
-    for(int c = 0; c < cin; c++) dst[c] = (T)src[c];
-    for(int c = cin; c < cinPad; c++) dst[c] = (T)0.0f;
-    mask[md] = src[0];
+  // The mask sum: within each wave by xor shuffles, then the waves in order
+  // (exact for 0/1 masks, whatever the order).
+  __shared__ float waveSums[PREP_MAX_THREADS / 64];
+  for(int off = 32; off > 0; off >>= 1) onBoard += __shfl_xor(onBoard, off);
+  if((threadIdx.x & 63) == 0) waveSums[threadIdx.x >> 6] = onBoard;
+  // Global-input bias row.
+  if(a.Wg != nullptr) {
+    const float* gx = a.global + (size_t)n * a.ldGlobal;
+    for(int co = threadIdx.x; co < a.cout; co += nt) {
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+      int i = 0;
+      for(; i + 4 <= a.globalC; i += 4) {
+        a0 += gx[i] * a.Wg[(size_t)i * a.cout + co];
+        a1 += gx[i + 1] * a.Wg[(size_t)(i + 1) * a.cout + co];
+        a2 += gx[i + 2] * a.Wg[(size_t)(i + 2) * a.cout + co];
+        a3 += gx[i + 3] * a.Wg[(size_t)(i + 3) * a.cout + co];
+      }
+      for(; i < a.globalC; i++) a0 += gx[i] * a.Wg[(size_t)i * a.cout + co];
+      a.gbias[(size_t)n * a.cout + co] = (a0 + a1) + (a2 + a3);
+    }
   }
-}
-
-__global__ void maskSumKernel(const float* __restrict__ mask, int HW, float* __restrict__ maskSum) {
-  __shared__ float part[256];
-  int n = blockIdx.x;
-  float s = 0.0f;
-  for(int i = threadIdx.x; i < HW; i += blockDim.x) s += mask[(size_t)n * HW + i];
-  part[threadIdx.x] = s;
   __syncthreads();
-  for(int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
-    if((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
-    __syncthreads();
+  if(threadIdx.x == 0) {
+    float t = 0.0f;
+    for(int wv = 0; wv < nt / 64; wv++) t += waveSums[wv];
+    a.maskSum[n] = t;
   }
-  if(threadIdx.x == 0) maskSum[n] = part[0];
 }
 
 // out[n, co] = act(sum_i in[n, i] * W[i, co] + bias[co]); W ic-major.
@@ -848,19 +868,16 @@ __global__ __launch_bounds__(256) void postprocessKernel(PostArgs a) {
 namespace kgh {
 
 template<typename T>
-void launchPackInputs(const float* spatial, const int* sym, int batch, int H, int W, int cin, T* x, int cinPad, float* mask,
-                      float* maskSum, hipStream_t stream) {
-  int total = batch * H * W;
-  const bool vecRow = cin % 2 == 0 && cinPad <= 64 && (cinPad * sizeof(T)) % 16 == 0 && ((uintptr_t)spatial & 7) == 0 &&
-                      ((uintptr_t)x & 15) == 0;
+void launchPrepareBoards(const PrepareBoardsArgs<T>& a, int batch, hipStream_t stream) {
+  if(a.cinPad < a.cin || a.cin < 1) throw KghError(5, "input packing: channel padding smaller than the channels");
+  const bool vecRow = a.cin % 2 == 0 && a.cinPad <= 64 && (a.cinPad * sizeof(T)) % 16 == 0 && ((uintptr_t)a.spatial & 7) == 0 &&
+                      ((uintptr_t)a.x & 15) == 0;
+  // One thread per position (whole wavefronts, at most 1024 threads).
+  const int threads = std::min(PREP_MAX_THREADS, std::max(64, (a.H * a.W + 63) / 64 * 64));
   if(vecRow)
-    hipLaunchKernelGGL((packInputsKernel<T, true>), dim3((total + 255) / 256), dim3(256), 0, stream, spatial, sym, batch, H, W, cin, x,
-                       cinPad, mask);
+    hipLaunchKernelGGL((prepareBoardsKernel<T, true>), dim3(batch), dim3(threads), 0, stream, a);
   else
-    hipLaunchKernelGGL((packInputsKernel<T, false>), dim3((total + 255) / 256), dim3(256), 0, stream, spatial, sym, batch, H, W, cin,
-                       x, cinPad, mask);
-  KGH_CHECK_LAUNCH();
-  hipLaunchKernelGGL(maskSumKernel, dim3(batch), dim3(256), 0, stream, mask, H * W, maskSum);
+    hipLaunchKernelGGL((prepareBoardsKernel<T, false>), dim3(batch), dim3(threads), 0, stream, a);
   KGH_CHECK_LAUNCH();
 }
 
@@ -1024,7 +1041,7 @@ void launchPostprocess(const PostArgs& a, hipStream_t stream) {
 }
 
 #define KGH_INSTANTIATE(T)                                                                                                  \
-  template void launchPackInputs<T>(const float*, const int*, int, int, int, int, T*, int, float*, float*, hipStream_t);     \
+  template void launchPrepareBoards<T>(const PrepareBoardsArgs<T>&, int, hipStream_t);                                    \
   template void launchPool<T>(const T*, int, int, const float*, const float*, int, int, bool, float*, int, const float*, int, \
                               float*, int, hipStream_t);                                                                     \
   template void launchBnAct<T>(const T*, int, T*, int, int, const float*, const float*, int, const float*, const float*, int, \
