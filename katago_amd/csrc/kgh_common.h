@@ -274,6 +274,7 @@ enum ConvVariant {
   CONV_BOARD_HALF_64,  // the one-board kernel on half a board per workgroup (two per CU), 64 output channels per tile
   CONV_ALLK1_64,  // 1x1 fp16 kernel for small row counts: 64-row tiles, every input channel in LDS at once
   CONV_ALLK1_32,
+  CONV_DMA1_256_GLU,  // 1x1 fp16 DMA kernel, 384 x 256 tiles, gated (SwiGLU) epilogue only
   CONV_VARIANT_COUNT
 };
 

@@ -1800,6 +1800,18 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
   return true;
 }
 
+// 384 x 256 tiles for gated (SwiGLU) convs only: at 256 columns the
+// accumulators, fragments and the gated epilogue fit the 256 registers of a
+// lane (the ungated epilogues would spill), and the LDS holds 157.5 KB.
+void launch1x1DmaGlu256(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
+                        const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  if(!epi.glu || cout % 256 != 0) throw KghError(5, "256-column 1x1 kernel: gated convs with a multiple of 256 columns only");
+  const int M = g.batch * g.H * g.W;
+  dim3 grid((M + 383) / 384 * (cout / 256)), block(512);
+  hipLaunchKernelGGL((conv1x1DmaKernel<256, true, 384>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  KGH_CHECK_LAUNCH();
+}
+
 template<int BN, int BM = 384>
 void launch1x1Dma(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                   const ConvEpilogue<half_t>& epi, hipStream_t stream) {
@@ -1898,6 +1910,7 @@ bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g
       if(v == CONV_DMA1H_64) return dma1x1Fits(cinStride, cinPad, cout, 64, g);
       if(v == CONV_ALLK1_64) return allK1x1Fits(cinStride, cinPad, cout, 64, g);
       if(v == CONV_ALLK1_32) return allK1x1Fits(cinStride, cinPad, cout, 32, g);
+      if(v == CONV_DMA1_256_GLU) return epi.glu && dma1x1Fits(cinStride, cinPad, cout, 256, g);
     }
   }
   else {
@@ -1944,6 +1957,7 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
       case CONV_DMA1H_192: launch1x1Dma<192, 192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1H_128: launch1x1Dma<128, 192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1H_64: launch1x1Dma<64, 192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_DMA1_256_GLU: launch1x1DmaGlu256(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       default: break;
     }
   }
@@ -1987,7 +2001,8 @@ bool convMfmaSupported(int cinPad, int cout) {
 const char* convVariantName(int variant) {
   static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
                                 "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64",
-                                "dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "boardhalf64", "allk1x1_64", "allk1x1_32"};
+                                "dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "boardhalf64", "allk1x1_64", "allk1x1_32",
+                                "dma1x1_256glu"};
   return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
 }
 
