@@ -11,6 +11,7 @@
 
 #include <zlib.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -67,8 +68,13 @@ class ModelReader {
   }
 
   void floats(size_t n, const string& what, vector<float>& out) {
-    out.resize(n);
+    // Memory for a count the rest of the file cannot hold is never
+    // allocated: text floats take at least two bytes each (the reads fail
+    // with their usual message first), binary ones four, checked after the
+    // block header.
     if(!binary_) {
+      out.clear();
+      out.reserve(std::min(n, (data_.size() - pos_) / 2 + 1));
       for(size_t i = 0; i < n; i++) {
         string t = token(what);
         char* end = nullptr;
@@ -76,7 +82,7 @@ class ModelReader {
         if(end == t.c_str())
           throw StringError(what + ": could not read float weights. Invalid model - perhaps you are trying to load a .bin.gz model as a .txt.gz model?");
         checkFinite(v, what);
-        out[i] = v;
+        out.push_back(v);
       }
       return;
     }
@@ -91,8 +97,9 @@ class ModelReader {
     if(pos_ + 4 > data_.size() || data_.compare(pos_, 4, "BIN@") != 0)
       throw StringError(what + ": did not find expected header for binary float block");
     pos_ += 4;
-    if(pos_ + n * 4 > data_.size())
+    if(n > (data_.size() - pos_) / 4)
       throw StringError(what + ": did not find the expected number of floats in binary float block");
+    out.resize(n);
     for(size_t i = 0; i < n; i++) {
       const unsigned char* b = (const unsigned char*)data_.data() + pos_ + 4 * i;
       uint32_t bits = (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) | ((uint32_t)b[3] << 24);
