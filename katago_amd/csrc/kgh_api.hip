@@ -517,8 +517,6 @@ struct kgh_handle {
   float* pass = nullptr;
   float* value = nullptr;
   float* score = nullptr;
-  float* policyRaw = nullptr;
-  float* ownRaw = nullptr;
 
   // staging for host-memory forwards
   float* dSpatial = nullptr;
@@ -1127,27 +1125,17 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
   hs.p2W = net.p2W;
   hs.ownW = net.ownW;
   hs.mask = h->mask;
-  hs.policy = h->policyRaw;
-  hs.ownership = h->ownRaw;
+  hs.sym = dSym;
+  hs.optimism = dOpt;
+  hs.pass = h->pass;
+  hs.value = h->value;
+  hs.score = h->score;
+  hs.scoreC = net.scoreC;
+  hs.mixOptimism = (net.policyC == 2 || (net.policyC == 4 && net.modelVersion >= 16)) ? 1 : 0;
+  hs.W = h->W;
+  hs.rowFloats = h->rowFloats;
+  hs.out = dOut;
   kgh::launchHeadSpatial<T>(hs, s);
-
-  UnpackArgs ua;
-  ua.policy = h->policyRaw;
-  ua.pass = h->pass;
-  ua.value = h->value;
-  ua.score = h->score;
-  ua.ownership = h->ownRaw;
-  ua.sym = dSym;
-  ua.optimism = dOpt;
-  ua.policyC = net.policyC;
-  ua.scoreC = net.scoreC;
-  ua.mixOptimism = (net.policyC == 2 || (net.policyC == 4 && net.modelVersion >= 16)) ? 1 : 0;
-  ua.batch = n;
-  ua.H = h->H;
-  ua.W = h->W;
-  ua.rowFloats = h->rowFloats;
-  ua.out = dOut;
-  kgh::launchUnpackOutputs(ua, s);
 }
 
 // Runs one forward on the handle's stream. A forward whose batch size and
@@ -1414,8 +1402,6 @@ size_t carveActivations(kgh_handle* h, int maxBatch, int nn_x, int nn_y, Take&& 
   h->pass = getF(B * net.policyC);
   h->value = getF(B * 3);
   h->score = getF(B * net.scoreC);
-  h->policyRaw = getF(M * net.policyC);
-  h->ownRaw = getF(M);
   return total;
 }
 

@@ -19,8 +19,16 @@ struct HeadSpatialArgs {
   const float* p2W;   // [policyC][p1C]
   const float* ownW;  // [v1C]
   const float* mask;
-  float* policy;     // out [M][policyC]
-  float* ownership;  // out [M]
+  // The packed output rows (kgh_output_row_floats each): policy (optimism
+  // mixed) and ownership at the inverse symmetry's position, and the pass,
+  // value and score entries that headVectorKernel computed.
+  const int* sym;
+  const float* optimism;
+  const float* pass;   // [batch][policyC]
+  const float* value;  // [batch][3]
+  const float* score;  // [batch][scoreC]
+  int scoreC, mixOptimism, W, rowFloats;
+  float* out;
 };
 
 // The per-board head vectors in one launch (eigenbackend.cpp:1980-2024,
@@ -83,17 +91,6 @@ struct GpoolBiasActArgs {
   int act;
 };
 
-struct UnpackArgs {
-  const float* policy;  // [M][policyC]
-  const float* pass;    // [batch][policyC]
-  const float* value;   // [batch][3]
-  const float* score;   // [batch][scoreC]
-  const float* ownership;  // [M]
-  const int* sym;
-  const float* optimism;
-  int policyC, scoreC, mixOptimism, batch, H, W, rowFloats;
-  float* out;
-};
 
 // Post-processing of raw outputs into what NNEvaluator::evaluate returns
 // (nneval.cpp:946-1240). Per row: legal[policySize] (1 = legal),
@@ -177,7 +174,6 @@ bool headVectorApplies(const HeadVectorArgs<T>& a);
 template<typename T>
 void launchHeadVector(const HeadVectorArgs<T>& a, hipStream_t stream);
 
-void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream);
 void launchPostprocess(const PostArgs& a, hipStream_t stream);
 
 // Transformer trunk (kgh_transformer.hip).

@@ -607,8 +607,9 @@ __global__ void bnActVecKernel(const T* __restrict__ x, int ldX, T* __restrict__
 }
 
 // Per-position part of the heads: policy = p2Conv(act(p1BN(p1 + g1Bias)) * mask),
-// ownership = ownershipConv(v1). 16-byte loads of the p1 and v1 rows when the
-// channel counts and strides allow.
+// ownership = ownershipConv(v1), written straight into the packed output
+// rows. 16-byte loads of the p1 and v1 rows when the channel counts and
+// strides allow.
 template<typename T, int ACT>
 __global__ void headSpatialKernel(HeadSpatialArgs<T> a) {
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -645,9 +646,6 @@ __global__ void headSpatialKernel(HeadSpatialArgs<T> a) {
         if(pc < a.policyC) pol[pc] += act * a.p2W[(size_t)pc * a.p1C + c];
     }
   }
-#pragma unroll
-  for(int pc = 0; pc < MAX_PC; pc++)
-    if(pc < a.policyC) a.policy[(size_t)m * a.policyC + pc] = pol[pc];
   const T* v1 = a.v1 + (size_t)m * a.ldV1;
   float own = 0.0f;
   if(vec) {
@@ -661,33 +659,24 @@ __global__ void headSpatialKernel(HeadSpatialArgs<T> a) {
   else {
     for(int c = 0; c < a.v1C; c++) own += kgh_to_float(v1[c]) * a.ownW[c];
   }
-  a.ownership[m] = own;
-}
-
-// Packs the per-row outputs with policy optimism mixing and inverse symmetry
-// (eigenbackend.cpp:2527-2580).
-__global__ void unpackOutputsKernel(UnpackArgs a) {
-  int HW = a.H * a.W;
-  int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if(idx >= a.batch * HW) return;
-  int n = idx / HW;
-  int s = idx - n * HW;
-  int h = s / a.W;
-  int w = s - h * a.W;
+  // The output row (eigenbackend.cpp:2527-2580): policy with the optimism
+  // mix and ownership at the inverse symmetry's position; position 0 of each
+  // board also writes the pass, value and score entries.
+  const int s = m - n * a.HW;
+  const int h = s / a.W;
+  const int w = s - h * a.W;
   int hd, wd;
-  symDest(h, w, a.H, a.W, a.sym[n], true, hd, wd);
-  int sd = hd * a.W + wd;
+  symDest(h, w, a.HW / a.W, a.W, a.sym[n], true, hd, wd);
+  const int sd = hd * a.W + wd;
   float* row = a.out + (size_t)n * a.rowFloats;
-  const float* pol = a.policy + (size_t)idx * a.policyC;
-  float opt = a.optimism[n];
-  float p = a.mixOptimism ? pol[0] + (pol[1] - pol[0]) * opt : pol[0];
-  row[sd] = p;
-  row[HW + 1 + 3 + a.scoreC + sd] = a.ownership[idx];
+  const float opt = a.optimism[n];
+  row[sd] = a.mixOptimism ? pol[0] + (pol[1] - pol[0]) * opt : pol[0];
+  row[a.HW + 1 + 3 + a.scoreC + sd] = own;
   if(s == 0) {
     const float* pass = a.pass + (size_t)n * a.policyC;
-    row[HW] = a.mixOptimism ? pass[0] + (pass[1] - pass[0]) * opt : pass[0];
-    for(int i = 0; i < 3; i++) row[HW + 1 + i] = a.value[(size_t)n * 3 + i];
-    for(int i = 0; i < a.scoreC; i++) row[HW + 4 + i] = a.score[(size_t)n * a.scoreC + i];
+    row[a.HW] = a.mixOptimism ? pass[0] + (pass[1] - pass[0]) * opt : pass[0];
+    for(int i = 0; i < 3; i++) row[a.HW + 1 + i] = a.value[(size_t)n * 3 + i];
+    for(int i = 0; i < a.scoreC; i++) row[a.HW + 4 + i] = a.score[(size_t)n * a.scoreC + i];
   }
 }
 
@@ -1025,12 +1014,6 @@ void launchHeadSpatial(const HeadSpatialArgs<T>& a, hipStream_t stream) {
     case KGH_ACT_MISH_SCALE8: hipLaunchKernelGGL((headSpatialKernel<T, KGH_ACT_MISH_SCALE8>), grid, block, 0, stream, a); break;
     default: hipLaunchKernelGGL((headSpatialKernel<T, KGH_ACT_IDENTITY>), grid, block, 0, stream, a); break;
   }
-  KGH_CHECK_LAUNCH();
-}
-
-void launchUnpackOutputs(const UnpackArgs& a, hipStream_t stream) {
-  int total = a.batch * a.H * a.W;
-  hipLaunchKernelGGL(unpackOutputsKernel, dim3((total + 255) / 256), dim3(256), 0, stream, a);
   KGH_CHECK_LAUNCH();
 }
 
