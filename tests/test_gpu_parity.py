@@ -355,6 +355,30 @@ def test_c3_full_batch_mixed_boards_rows_match_small_batch(model_dir):
     _rows_match_small_batch(h, sp, gl, [0, 1, 2, 255], label="C3 256")
 
 
+@pytest.mark.parametrize("cfg_index", [3, 4], ids=["b18c384nbt-mixed", "t12d384h6"])
+def test_rows_do_not_depend_on_batch_size(model_dir, cfg_index):
+    """One handle, batches of 1 to 256 boards that cross every built-in
+    kernel-choice boundary (the whole-K 1x1 kernel below 24 tiles of 192
+    rows, the 192- and 384-row DMA kernels, half- and whole-board 3x3
+    kernels, 64- and 192-column tiles, the tile kernels): each board's row
+    is bitwise the same in every batch that holds it."""
+    cfg = modelgen.configs()[cfg_index]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    n_max = 256 if cfg_index == 3 else 128
+    h = nn.ComputeHandle(nn.ComputeContext(lm, 19, 19, use_fp16=True), max_batch=n_max)
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, n_max, board_sizes=(9, 13, 19))
+    sym = np.arange(n_max) % 8
+    full = h.get_output(sp, gl, symmetry=sym)
+    for n in (1, 2, 5, 12, 13, 16, 17, 24, 31, 32, 48, 64, 65, 96, 127, 128, 129, 200, 255):
+        if n > n_max:
+            continue
+        out = h.get_output(sp[:n], gl[:n], symmetry=sym[:n])
+        for k in full:
+            assert np.isfinite(out[k]).all(), (n, k)
+            same = np.array_equal(out[k], full[k][:n])
+            assert same, f"batch {n} vs {n_max}, {k}: max-abs {np.abs(out[k] - full[k][:n]).max()}"
+
+
 def test_nchw_rows_match_oracle(model_dir):
     """getOutput with inputsUseNHWC = false (rows in NCHW order, as the
     OpenCL/TensorRT/Metal backends take them, setup.cpp:145)."""
