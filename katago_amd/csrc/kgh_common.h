@@ -275,6 +275,7 @@ enum ConvVariant {
   CONV_ALLK1_64,  // 1x1 fp16 kernel for small row counts: 64-row tiles, every input channel in LDS at once
   CONV_ALLK1_32,
   CONV_DMA1_256_GLU,  // 1x1 fp16 DMA kernel, 384 x 256 tiles, gated (SwiGLU) epilogue only
+  CONV_BOARD_HALF_64_T32,  // the half-board kernel with 32-row wave tiles (12 waves per workgroup)
   CONV_VARIANT_COUNT
 };
 

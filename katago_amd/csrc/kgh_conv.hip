@@ -1076,8 +1076,15 @@ __device__ __forceinline__ void splitKEpilogue8(const float* __restrict__ work, 
 // column waves, two workgroups per CU: twice the workgroups at small and
 // middle batches. Every output sums the same products in the same order as
 // with RW = 4, so the two are bitwise equal.
-template<int BN, int NB, bool SPLIT = false, int RW = BW_ROW_WAVES>
-__global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoardWindowKernel(
+//
+// WT = 32: wave tiles of 32 rows instead of 96, three times the waves (12
+// per half board) for the same work: the RW loader waves of each kind still
+// issue every DMA, the others only compute, and each SIMD holds three waves
+// to hide the per-step latencies that bound small and middle batches (LDS
+// fragment reads per matrix instruction 2 instead of 4/3). The sums are the
+// same, in the same order: bitwise equal to WT = 96.
+template<int BN, int NB, bool SPLIT = false, int RW = BW_ROW_WAVES, int WT = BW_WTM>
+__global__ __launch_bounds__(128 * RW * BW_WTM / WT, RW == BW_ROW_WAVES || WT != BW_WTM ? 1 : 2) void convBoardWindowKernel(
     const half_t* __restrict__ x, int cinStride, int cinPad, int cout, const half_t* __restrict__ w, int batch,
     ConvEpilogue<half_t> epi, float* __restrict__ work = nullptr) {
   // NB weight buffers, loaded LA = NB - 3 steps ahead: the DMA for step
@@ -1095,8 +1102,11 @@ __global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoar
   // vs 68.4 us), +8% at 8-32 boards.
   constexpr int TPB = 3;
   constexpr int WTN = BN / 2;
-  constexpr int RB = BW_WTM / 32;
+  static_assert(WT == BW_WTM || WT == 32, "wave tiles of 96 or 32 rows");
+  constexpr int RB = WT / 32;
   constexpr int CB = WTN / 32;
+  constexpr int CW = RW * BW_WTM / WT;  // row waves that compute (RW of them also load)
+  constexpr int NW = 2 * CW;
   static_assert(WTN % 32 == 0, "wave tile must be a multiple of 32 columns");
   static_assert(RW == BW_ROW_WAVES || RW == 2, "a whole board or half of one");
   constexpr int B_PER = BN / 16 / RW;
@@ -1121,20 +1131,22 @@ __global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoar
   __shared__ __attribute__((aligned(1024))) unsigned char wt8[NB > 6 ? BN * 64 : 64];
   __shared__ __attribute__((aligned(1024))) unsigned char win0[WIN_BYTES];
   __shared__ __attribute__((aligned(1024))) unsigned char win1[WIN_BYTES];
+  // The accumulator stage of the residual load and the epilogue (32 x
+  // CONV_STAGE_LD floats per wave) lives in win0 while the windows are idle,
+  // or, when the waves' stages do not fit there, in an array of its own.
+  constexpr int STAGE_BYTES = 32 * CONV_STAGE_LD * 4;
+  constexpr bool OWN_STAGE = NW * STAGE_BYTES > WIN_BYTES;
+  __shared__ __attribute__((aligned(16))) float stageArr[OWN_STAGE ? NW * 32 * CONV_STAGE_LD : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // The accumulator stage of the residual load and the epilogue (32 x
-  // CONV_STAGE_LD floats per wave) lives in win0 while the windows are idle.
-  constexpr int STAGE_BYTES = 32 * CONV_STAGE_LD * 4;
-  static_assert(2 * RW * STAGE_BYTES <= WIN_BYTES, "stage fits in a window");
-  float* stage = (float*)(win0 + wave * STAGE_BYTES);
-  const int wm = wave % RW;  // row block of 96
-  const int wn = wave / RW;  // column half
+  float* stage = OWN_STAGE ? stageArr + wave * 32 * CONV_STAGE_LD : (float*)(win0 + wave * STAGE_BYTES);
+  const int wm = wave % CW;  // row block of WT rows
+  const int wn = wave / CW;  // column half
   const int loader = wave % RW;
   const bool loadsWeights = wave < RW;
-  const bool loadsWindow = wave >= RW;
+  const bool loadsWindow = wave >= RW && wave < 2 * RW;
   int rowTile, colTile;
   rowColTile(cout / BN, rowTile, colTile);
   const int board = RW == BW_ROW_WAVES ? rowTile : rowTile >> 1;
@@ -1202,7 +1214,7 @@ __global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoar
   int aBase[RB];
 #pragma unroll
   for(int rb = 0; rb < RB; rb++) {
-    const int i = rowBase + wm * BW_WTM + rb * 32 + laneRow;
+    const int i = rowBase + wm * WT + rb * 32 + laneRow;
     const int pos = i < BW_HW ? (i / BW_SIDE + 1 - py0) * BW_PSIDE + (i % BW_SIDE + 1) : BW_PSIDE + 1;
     aBase[rb] = (pos - BW_PSIDE - 1) * BW_ROW_BYTES + kq * 16;
   }
@@ -1219,7 +1231,7 @@ __global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoar
   // C2's residual convs.)
   floatx16 acc[RB][CB];
   if(!SPLIT && epi.residual != nullptr) {
-    residualToAcc<half_t, RB, CB, 1>(acc, epi.residual, epi.ldRes, m0 + rowBase + wm * BW_WTM, n0 + wn * WTN, mEnd, stage);
+    residualToAcc<half_t, RB, CB, 1>(acc, epi.residual, epi.ldRes, m0 + rowBase + wm * WT, n0 + wn * WTN, mEnd, stage);
     __syncthreads();
   }
   else {
@@ -1335,7 +1347,7 @@ __global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoar
     for(int rb = 0; rb < RB; rb++)
 #pragma unroll
       for(int r = 0; r < 16; r++) {
-        const int i = rowBase + wm * BW_WTM + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        const int i = rowBase + wm * WT + rb * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
         if(i < BW_HW) {
 #pragma unroll
           for(int cb = 0; cb < CB; cb++) dst[(size_t)(m0 + i) * cout + n0 + wn * WTN + cb * 32 + laneRow] = acc[rb][cb][r];
@@ -1343,7 +1355,7 @@ __global__ __launch_bounds__(128 * RW, RW == BW_ROW_WAVES ? 1 : 2) void convBoar
       }
   }
   else {
-    storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage, m0 + rowBase + wm * BW_WTM, n0 + wn * WTN, mEnd, BW_HW, epi);
+    storeWaveEpilogue<half_t, RB, CB, true, false>(acc, stage, m0 + rowBase + wm * WT, n0 + wn * WTN, mEnd, BW_HW, epi);
   }
 }
 
@@ -1722,12 +1734,12 @@ void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const
   KGH_CHECK_LAUNCH();
 }
 
-template<int BN, int RW = BW_ROW_WAVES>
+template<int BN, int RW = BW_ROW_WAVES, int WT = BW_WTM>
 void launchBoardWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                        const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   dim3 grid(g.batch * (RW == BW_ROW_WAVES ? 1 : 2) * (cout / BN));
-  hipLaunchKernelGGL((convBoardWindowKernel<BN, BN == 64 ? 9 : 6, false, RW>), grid, dim3(128 * RW), 0, stream, x, cinStride, cinPad,
-                     cout, w, g.batch, epi);
+  hipLaunchKernelGGL((convBoardWindowKernel<BN, BN == 64 ? 9 : 6, false, RW, WT>), grid, dim3(128 * RW * BW_WTM / WT), 0, stream, x,
+                     cinStride, cinPad, cout, w, g.batch, epi);
   KGH_CHECK_LAUNCH();
 }
 
@@ -1783,9 +1795,13 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
       return true;
     }
     if(cinPad >= 64) {
-      // Half boards (two workgroups per CU) while the doubled count still
+      // Half boards with 32-row wave tiles (12 waves, one workgroup per CU)
+      // while the half boards fit the CUs one to a CU; half boards with
+      // 96-row tiles (two workgroups per CU) while the doubled count still
       // fits the CUs' 512 slots in one round.
-      if((long)g.batch * (cout / 64) <= 256) launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      const long halves = (long)g.batch * 2 * (cout / 64);
+      if(halves <= 256) launchBoardWindow<64, 2, 32>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      else if(halves <= 512) launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
       else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
       return true;
     }
@@ -1899,7 +1915,8 @@ bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g
       if(v == CONV_TW_64) return tapWindowFits(cinStride, cinPad, cout, 64, g, epi);
       if(v == CONV_BOARD_192) return boardWindowFits(cinStride, cinPad, cout, 192, g, epi);
       if(v == CONV_BOARD_128) return boardWindowFits(cinStride, cinPad, cout, 128, g, epi);
-      if(v == CONV_BOARD_64 || v == CONV_BOARD_HALF_64) return boardWindowFits(cinStride, cinPad, cout, 64, g, epi);
+      if(v == CONV_BOARD_64 || v == CONV_BOARD_HALF_64 || v == CONV_BOARD_HALF_64_T32)
+        return boardWindowFits(cinStride, cinPad, cout, 64, g, epi);
     }
     else {
       if(v == CONV_DMA1_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
@@ -1949,6 +1966,7 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
       case CONV_BOARD_128: launchBoardWindow<128>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_64: launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_HALF_64: launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_BOARD_HALF_64_T32: launchBoardWindow<64, 2, 32>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_ALLK1_64: launch1x1AllK<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_ALLK1_32: launch1x1AllK<32>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_192: launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
@@ -2002,7 +2020,7 @@ const char* convVariantName(int variant) {
   static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
                                 "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64",
                                 "dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "boardhalf64", "allk1x1_64", "allk1x1_32",
-                                "dma1x1_256glu"};
+                                "dma1x1_256glu", "boardhalf64t32"};
   return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
 }
 
@@ -2092,9 +2110,10 @@ void launchConvSplitK(const half_t* x, int cinStride, int cinPad, int cout, cons
                       const ConvEpilogue<half_t>& epi, float* work, hipStream_t stream) {
   if(!convSplitKApplies(cinStride, cinPad, cout, 3, 3, w, g, epi)) throw KghError(5, "conv: split-K does not apply to this shape");
   const int splits = splitKCount(cinPad);
-  // Half boards: at one board, 2 x 3 x 6 = 36 workgroups for a 192-channel conv.
-  hipLaunchKernelGGL((convBoardWindowKernel<SPLITK_BN, 9, true, 2>), dim3(g.batch * 2 * (cout / SPLITK_BN), splits), dim3(128 * 2), 0,
-                     stream, x, cinStride, cinPad, cout, w, g.batch, epi, work);
+  // Half boards with 32-row wave tiles: at one board, 2 x 3 x 6 = 36
+  // workgroups of 12 waves for a 192-channel conv.
+  hipLaunchKernelGGL((convBoardWindowKernel<SPLITK_BN, 9, true, 2, 32>), dim3(g.batch * 2 * (cout / SPLITK_BN), splits), dim3(128 * 2 * 3),
+                     0, stream, x, cinStride, cinPad, cout, w, g.batch, epi, work);
   KGH_CHECK_LAUNCH();
   const int M = g.batch * g.H * g.W;
   const long threads = (long)M * (cout / 8);
