@@ -1797,11 +1797,12 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
     if(cinPad >= 64) {
       // Half boards with 32-row wave tiles (12 waves, one workgroup per CU)
       // while the half boards fit the CUs one to a CU; half boards with
-      // 96-row tiles (two workgroups per CU) while the doubled count still
-      // fits the CUs' 512 slots in one round.
+      // 96-row tiles (two workgroups per CU) up to one and a half rounds of
+      // the CUs' 512 slots (the tuner's pick over whole boards for C2's net
+      // at 96 and 128 boards: 40 vs 45 us per conv).
       const long halves = (long)g.batch * 2 * (cout / 64);
       if(halves <= 256) launchBoardWindow<64, 2, 32>(x, cinStride, cinPad, cout, w, g, epi, stream);
-      else if(halves <= 512) launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
+      else if(halves <= 768) launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream);
       else launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream);
       return true;
     }
