@@ -203,12 +203,14 @@ __global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, c
 // (board, query head); K (row-major, rows padded by 16 bytes) and V
 // (transposed, [dim][key], rows padded by 8 bytes) of the board's kv head are
 // staged in LDS once, so each wave then streams the keys from LDS with no
-// further barrier. Wave w owns queries 32w .. 32w+31 and, per block of 32
-// keys, computes S^T = K Q^T (lane = query, 16 keys per lane), an online
-// softmax per lane, and O^T += V^T P^T with P taken straight from the
-// accumulator registers: the key order inside the second product's k slots
-// is the accumulator's row order (lane half kq holds keys kq*4 + {0..3, 8..11}
-// of each 16-key step), and V^T is read in that same order.
+// further barrier. Wave w owns queries 32w .. 32w+31 and, per block of 32 keys, computes
+// S^T = K Q^T (lane = query, 16 keys per lane), an online softmax per lane,
+// and O^T += V^T P^T with P taken straight from the accumulator registers:
+// the key order inside the second product's k slots is the accumulator's row
+// order (lane half kq holds keys kq*4 + {0..3, 8..11} of each 16-key step),
+// and V^T is read in that same order. The score products of the next key
+// block are issued before the softmax of the current one, so the matrix
+// cores run them while the vector units work through the softmax.
 constexpr int FA_THREADS = 768;
 constexpr int FA_MAX_KEYS = 384;
 
@@ -228,31 +230,61 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
   constexpr int VLD = FA_MAX_KEYS + 4;    // halves per V^T row (8-byte pad)
   __shared__ __attribute__((aligned(16))) half_t Ks[FA_MAX_KEYS * KLD];
   __shared__ __attribute__((aligned(16))) half_t Vt[DVP * VLD];
-  __shared__ float keyOk[FA_MAX_KEYS];
+  __shared__ float keyBias[FA_MAX_KEYS];  // 0 for a valid key, -inf for a masked one or one past HW
 
-  const int n = blockIdx.x / H;
-  const int h = blockIdx.x - n * H;
-  const int kvh = h / (H / KV);
   const int tid = threadIdx.x;
-  const size_t rowBase = (size_t)n * HW;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int q0 = wave * 32;
+  const int laneRow = lane & 31;
+  const int kq = lane >> 5;
+  const int qi = q0 + laneRow;
+  const int qRow = qi < HW ? qi : HW - 1;
 
-  // Stage K rows (16-byte groups), V^T (8 dims of one key per thread) and the
-  // key mask; keys past HW and dims past DV are zero.
+  // Thread tid covers K 16-byte groups and V 16-byte groups tid + it *
+  // FA_THREADS (key = index / groups per row) and, below FA_MAX_KEYS, key
+  // tid's mask value; keys past HW and dims past DV are zero.
   constexpr int PAIRS = DQ / 2;
   constexpr int K_ITERS = FA_MAX_KEYS * (DQ / 8) / FA_THREADS;
   constexpr int V_ITERS = FA_MAX_KEYS * (DVP / 8) / FA_THREADS;
   static_assert(K_ITERS * FA_THREADS == FA_MAX_KEYS * (DQ / 8) && V_ITERS * FA_THREADS == FA_MAX_KEYS * (DVP / 8),
                 "staging loops without a remainder");
+  static_assert(FA_MAX_KEYS <= FA_THREADS, "one key mask value per thread");
+  uint4 kPre[K_ITERS];
+  uint4 vPre[V_ITERS];
+  float mPre = 0.0f;
+  auto fetch = [&](int item) {
+    const int n = item / H;
+    const int kvh = (item - n * H) / (H / KV);
+    const size_t rowBase = (size_t)n * HW;
 #pragma unroll
-  for(int it = 0; it < K_ITERS; it++) {
-    const int i = tid + it * FA_THREADS;
-    const int key = i / (DQ / 8);
-    const int g = i - key * (DQ / 8);
-    half_t v[8];
-    *(uint4*)v = make_uint4(0, 0, 0, 0);
-    if(key < HW) {
-      *(uint4*)v = *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8);
-      if(cosT != nullptr) {
+    for(int it = 0; it < K_ITERS; it++) {
+      const int i = tid + it * FA_THREADS;
+      const int key = i / (DQ / 8);
+      const int g = i - key * (DQ / 8);
+      kPre[it] = key < HW ? *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for(int it = 0; it < V_ITERS; it++) {
+      const int i = tid + it * FA_THREADS;
+      const int key = i / (DVP / 8);
+      const int g = i - key * (DVP / 8);
+      vPre[it] = key < HW && g * 8 < DV ? *(const uint4*)(qkv + (rowBase + key) * ld + vOff + kvh * DV + g * 8) : make_uint4(0, 0, 0, 0);
+    }
+    mPre = tid < HW ? mask[rowBase + tid] : 0.0f;
+  };
+  // Writes the fetched item's K rows (rotated when cosT is set), V^T and key
+  // mask into LDS.
+  auto stage = [&](int item) {
+    const int kvh = (item - item / H * H) / (H / KV);
+#pragma unroll
+    for(int it = 0; it < K_ITERS; it++) {
+      const int i = tid + it * FA_THREADS;
+      const int key = i / (DQ / 8);
+      const int g = i - key * (DQ / 8);
+      half_t v[8];
+      *(uint4*)v = kPre[it];
+      if(cosT != nullptr && key < HW) {
         // The group's four pairs are contiguous in the tables: one 16-byte
         // load each.
         const size_t ti = ((size_t)(learnable ? kvh : 0) * HW + key) * PAIRS + g * 4;
@@ -266,131 +298,149 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
           v[2 * q + 1] = (half_t)y1;
         }
       }
+      *(uint4*)&Ks[key * KLD + g * 8] = *(const uint4*)v;
     }
-    *(uint4*)&Ks[key * KLD + g * 8] = *(const uint4*)v;
-  }
 #pragma unroll
-  for(int it = 0; it < V_ITERS; it++) {
-    const int i = tid + it * FA_THREADS;
-    const int key = i / (DVP / 8);
-    const int g = i - key * (DVP / 8);
-    half_t v[8];
-    *(uint4*)v = make_uint4(0, 0, 0, 0);
-    if(key < HW && g * 8 < DV) *(uint4*)v = *(const uint4*)(qkv + (rowBase + key) * ld + vOff + kvh * DV + g * 8);
+    for(int it = 0; it < V_ITERS; it++) {
+      const int i = tid + it * FA_THREADS;
+      const int key = i / (DVP / 8);
+      const int g = i - key * (DVP / 8);
+      half_t v[8];
+      *(uint4*)v = vPre[it];
 #pragma unroll
-    for(int j = 0; j < 8; j++) Vt[(g * 8 + j) * VLD + key] = v[j];
-  }
-  for(int i = tid; i < FA_MAX_KEYS; i += FA_THREADS) keyOk[i] = (i < HW && mask[rowBase + i] != 0.0f) ? 1.0f : 0.0f;
-  __syncthreads();
+      for(int j = 0; j < 8; j++) Vt[(g * 8 + j) * VLD + key] = v[j];
+    }
+    if(tid < FA_MAX_KEYS) keyBias[tid] = (tid < HW && mPre != 0.0f) ? 0.0f : -INFINITY;
+  };
 
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int q0 = wave * 32;
-  if(q0 >= HW) return;  // no barrier follows
-  const int laneRow = lane & 31;
-  const int kq = lane >> 5;
-  const int qi = q0 + laneRow;
-  const int qRow = qi < HW ? qi : HW - 1;
-
-  half8_t qf[DQ / 16];
+  auto attend = [&](int item) {
+    stage(item);
+    __syncthreads();
+    const int n = item / H;
+    const int h = item - n * H;
+    const size_t rowBase = (size_t)n * HW;
+    half8_t qf[DQ / 16];
+    if(q0 < HW) {
+      // All fragment loads first, then the rotation: a rotation between
+      // them would make each load wait for the one before.
 #pragma unroll
-  for(int ks = 0; ks < DQ / 16; ks++) {
-    qf[ks] = *(const half8_t*)(qkv + (rowBase + qRow) * ld + h * DQ + ks * 16 + kq * 8);
-    if(cosT != nullptr) {
-      const size_t ti = ((size_t)(learnable ? h * KV / H : 0) * HW + qRow) * PAIRS + (ks * 16 + kq * 8) / 2;
-      const float4 c4 = *(const float4*)(cosT + ti), s4 = *(const float4*)(sinT + ti);
-      const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+      for(int ks = 0; ks < DQ / 16; ks++) qf[ks] = *(const half8_t*)(qkv + (rowBase + qRow) * ld + h * DQ + ks * 16 + kq * 8);
+      if(cosT != nullptr) {
 #pragma unroll
-      for(int q = 0; q < 4; q++) {
-        float y0, y1;
-        kgh_rope_pair((float)qf[ks][2 * q], (float)qf[ks][2 * q + 1], cc[q], ss[q], y0, y1);
-        qf[ks][2 * q] = (half_t)y0;
-        qf[ks][2 * q + 1] = (half_t)y1;
+        for(int ks = 0; ks < DQ / 16; ks++) {
+          const size_t ti = ((size_t)(learnable ? h * KV / H : 0) * HW + qRow) * PAIRS + (ks * 16 + kq * 8) / 2;
+          const float4 c4 = *(const float4*)(cosT + ti), s4 = *(const float4*)(sinT + ti);
+          const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+          for(int q = 0; q < 4; q++) {
+            float y0, y1;
+            kgh_rope_pair((float)qf[ks][2 * q], (float)qf[ks][2 * q + 1], cc[q], ss[q], y0, y1);
+            qf[ks][2 * q] = (half_t)y0;
+            qf[ks][2 * q + 1] = (half_t)y1;
+          }
+        }
       }
     }
-  }
 
-  floatx16 o[DVP / 32];
+    if(q0 < HW) {
+      floatx16 o[DVP / 32];
 #pragma unroll
-  for(int db = 0; db < DVP / 32; db++)
+      for(int db = 0; db < DVP / 32; db++)
 #pragma unroll
-    for(int r = 0; r < 16; r++) o[db][r] = 0.0f;
-  float mRun = -INFINITY, lRun = 0.0f;
+        for(int r = 0; r < 16; r++) o[db][r] = 0.0f;
+      // Scores stay unscaled (scale > 0 keeps their order); the exponent
+      // scales them by c = scale * log2(e): p = 2^(s c - m c).
+      const float c = scale * 1.44269504088896341f;
+      float mRun = -INFINITY, lRun = 0.0f;
 
-  const int keyTiles = (HW + 31) / 32;
-  for(int kt = 0; kt < keyTiles; kt++) {
-    const int kb = kt * 32;
-    floatx16 s;
+      // S^T of the 32-key block at kb.
+      auto scores = [&](int kb, floatx16& sc) {
 #pragma unroll
-    for(int r = 0; r < 16; r++) s[r] = 0.0f;
+        for(int r = 0; r < 16; r++) sc[r] = 0.0f;
 #pragma unroll
-    for(int ks = 0; ks < DQ / 16; ks++) {
-      const half8_t a = *(const half8_t*)&Ks[(kb + laneRow) * KLD + ks * 16 + kq * 8];
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], s, 0, 0, 0);
-    }
-    float mTile = -INFINITY;
+        for(int ks = 0; ks < DQ / 16; ks++) {
+          const half8_t a = *(const half8_t*)&Ks[(kb + laneRow) * KLD + ks * 16 + kq * 8];
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], sc, 0, 0, 0);
+        }
+      };
+      const int keyTiles = (HW + 31) / 32;
+      floatx16 sNext;
+      scores(0, sNext);
+      for(int kt = 0; kt < keyTiles; kt++) {
+        const int kb = kt * 32;
+        floatx16 s = sNext;
+        if(kt + 1 < keyTiles) scores(kb + 32, sNext);
+        float mTile = -INFINITY;
 #pragma unroll
-    for(int r = 0; r < 16; r++) {
-      const int key = kb + (r >> 2) * 8 + kq * 4 + (r & 3);
-      const float v = keyOk[key] != 0.0f ? s[r] * scale : -INFINITY;
-      s[r] = v;
-      mTile = fmaxf(mTile, v);
-    }
-    mTile = fmaxf(mTile, __shfl_xor(mTile, 32));
-    // Every lane runs every matrix instruction (no divergence around them):
-    // while a query has seen no valid key, mNew is -inf and the reference
-    // point 0 makes corr and every p exactly 0.
-    const float mNew = fmaxf(mRun, mTile);
-    const float mRef = mNew == -INFINITY ? 0.0f : mNew;
-    const float corr = __expf(mRun - mRef);
-    float psum = 0.0f;
+        for(int r = 0; r < 16; r++) {
+          s[r] += keyBias[kb + (r >> 2) * 8 + kq * 4 + (r & 3)];
+          mTile = fmaxf(mTile, s[r]);
+        }
+        mTile = fmaxf(mTile, __shfl_xor(mTile, 32));
+        // Every lane runs every matrix instruction (no divergence around
+        // them): while a query has seen no valid key, mNew is -inf and the
+        // reference point 0 makes corr and every p exactly 0.
+        const float mNew = fmaxf(mRun, mTile);
+        const float mRef = mNew == -INFINITY ? 0.0f : mNew;
+        const float corr = __builtin_amdgcn_exp2f((mRun - mRef) * c);
+        const float negM = -mRef * c;
+        float psum = 0.0f;
 #pragma unroll
-    for(int r = 0; r < 16; r++) {
-      const float p = __expf(s[r] - mRef);
-      s[r] = p;
-      psum += p;
-    }
-    psum += __shfl_xor(psum, 32);
-    lRun = lRun * corr + psum;
-    mRun = mNew;
+        for(int r = 0; r < 16; r++) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[r], c, negM));
+          s[r] = p;
+          psum += p;
+        }
+        psum += __shfl_xor(psum, 32);
+        lRun = lRun * corr + psum;
+        mRun = mNew;
+        // corr is exactly 1 for a query whose running maximum did not move,
+        // and the rescale is skipped when that holds for the whole wave.
+        if(__any(corr != 1.0f)) {
 #pragma unroll
-    for(int db = 0; db < DVP / 32; db++)
+          for(int db = 0; db < DVP / 32; db++)
 #pragma unroll
-      for(int r = 0; r < 16; r++) o[db][r] *= corr;
+            for(int r = 0; r < 16; r++) o[db][r] *= corr;
+        }
 #pragma unroll
-    for(int j = 0; j < 2; j++) {
-      half8_t b;
+        for(int j = 0; j < 2; j++) {
+          half8_t b;
 #pragma unroll
-      for(int r = 0; r < 8; r++) b[r] = (half_t)s[8 * j + r];
-      const int k0 = kb + 16 * j + kq * 4;
+          for(int r = 0; r < 8; r++) b[r] = (half_t)s[8 * j + r];
+          const int k0 = kb + 16 * j + kq * 4;
 #pragma unroll
-      for(int db = 0; db < DVP / 32; db++) {
-        const half_t* vr = &Vt[(db * 32 + laneRow) * VLD + k0];
-        half4_t lo = *(const half4_t*)vr;
-        half4_t hi = *(const half4_t*)(vr + 8);
-        half8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[db], 0, 0, 0);
+          for(int db = 0; db < DVP / 32; db++) {
+            const half_t* vr = &Vt[(db * 32 + laneRow) * VLD + k0];
+            half4_t lo = *(const half4_t*)vr;
+            half4_t hi = *(const half4_t*)(vr + 8);
+            half8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[db], 0, 0, 0);
+          }
+        }
+      }
+
+      if(qi < HW) {
+        const size_t row = rowBase + qi;
+        const bool on = mask[row] != 0.0f && lRun > 0.0f;
+        const float invL = on ? 1.0f / lRun : 0.0f;
+        half_t* dst = out + row * ldOut + h * DV;
+#pragma unroll
+        for(int db = 0; db < DVP / 32; db++)
+#pragma unroll
+          for(int g = 0; g < 4; g++) {
+            const int d = db * 32 + g * 8 + kq * 4;
+            if(d < DV) {
+              half4_t v;
+#pragma unroll
+              for(int j = 0; j < 4; j++) v[j] = (half_t)(o[db][4 * g + j] * invL);
+              *(half4_t*)(dst + d) = v;
+            }
+          }
       }
     }
-  }
-
-  if(qi >= HW) return;
-  const size_t row = rowBase + qi;
-  const bool on = mask[row] != 0.0f && lRun > 0.0f;
-  const float invL = on ? 1.0f / lRun : 0.0f;
-  half_t* dst = out + row * ldOut + h * DV;
-#pragma unroll
-  for(int db = 0; db < DVP / 32; db++)
-#pragma unroll
-    for(int g = 0; g < 4; g++) {
-      const int d = db * 32 + g * 8 + kq * 4;
-      if(d < DV) {
-        half4_t v;
-#pragma unroll
-        for(int j = 0; j < 4; j++) v[j] = (half_t)(o[db][4 * g + j] * invL);
-        *(half4_t*)(dst + d) = v;
-      }
-    }
+  };
+  fetch(blockIdx.x);
+  attend(blockIdx.x);
 }
 
 // Attention without matrix cores, for fp32 contexts and head shapes the
