@@ -203,12 +203,12 @@ __global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, c
 // (board, query head); K (row-major, rows padded by 16 bytes) and V
 // (transposed, [dim][key], rows padded by 8 bytes) of the board's kv head are
 // staged in LDS once, so each wave then streams the keys from LDS with no
-// further barrier. Wave w owns queries 32w .. 32w+31 and, per block of 32 keys, computes
-// S^T = K Q^T (lane = query, 16 keys per lane), an online softmax per lane,
-// and O^T += V^T P^T with P taken straight from the accumulator registers:
-// the key order inside the second product's k slots is the accumulator's row
-// order (lane half kq holds keys kq*4 + {0..3, 8..11} of each 16-key step),
-// and V^T is read in that same order. The score products of the next key
+// further barrier. Wave w owns queries 32w .. 32w+31 and, per block of 32
+// keys, computes S^T = K Q^T (lane = query, 16 keys per lane), an online
+// softmax per lane, and O^T += V^T P^T with P taken straight from the
+// accumulator registers: the key order inside the second product's k slots
+// is the accumulator's row order (lane half kq holds keys kq*4 + {0..3, 8..11}
+// of each 16-key step), and V^T is read in that same order. The score products of the next key
 // block are issued before the softmax of the current one, so the matrix
 // cores run them while the vector units work through the softmax.
 constexpr int FA_THREADS = 768;
@@ -250,9 +250,9 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
   static_assert(K_ITERS * FA_THREADS == FA_MAX_KEYS * (DQ / 8) && V_ITERS * FA_THREADS == FA_MAX_KEYS * (DVP / 8),
                 "staging loops without a remainder");
   static_assert(FA_MAX_KEYS <= FA_THREADS, "one key mask value per thread");
-  uint4 kPre[K_ITERS];
-  uint4 vPre[V_ITERS];
-  float mPre = 0.0f;
+  uint4 kRows[K_ITERS];
+  uint4 vRows[V_ITERS];
+  float keyMask = 0.0f;
   auto fetch = [&](int item) {
     const int n = item / H;
     const int kvh = (item - n * H) / (H / KV);
@@ -262,19 +262,19 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
       const int i = tid + it * FA_THREADS;
       const int key = i / (DQ / 8);
       const int g = i - key * (DQ / 8);
-      kPre[it] = key < HW ? *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8) : make_uint4(0, 0, 0, 0);
+      kRows[it] = key < HW ? *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8) : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for(int it = 0; it < V_ITERS; it++) {
       const int i = tid + it * FA_THREADS;
       const int key = i / (DVP / 8);
       const int g = i - key * (DVP / 8);
-      vPre[it] = key < HW && g * 8 < DV ? *(const uint4*)(qkv + (rowBase + key) * ld + vOff + kvh * DV + g * 8) : make_uint4(0, 0, 0, 0);
+      vRows[it] = key < HW && g * 8 < DV ? *(const uint4*)(qkv + (rowBase + key) * ld + vOff + kvh * DV + g * 8) : make_uint4(0, 0, 0, 0);
     }
-    mPre = tid < HW ? mask[rowBase + tid] : 0.0f;
+    keyMask = tid < HW ? mask[rowBase + tid] : 0.0f;
   };
-  // Writes the fetched item's K rows (rotated when cosT is set), V^T and key
-  // mask into LDS.
+  // Writes the loaded K rows (rotated when cosT is set), V^T and key mask
+  // into LDS.
   auto stage = [&](int item) {
     const int kvh = (item - item / H * H) / (H / KV);
 #pragma unroll
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
       const int key = i / (DQ / 8);
       const int g = i - key * (DQ / 8);
       half_t v[8];
-      *(uint4*)v = kPre[it];
+      *(uint4*)v = kRows[it];
       if(cosT != nullptr && key < HW) {
         // The group's four pairs are contiguous in the tables: one 16-byte
         // load each.
@@ -306,11 +306,11 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
       const int key = i / (DVP / 8);
       const int g = i - key * (DVP / 8);
       half_t v[8];
-      *(uint4*)v = vPre[it];
+      *(uint4*)v = vRows[it];
 #pragma unroll
       for(int j = 0; j < 8; j++) Vt[(g * 8 + j) * VLD + key] = v[j];
     }
-    if(tid < FA_MAX_KEYS) keyBias[tid] = (tid < HW && mPre != 0.0f) ? 0.0f : -INFINITY;
+    if(tid < FA_MAX_KEYS) keyBias[tid] = (tid < HW && keyMask != 0.0f) ? 0.0f : -INFINITY;
   };
 
   auto attend = [&](int item) {
