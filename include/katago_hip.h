@@ -197,8 +197,8 @@ int kgh_handle_synchronize(kgh_handle* handle);
  * built-in kernel choices (bitwise). Runs on hip_stream (a hipStream_t, NULL
  * for the null stream), asynchronously; the caller synchronizes. n boards of
  * nn_x by nn_y must fit the array (C2's b18c384nbt: about 44 boards at 19x19),
- * else KGH_ERR_INVALID_ARGUMENT names the bytes needed; nets with attention
- * blocks return KGH_ERR_UNSUPPORTED (their rotary tables live in a handle).
+ * else KGH_ERR_INVALID_ARGUMENT names the bytes needed; nets with transformer
+ * blocks (attention or FFN, at any depth) return KGH_ERR_UNSUPPORTED.
  * Every call on one GPU shares the array: calls that overlap on one GPU race
  * and must be serialized by the caller (one stream, or events). */
 int kgh_forward_device_noalloc(kgh_model* model, int32_t n, int32_t nn_x, int32_t nn_y, const float* d_spatial,

@@ -1632,6 +1632,15 @@ void forwardStaged(kgh_handle* handle, int n) {
 }
 }  // namespace
 
+namespace {
+// Attention and FFN blocks, at any nesting depth.
+bool hasTransformerBlock(const std::vector<Block>& blocks) {
+  for(const Block& b : blocks)
+    if(b.kind == BK_ATTENTION || b.kind == BK_FFN || hasTransformerBlock(b.inner)) return true;
+  return false;
+}
+}  // namespace
+
 int kgh_forward_device_noalloc(kgh_model* model, int32_t n, int32_t nn_x, int32_t nn_y, const float* d_spatial,
                                const float* d_global, const int32_t* d_symmetry, const float* d_policy_optimism, float* d_out,
                                void* hip_stream) {
@@ -1640,9 +1649,9 @@ int kgh_forward_device_noalloc(kgh_model* model, int32_t n, int32_t nn_x, int32_
     if(n <= 0) invalid("batch size must be positive");
     if(nn_x <= 0 || nn_y <= 0 || nn_x > 64 || nn_y > 64) invalid("nn_x and nn_y must be in 1..64");
     if(!d_spatial || !d_global || !d_symmetry || !d_policy_optimism || !d_out) invalid("null device pointer");
-    if(!model->net.ropes.empty())
-      unsupported("kgh_forward_device_noalloc: attention blocks need rotary tables per board size, which only a handle "
-                  "holds; use kgh_forward_device");
+    if(hasTransformerBlock(model->net.blocks))
+      unsupported("kgh_forward_device_noalloc: nets with transformer (attention or FFN) blocks need a handle (rotary "
+                  "tables per board size); use kgh_forward_device");
     KGH_HIP_CHECK(hipSetDevice(model->device));
     unsigned char* base = scratchAddress(model->device);
     const size_t limit = KGH_NOALLOC_SCRATCH_BYTES - KGH_NOALLOC_GUARD_BYTES;

@@ -95,6 +95,9 @@ struct GoBoard {
   // breadth-first order from its first stone in scan order.
   void init(int xSize, int ySize, const int8_t* colors, int koPoint, const int16_t* chainHead, const int16_t* chainNext,
             Scratch& s) {
+    // Board::ko_loc is a point of this board or none (-1); any other value
+    // would address a feature plane outside the row.
+    if(koPoint < -1 || koPoint >= xSize * ySize) throw std::runtime_error("featurize: ko_point off the board");
     xs = xSize;
     ys = ySize;
     stride = xs + 2;
@@ -1043,6 +1046,11 @@ void featurizeOne(const kgn_position& pos, int nnX, int nnY, bool nhwc, float* r
   if(pos.next_player != BLACK && pos.next_player != WHITE) throw std::runtime_error("featurize: next_player must be 1 or 2");
   if(pos.colors[0] == nullptr) throw std::runtime_error("featurize: no current board");
   if(pos.num_moves < 0 || pos.num_moves > 5) throw std::runtime_error("featurize: num_moves outside 0..5");
+  // Every board supplied must have its ko point on it (or -1), whether or
+  // not the history below reaches that board.
+  for(int k = 0; k < 3; k++)
+    if((k == 0 || pos.colors[k] != nullptr) && (pos.ko_point[k] < -1 || pos.ko_point[k] >= xs * ys))
+      throw std::runtime_error("featurize: ko_point off the board");
   const int C = KGN_FEATURES_SPATIAL_V7;
   std::fill(rowBin, rowBin + (size_t)C * nnX * nnY, 0.0f);
   std::fill(rowGlobal, rowGlobal + KGN_FEATURES_GLOBAL_V7, 0.0f);

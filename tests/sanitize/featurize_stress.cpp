@@ -157,6 +157,22 @@ int main(int argc, char** argv) {
       return 1;
     }
   }
+  // Off-board ko points on each board, as the last row of a batch whose
+  // output arrays end exactly at that row (an overrun is a sanitizer error).
+  for(size_t i = 0; i < pos.size() && i < 64; i++) {
+    const Stored& s = pos[i];
+    for(int k = 0; k < 3; k++)
+      for(int ko : {-7, s.p.x_size * s.p.y_size, 399, 100000}) {
+        kgn_position bad[2] = {s.p, s.p};
+        bad[1].ko_point[k] = ko;
+        std::vector<float> sp((size_t)2 * s.nnx * s.nny * KGN_FEATURES_SPATIAL_V7), gl(2 * KGN_FEATURES_GLOBAL_V7);
+        if(kgn_featurize(bad, 2, s.nnx, s.nny, 1, sp.data(), gl.data(), 1, err, sizeof(err)) == 0 &&
+           (k == 0 || bad[1].colors[k] != nullptr)) {
+          std::fprintf(stderr, "position %zu: ko point %d on board %d was accepted\n", i, ko, k);
+          return 1;
+        }
+      }
+  }
   std::FILE* f = std::fopen(argv[2], "wb");
   if(f == nullptr) return 1;
   for(const std::vector<float>& r : single) std::fwrite(r.data(), sizeof(float), r.size(), f);

@@ -107,6 +107,20 @@ def test_featurizer_rejects_invalid_positions():
         nn.featurize(nn.Positions([fx]), 3, 3)
 
 
+@pytest.mark.parametrize("board", [0, 1, 2])
+@pytest.mark.parametrize("ko", [-2, "area", 399])
+def test_featurizer_rejects_off_board_ko_points(board, ko):
+    """A ko point outside -1..x_size*y_size-1 is refused for each of the
+    three boards supplied (it would otherwise address a feature plane
+    outside the row)."""
+    fx = next(f for f in FIXTURES if f["nnx"] == 19 and f["x_size"] == 19 and f["y_size"] == 19 and
+              all(c is not None for c in f["colors"]))
+    fx = dict(fx, ko_point=list(fx["ko_point"]))
+    fx["ko_point"][board] = fx["x_size"] * fx["y_size"] if ko == "area" else ko
+    with pytest.raises(nn.StringError, match="ko_point off the board"):
+        nn.featurize(nn.Positions([fx]), 19, 19)
+
+
 @pytest.mark.skipif(not os.path.isdir(REF_CPP), reason="needs the reference source tree")
 def test_featurizer_matches_katago_on_random_games():
     """About 35,000 positions: every named ruleset, nine board shapes, forced

@@ -104,6 +104,28 @@ def test_shortterm_error_version_branches():
     assert (v8[6], v8[7], v8[8]) == (-1.0, -1.0, -1.0)
 
 
+@pytest.mark.parametrize("version", [14, 15, 17])
+def test_shortterm_error_squared_softplus_branch(version):
+    """Model versions 14+ (nneval.cpp:1148-1157): the two shortterm outputs
+    are variances the training model produces as softplus(x / 2)^2
+    (SoftPlusWithGradientFloorFunction with square=True,
+    model_pytorch.py:111-131), so the error is sqrt(multiplier) *
+    softplus(x / 2). Known answers away from 0, where the v10-13 branch
+    sqrt(softplus(x) * multiplier) gives other values."""
+    for xw, xs in [(2.0, -3.0), (-1.5, 4.0), (6.0, 0.7)]:
+        _, v, _ = _row(np.zeros(HW + 1), score=(0.0, 0.0, 0.0, 0.0, xw, xs), model_version=version)
+        sp = lambda x: math.log1p(math.exp(x))
+        assert v[7] == pytest.approx(math.sqrt(0.25) * sp(xw / 2), rel=1e-12)
+        assert v[8] == pytest.approx(math.sqrt(30.0) * sp(xs / 2), rel=1e-12)
+        _, v13, _ = _row(np.zeros(HW + 1), score=(0.0, 0.0, 0.0, 0.0, xw, xs), model_version=13)
+        assert abs(v13[7] - v[7]) > 1e-3 and abs(v13[8] - v[8]) > 1e-3
+    # x = 2 ln(e - 1): softplus(x / 2) = 1 exactly, so the errors are the
+    # square roots of the multipliers.
+    x = 2 * math.log(math.e - 1)
+    _, v, _ = _row(np.zeros(HW + 1), score=(0.0, 0.0, 0.0, 0.0, x, x), model_version=version)
+    assert (v[7], v[8]) == pytest.approx((0.5, math.sqrt(30.0)), rel=1e-12)
+
+
 def test_ownership_tanh_sign_and_off_board_zero():
     own = np.full(HW, 0.5, np.float32)
     _, _, ow = _row(np.zeros(HW + 1), own=own, board_x=9, board_y=13, white_to_move=False)

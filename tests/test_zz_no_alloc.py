@@ -57,9 +57,10 @@ def test_noalloc_forward_matches_handle_forward(model_dir, cfg_index, nn_x, nn_y
         assert np.array_equal(ref, got), f"{label}: max-abs {np.nanmax(np.abs(ref - got))}"
 
 
-def test_noalloc_rejects_batches_beyond_the_scratch_and_attention_nets(model_dir):
+def test_noalloc_rejects_batches_beyond_the_scratch_and_transformer_nets(model_dir):
     """Checked on the host before any launch: a batch whose activations do not
-    fit the static scratch, and a net with attention blocks."""
+    fit the static scratch, and nets with transformer blocks (attention with
+    rotary tables, or FFN blocks alone)."""
     cfg = modelgen.configs()[2]
     dm = nn.DeviceModel(nn.LoadedModel(modelgen.ensure_model(model_dir, cfg)), use_fp16=True)
     dummy = nn.DeviceBuffer(256)
@@ -67,5 +68,13 @@ def test_noalloc_rejects_batches_beyond_the_scratch_and_attention_nets(model_dir
         dm.forward_device_noalloc(256, 19, 19, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr)
     cfg4 = modelgen.configs()[4]
     dm4 = nn.DeviceModel(nn.LoadedModel(modelgen.ensure_model(model_dir, cfg4)), use_fp16=True)
-    with pytest.raises(nn.StringError, match="attention"):
+    with pytest.raises(nn.StringError, match="transformer"):
         dm4.forward_device_noalloc(1, 19, 19, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr)
+    # A transformer net without rotary tables (FFN blocks only) is refused too.
+    arch = modelgen.Arch("tiny-ffn-only", 17, 64, 64, 32, ["regular", "ffn", "ffn"], 16, 16, 32, 24, "ACTIVATION_SILU",
+                         heads=2, kv_heads=2, q_head_dim=32, v_head_dim=32, ffn_c=96, trunk_rmsnorm=True,
+                         transformer_std=0.08, residual_gain=0.5)
+    path = modelgen.write_model(arch, 7, f"{model_dir}/{arch.name}.bin.gz")
+    dm5 = nn.DeviceModel(nn.LoadedModel(path), use_fp16=True)
+    with pytest.raises(nn.StringError, match="transformer"):
+        dm5.forward_device_noalloc(1, 19, 19, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr, dummy.ptr)
