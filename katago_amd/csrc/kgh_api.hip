@@ -1254,9 +1254,15 @@ void buildNet(kgh_model* m, const kgh_model_desc* d, hipStream_t stream) {
     net.tipEps = r.f[0];
     net.tipGamma = b.dev(r, 0, net.trunkC, "trunk tip gamma");
     net.tipBeta = b.dev(r, 1, net.trunkC, "trunk tip beta");
-    net.tipAct = b.act("trunk tip activation");
-    if(net.tipAct != KGH_ACT_IDENTITY && net.tipAct != KGH_ACT_SILU && net.tipAct != KGH_ACT_RELU && net.tipAct != KGH_ACT_MISH)
+    const int act = b.act("trunk tip activation");
+    if(act != KGH_ACT_IDENTITY && act != KGH_ACT_SILU && act != KGH_ACT_RELU && act != KGH_ACT_MISH)
       invalid("trunk tip: unknown activation");
+    // After an RMSNorm tip the Eigen backend applies the file's activation
+    // only when it is SiLU, and none otherwise (RMSNormLayer::apply,
+    // eigenbackend.cpp:982-984,1012-1014); this backend gives its results.
+    // (KataGo's CUDA backend and the training model apply ReLU and Mish too,
+    // and its OpenCL backend refuses them.)
+    net.tipAct = act == KGH_ACT_SILU ? KGH_ACT_SILU : KGH_ACT_IDENTITY;
   }
 
   // Policy head

@@ -1684,6 +1684,51 @@ __global__ void convDirectKernel(const T* __restrict__ x, int cinStride, int cin
   kgh_epilogue_store(epi, m, n, c, acc);
 }
 
+// The gated (SwiGLU) epilogue for shapes the matrix-core kernels do not
+// take: one thread per gated output o of row m. Output o pairs the value
+// column actBegin + 16*(o/8) + o%8 with the gate column 8 further on (the
+// interleaved layout of the ConvEpilogue contract) and stores
+// act(value) * gate.
+template<typename T>
+__global__ void convDirectGluKernel(const T* __restrict__ x, int cinStride, int cin, int cout, int ky, int kx,
+                                    const float* __restrict__ w, BoardGeom g, ConvEpilogue<T> epi) {
+  const int HW = g.H * g.W;
+  const int gated = (cout - epi.actBegin) / 2;
+  const long total = (long)g.batch * HW * gated;
+  long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= total) return;
+  int m = (int)(idx / gated);
+  int o = (int)(idx - (long)m * gated);
+  int n = m / HW;
+  int s = m - n * HW;
+  int y = s / g.W;
+  int xx0 = s - y * g.W;
+  const int cv = epi.actBegin + 16 * (o / 8) + o % 8;
+  const int cg = cv + 8;
+  float accV = 0.0f, accG = 0.0f;
+  for(int ty = 0; ty < ky; ty++) {
+    int yy = y + ty - ky / 2;
+    if(yy < 0 || yy >= g.H) continue;
+    for(int tx = 0; tx < kx; tx++) {
+      int xx = xx0 + tx - kx / 2;
+      if(xx < 0 || xx >= g.W) continue;
+      const T* src = x + (size_t)(n * HW + yy * g.W + xx) * cinStride;
+      const float* wv = w + ((size_t)cv * cin * ky + ty) * kx + tx;
+      const float* wg = w + ((size_t)cg * cin * ky + ty) * kx + tx;
+      for(int ic = 0; ic < cin; ic++) {
+        const float a = kgh_to_float(src[ic]);
+        accV += a * wv[(size_t)ic * ky * kx];
+        accG += a * wg[(size_t)ic * ky * kx];
+      }
+    }
+  }
+  if(epi.ncBias != nullptr) {
+    accV += epi.ncBias[(size_t)n * epi.ldNC + cv];
+    accG += epi.ncBias[(size_t)n * epi.ldNC + cg];
+  }
+  epi.outAct[(size_t)m * epi.ldAct + o] = kgh_from_float<T>(kgh_activate(accV, epi.actKind) * accG);
+}
+
 template<typename T>
 __global__ void prepareConvWeightsKernel(const float* __restrict__ src, T* __restrict__ dst, int cout, int cin, int cinPad,
                                          int ky, int kx) {
@@ -2086,10 +2131,19 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
   }
   if(usedMfma != nullptr) *usedMfma = done;
   if(done) return;
-  if(epi.glu) throw KghError(3, "conv: the gated (SwiGLU) epilogue needs the matrix-core kernels (channel counts multiples of 32)");
   if(wDirect == nullptr) throw KghError(5, "conv: no direct-layout weights for a shape the matrix-core kernel does not take");
-  long total = (long)g.batch * g.H * g.W * cout;
   int threads = 256;
+  if(epi.glu) {
+    if(epi.residual != nullptr || epi.rawEnd > 0 || epi.outAct == nullptr || (cout - epi.actBegin) % 16 != 0 || epi.actBegin < 0)
+      throw KghError(5, "conv: the gated epilogue takes only gated outputs in blocks of 16 columns");
+    long total = (long)g.batch * g.H * g.W * ((cout - epi.actBegin) / 2);
+    long blocks = (total + threads - 1) / threads;
+    hipLaunchKernelGGL(convDirectGluKernel<T>, dim3((unsigned)blocks), dim3(threads), 0, stream, x, cinStride, cin, cout, ky, kx,
+                       wDirect, g, epi);
+    KGH_CHECK_LAUNCH();
+    return;
+  }
+  long total = (long)g.batch * g.H * g.W * cout;
   long blocks = (total + threads - 1) / threads;
   hipLaunchKernelGGL(convDirectKernel<T>, dim3((unsigned)blocks), dim3(threads), 0, stream, x, cinStride, cin, cout, ky, kx,
                      wDirect, g, epi);
