@@ -395,6 +395,7 @@ def main():
     h.synchronize()
     ms3, n3, fl3 = h.profile(0)
     ms1, n1, fl1 = h.profile(1)
+    per_kernel = h.profile_kernels()
     h.set_profiling(False)
     # Every conv kernel together (3x3 and 1x1): the conv-kernel fraction of the
     # dense peak as the target defines it, direct-conv FLOPs over conv time.
@@ -406,17 +407,14 @@ def main():
           f"{ms3:.2f} ms total, 1x1 conv {n1} launches {ms1:.2f} ms total", file=sys.stderr, flush=True)
     headline = args.config == CFG_INDEX and batch == cfg.batch
     # Roofline kernel: the 3x3 conv for the convolutional nets, the 1x1
-    # (per-position GEMM) kernel for a transformer trunk.
-    # Which 3x3 kernel runs: the one-board kernel for fp16 batches of 128 or
-    # more 19x19 boards, else the 128-row tile kernel (fp16 or fp32).
+    # (per-position GEMM) kernel for a transformer trunk; the figures cover
+    # every launch of that kind, and the name lists the kernels that ran
+    # (as the launches recorded them), the one with the most time first.
     peak = PEAK_FP16_TFLOPS if cfg.fp16 else PEAK_FP32_TFLOPS
-    if ms3 >= ms1:
-        ms_k, n_k, fl_k = ms3, n3, fl3
-        kname = ("convBoardWindowKernel (3x3, fp16, one board per workgroup, trunk and stem)" if cfg.fp16 and batch >= 128 else
-                 f"convMfmaKernel (3x3, {'fp16' if cfg.fp16 else 'fp32'}, 128-row tiles)")
-    else:
-        ms_k, n_k, fl_k = ms1, n1, fl1
-        kname = "conv1x1DmaKernel (1x1 GEMM, fp16, 384- or 192-row tiles as tuned)"
+    kind = 0 if ms3 >= ms1 else 1
+    ms_k, n_k, fl_k = (ms3, n3, fl3) if kind == 0 else (ms1, n1, fl1)
+    ran = sorted((r for r in per_kernel if r[0] == kind), key=lambda r: -r[2])
+    kname = "; ".join(f"{r[4]} x{r[1] // prof_steps}" for r in ran) + " per forward"
     avg_ms = ms_k / max(n_k, 1)
     achieved = (fl_k / max(n_k, 1)) / (avg_ms * 1e-3) / 1e12 if n_k else 0.0
     name = cfg.arch.name.replace("-synthetic", "")
@@ -448,6 +446,9 @@ def main():
                       "ms_3x3": round(ms3 / prof_steps, 4), "ms_1x1": round(ms1 / prof_steps, 4),
                       "what": "sum of direct-conv FLOPs of every 3x3 and 1x1 conv launch over the sum of their durations "
                               "(HIP events), per forward"},
+        "kernels_per_forward": [{"kernel": r[4], "kind": ("3x3", "1x1", "other")[r[0]], "launches": r[1] // prof_steps,
+                                 "us_per_launch": round(1000.0 * r[2] / r[1], 2),
+                                 "tflops": round(r[3] / (r[2] * 1e-3) / 1e12, 1) if r[2] > 0 else None} for r in per_kernel],
         "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(achieved, 2),
                      "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic() if headline else None, "avg_launch_ms": round(avg_ms, 5), "launches": n_k,

@@ -272,6 +272,11 @@ int kgh_handle_set_low_latency(kgh_handle* handle, int32_t enabled);
  * launches' algorithmic FLOPs (2*M*Cin*Cout*ky*kx each). */
 int kgh_handle_set_profiling(kgh_handle* handle, int32_t enabled);
 int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32_t* launches, double* flops);
+/* The same records per kernel: one text line per (kind, kernel) in order of
+ * first launch, "kind<TAB>launches<TAB>total_ms<TAB>flops<TAB>kernel", the
+ * kernel named with the template arguments that select it. No counterpart
+ * in the reference (a measurement aid like the two calls above). */
+int kgh_handle_profile_kernels(kgh_handle* handle, char* buf, int32_t len);
 
 /* Self-test of the matrix-core operand/result layout the conv kernels assume:
  * multiplies fixed 32x32x16 fp16 (and 32x32x2 fp32) tiles on device and

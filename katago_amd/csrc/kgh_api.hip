@@ -17,6 +17,7 @@
 #include <map>
 #include <sstream>
 #include <climits>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -485,6 +486,7 @@ namespace {
 struct ProfRec {
   int kind;  // 0 = 3x3 conv, 1 = 1x1 conv, 2 = other conv
   double flops;
+  const char* kernel = "";  // the kernel that ran (static string)
   hipEvent_t start, stop;
 };
 
@@ -657,7 +659,7 @@ struct Runner {
       if(h != nullptr && h->lowLatency && kgh::convSplitKApplies(ldx, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, g, e)) {
         ProfRec* rec = profStart(c);
         kgh::launchConvSplitK((const half_t*)x, ldx, c.cinPad, c.cout, (const half_t*)c.wPrep, g, e, h->splitWork, s);
-        if(rec != nullptr) KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
+        profStop(rec);
         return;
       }
     }
@@ -693,7 +695,13 @@ struct Runner {
     }
     ProfRec* rec = profStart(c);
     kgh::launchConv<T>(x, ldx, c.cin, c.cinPad, c.cout, c.ky, c.kx, c.wPrep, c.wDirect, g, e, s, nullptr, variant);
-    if(rec != nullptr) KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
+    profStop(rec);
+  }
+
+  void profStop(ProfRec* rec) {
+    if(rec == nullptr) return;
+    rec->kernel = kgh::lastConvKernel();
+    KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
   }
 
   // Starts the profiling record of a conv launch (null when not profiling).
@@ -2110,6 +2118,41 @@ int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32
     *total_ms = ms;
     *launches = cnt;
     *flops = fl;
+  });
+}
+
+int kgh_handle_profile_kernels(kgh_handle* handle, char* buf, int32_t len) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(!buf || len <= 0) invalid("null output");
+    KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
+    struct Sum {
+      int kind = 0, launches = 0;
+      double ms = 0, flops = 0;
+    };
+    std::vector<std::pair<std::string, Sum>> sums;  // in first-launch order
+    for(size_t i = 0; i < handle->profUsed; i++) {
+      const ProfRec& r = handle->prof[i];
+      float e = 0;
+      KGH_HIP_CHECK(hipEventElapsedTime(&e, r.start, r.stop));
+      auto it = std::find_if(sums.begin(), sums.end(), [&](const auto& p) { return p.first == r.kernel && p.second.kind == r.kind; });
+      if(it == sums.end()) {
+        sums.push_back({r.kernel, Sum{}});
+        it = sums.end() - 1;
+        it->second.kind = r.kind;
+      }
+      it->second.launches++;
+      it->second.ms += e;
+      it->second.flops += r.flops;
+    }
+    std::string text;
+    for(const auto& [name, sm] : sums) {
+      char line[96];
+      std::snprintf(line, sizeof(line), "%d\t%d\t%.9f\t%.17g\t", sm.kind, sm.launches, sm.ms, sm.flops);
+      text += line + name + "\n";
+    }
+    if((int32_t)text.size() >= len) invalid("kgh_handle_profile_kernels: buffer of " + std::to_string(len) + " bytes is too small");
+    std::memcpy(buf, text.c_str(), text.size() + 1);
   });
 }
 

@@ -17,9 +17,31 @@
 #include "kgh_common.h"
 
 #include <climits>
+#include <cstdio>
+#include <string>
 #include <type_traits>
 #include <cstdint>
 #include <vector>
+
+namespace kgh {
+// The kernel the calling thread's last conv launch ran (with the template
+// arguments that select it), for the per-launch profile records.
+thread_local const char* g_lastConvKernel = "";
+const char* lastConvKernel() { return g_lastConvKernel; }
+}  // namespace kgh
+
+namespace {
+
+template<typename... A>
+std::string kernelLabel(const char* fmt, A... a) {
+  char buf[160];
+  std::snprintf(buf, sizeof(buf), fmt, a...);
+  return buf;
+}
+
+template<typename T> const char* typeLabel() { return std::is_same<T, half_t>::value ? "fp16" : "fp32"; }
+
+}  // namespace
 
 namespace {
 
@@ -1760,6 +1782,8 @@ __global__ void convertToFloatKernel(const T* __restrict__ src, float* __restric
 template<typename T, int KS, int BN, int WM>
 void launchMfma(const T* x, int cinStride, int cinPad, int cout, const T* w, BoardGeom g, const ConvEpilogue<T>& epi,
                 hipStream_t stream) {
+  static const std::string name = kernelLabel("convMfmaKernel<%s, %dx%d, BN=%d, 128-row tiles>", typeLabel<T>(), KS, KS, BN);
+  kgh::g_lastConvKernel = name.c_str();
   int M = g.batch * g.H * g.W;
   dim3 grid((M + CONV_BM - 1) / CONV_BM, cout / BN);
   hipLaunchKernelGGL((convMfmaKernel<T, KS, BN, WM>), grid, dim3(CONV_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
@@ -1773,6 +1797,8 @@ constexpr int TW_WEIGHT_BUFFERS = 4;
 template<int BN, int RW = TW_ROW_WAVES, int NB = TW_WEIGHT_BUFFERS>
 void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                      const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  static const std::string name = kernelLabel("convTapWindowKernel<3x3 fp16, BN=%d, %d waves>", BN, RW * 2);
+  kgh::g_lastConvKernel = name.c_str();
   int M = g.batch * g.H * g.W;
   dim3 grid((M + TW_BM - 1) / TW_BM * (cout / BN));
   hipLaunchKernelGGL((convTapWindowKernel<BN, RW, NB>), grid, dim3(RW * 2 * 64), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
@@ -1782,6 +1808,9 @@ void launchTapWindow(const half_t* x, int cinStride, int cinPad, int cout, const
 template<int BN, int RW = BW_ROW_WAVES, int WT = BW_WTM>
 void launchBoardWindow(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                        const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  static const std::string name = kernelLabel("convBoardWindowKernel<3x3 fp16, BN=%d, %s, %d-row wave tiles>", BN,
+                                              RW == BW_ROW_WAVES ? "one board per workgroup" : "half a board per workgroup", WT);
+  kgh::g_lastConvKernel = name.c_str();
   dim3 grid(g.batch * (RW == BW_ROW_WAVES ? 1 : 2) * (cout / BN));
   hipLaunchKernelGGL((convBoardWindowKernel<BN, BN == 64 ? 9 : 6, false, RW, WT>), grid, dim3(128 * RW * BW_WTM / WT), 0, stream, x,
                      cinStride, cinPad, cout, w, g.batch, epi);
@@ -1868,6 +1897,7 @@ bool dispatchTapWindow<half_t>(const half_t* x, int cinStride, int cinPad, int c
 void launch1x1DmaGlu256(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                         const ConvEpilogue<half_t>& epi, hipStream_t stream) {
   if(!epi.glu || cout % 256 != 0) throw KghError(5, "256-column 1x1 kernel: gated convs with a multiple of 256 columns only");
+  kgh::g_lastConvKernel = "conv1x1DmaKernel<1x1 fp16, BN=256, gated, BM=384>";
   const int M = g.batch * g.H * g.W;
   dim3 grid((M + 383) / 384 * (cout / 256)), block(512);
   hipLaunchKernelGGL((conv1x1DmaKernel<256, true, 384>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
@@ -1877,6 +1907,9 @@ void launch1x1DmaGlu256(const half_t* x, int cinStride, int cinPad, int cout, co
 template<int BN, int BM = 384>
 void launch1x1Dma(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                   const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  static const std::string name = kernelLabel("conv1x1DmaKernel<1x1 fp16, BN=%d, BM=%d>", BN, BM);
+  static const std::string gname = kernelLabel("conv1x1DmaKernel<1x1 fp16, BN=%d, gated, BM=%d>", BN, BM);
+  kgh::g_lastConvKernel = epi.glu ? gname.c_str() : name.c_str();
   int M = g.batch * g.H * g.W;
   dim3 grid((M + BM - 1) / BM * (cout / BN)), block(BM / 48 * 64);
   if(epi.glu) hipLaunchKernelGGL((conv1x1DmaKernel<BN, true, BM>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
@@ -1899,6 +1932,8 @@ bool allK1x1Fits(int cinStride, int cinPad, int cout, int bn, BoardGeom g) {
 template<int BN>
 void launch1x1AllK(const half_t* x, int cinStride, int cinPad, int cout, const half_t* w, BoardGeom g,
                    const ConvEpilogue<half_t>& epi, hipStream_t stream) {
+  static const std::string name = kernelLabel("conv1x1AllKKernel<1x1 fp16, BN=%d>", BN);
+  kgh::g_lastConvKernel = name.c_str();
   const int M = g.batch * g.H * g.W;
   dim3 grid((M + SMALL1_BM - 1) / SMALL1_BM * (cout / BN)), block(BN / 32 * 128);
   if(epi.glu) hipLaunchKernelGGL((conv1x1AllKKernel<BN, true>), grid, block, 0, stream, x, cinStride, cinPad, cout, w, g, epi);
@@ -2138,6 +2173,7 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
       throw KghError(5, "conv: the gated epilogue takes only gated outputs in blocks of 16 columns");
     long total = (long)g.batch * g.H * g.W * ((cout - epi.actBegin) / 2);
     long blocks = (total + threads - 1) / threads;
+    kgh::g_lastConvKernel = std::is_same<T, half_t>::value ? "convDirectGluKernel<fp16>" : "convDirectGluKernel<fp32>";
     hipLaunchKernelGGL(convDirectGluKernel<T>, dim3((unsigned)blocks), dim3(threads), 0, stream, x, cinStride, cin, cout, ky, kx,
                        wDirect, g, epi);
     KGH_CHECK_LAUNCH();
@@ -2145,6 +2181,7 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
   }
   long total = (long)g.batch * g.H * g.W * cout;
   long blocks = (total + threads - 1) / threads;
+  kgh::g_lastConvKernel = std::is_same<T, half_t>::value ? "convDirectKernel<fp16>" : "convDirectKernel<fp32>";
   hipLaunchKernelGGL(convDirectKernel<T>, dim3((unsigned)blocks), dim3(threads), 0, stream, x, cinStride, cin, cout, ky, kx,
                      wDirect, g, epi);
   KGH_CHECK_LAUNCH();
@@ -2167,6 +2204,7 @@ void launchConvSplitK(const half_t* x, int cinStride, int cinPad, int cout, cons
   const int splits = splitKCount(cinPad);
   // Half boards with 32-row wave tiles: at one board, 2 x 3 x 6 = 36
   // workgroups of 12 waves for a 192-channel conv.
+  kgh::g_lastConvKernel = "convBoardWindowKernel<3x3 fp16, split-K, half a board per workgroup> + splitKEpilogueKernel";
   hipLaunchKernelGGL((convBoardWindowKernel<SPLITK_BN, 9, true, 2, 32>), dim3(g.batch * 2 * (cout / SPLITK_BN), splits), dim3(128 * 2 * 3),
                      0, stream, x, cinStride, cinPad, cout, w, g.batch, epi, work);
   KGH_CHECK_LAUNCH();

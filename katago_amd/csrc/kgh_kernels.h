@@ -143,6 +143,11 @@ struct PrepareBoardsArgs {
 
 namespace kgh {
 
+// The kernel the calling thread's last conv launch ran, with the template
+// arguments that select it (a static string).
+const char* lastConvKernel();
+
+
 // Per-board input preparation (one launch): rows packed with the symmetry
 // applied, the on-board mask and its sum, and the stem's global-input bias.
 template<typename T>

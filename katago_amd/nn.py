@@ -537,6 +537,19 @@ class DeviceHandle:
         hip_check(hip_library().kgh_handle_profile(self._ptr, kind, ctypes.byref(ms), ctypes.byref(cnt), ctypes.byref(fl)))
         return ms.value, cnt.value, fl.value
 
+    def profile_kernels(self):
+        """kgh_handle_profile_kernels: [(kind, launches, total_ms, flops,
+        kernel)] per kernel that ran, in order of first launch."""
+        lib = hip_library()
+        lib.kgh_handle_profile_kernels.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int32]
+        buf = ctypes.create_string_buffer(1 << 16)
+        hip_check(lib.kgh_handle_profile_kernels(self._ptr, buf, len(buf)))
+        rows = []
+        for line in buf.value.decode().splitlines():
+            kind, launches, ms, flops, name = line.split("\t", 4)
+            rows.append((int(kind), int(launches), float(ms), float(flops), name))
+        return rows
+
     def close(self):
         if getattr(self, "_ptr", None) and self._ptr.value:
             hip_library().kgh_handle_free(self._ptr)

@@ -457,3 +457,33 @@ def test_errors_are_raised_not_crashed(model_dir):
         h.get_output(sp, gl)
     with pytest.raises(nn.StringError, match="symmetry"):
         h.get_output(sp[:1], gl[:1], symmetry=[9])
+
+
+def test_profile_records_name_the_kernels_that_ran(model_dir):
+    """kgh_handle_profile_kernels: per-kernel records that add up to the
+    kgh_handle_profile totals of each kind, naming the kernel each launch
+    ran (C3's net at 8 mixed boards: tap-window 3x3 kernels, 1x1 kernels)."""
+    cfg = modelgen.configs()[3]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    dm = nn.DeviceModel(lm, use_fp16=True)
+    n = 8
+    h = nn.DeviceHandle(dm, n)
+    sp, gl = modelgen.synthetic_inputs(3, n, board_sizes=(9, 13, 19))
+    bufs = [nn.DeviceBuffer.from_array(a) for a in (sp, gl, np.zeros(n, np.int32), np.zeros(n, np.float32))]
+    out = nn.DeviceBuffer(n * h.row_floats * 4)
+    h.set_profiling(True)
+    for _ in range(2):
+        h.forward_device(n, *(b.ptr for b in bufs), out.ptr)
+    h.synchronize()
+    rows = h.profile_kernels()
+    totals = [h.profile(kind) for kind in (0, 1)]
+    h.set_profiling(False)
+    assert rows and all(r[4] for r in rows)
+    for kind in (0, 1):
+        ms, cnt, fl = totals[kind]
+        mine = [r for r in rows if r[0] == kind]
+        assert cnt > 0 and sum(r[1] for r in mine) == cnt
+        assert abs(sum(r[2] for r in mine) - ms) <= 1e-6 * max(ms, 1.0)
+        assert abs(sum(r[3] for r in mine) - fl) <= 1e-12 * fl
+    assert any(r[4].startswith("conv") and "3x3" in r[4] for r in rows if r[0] == 0), rows
+    assert any("1x1" in r[4] for r in rows if r[0] == 1), rows
