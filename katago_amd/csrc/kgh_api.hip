@@ -235,7 +235,7 @@ struct Builder {
     bool shapeOk = (ky == kx) && (ky == 1 || ky == 3);
     bool mfmaOk = fp16 ? kgh::convMfmaSupported<half_t>(c.cinPad, cout) : kgh::convMfmaSupported<float>(c.cinPad, cout);
     if(shapeOk && mfmaOk) {
-      size_t count = (size_t)ky * kx * cout * c.cinPad;
+      size_t count = kgh::preparedConvWeightElems(fp16, ky, kx, cout, c.cinPad);
       if(fp16) {
         half_t* p = arena.allocN<half_t>(count);
         kgh::prepareConvWeights<half_t>(dW, p, cout, cin, c.cinPad, ky, kx, stream);

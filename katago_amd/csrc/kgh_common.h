@@ -327,6 +327,11 @@ void launchConvSplitK(const half_t* x, int cinStride, int cinPad, int cout, cons
 // of type T on device (zero-padded channels).
 template<typename T>
 void prepareConvWeights(const float* dWeightsOIYX, T* dOut, int cout, int cin, int cinPad, int ky, int kx, hipStream_t stream);
+// Elements prepareConvWeights writes: ky*kx*cout*cinPad, and for fp32 3x3
+// convs with cinPad a multiple of 16 and cout of 32 as many again, the
+// layout of the fp32 3x3 kernel (each wave's weight fragments of a step one
+// contiguous 2 KB run) following the first.
+size_t preparedConvWeightElems(bool fp16, int ky, int kx, int cout, int cinPad);
 
 template<typename T>
 void launchConvertFromFloat(const float* src, T* dst, size_t n, hipStream_t stream);

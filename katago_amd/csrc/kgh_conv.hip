@@ -493,6 +493,178 @@ __global__ __launch_bounds__(CONV_THREADS, 3) void convMfmaKernel(const T* __res
 }
 
 // ---------------------------------------------------------------------------
+// fp32 3x3 convolution, every batch size. A workgroup of eight wave64s owns
+// one 32-row x 32-column output block. Its input window (the block's rows
+// and one board row plus one position either side, all input channels) is
+// loaded into LDS once with coalesced 16-byte loads; rows are padded by four
+// floats, so the 16 lanes of a ds_read_b128 phase (16 rows, one channel
+// offset) fall in distinct banks. The K steps (16 input channels of one
+// tap, chunk outer and tap inner as in the other kernels) are dealt to the
+// waves round-robin, wave w taking steps w, w + 8, ..., so each wave's chain
+// of dependent matrix instructions is an eighth of K and two waves share a
+// SIMD. For instruction j of a step, lane l supplies A[row l % 32 shifted by
+// the tap][channel c0 + 8 (l / 32) + j] from the window (a tap that leaves
+// the board reads zero) and the matching weight from L2 through a ring of
+// eight steps of registers. The epilogue's operands (residual, mask,
+// per-board bias, scale and bias of the activation) are loaded before the K
+// loop. The eight partial sums are added in LDS in wave order ((w0 + w1) +
+// w2) + ... + w7, and each wave stores two of the sixteen result registers.
+// The rows round the same way whatever the batch (the dispatch sends every
+// fp32 3x3 conv of a given epilogue kind here), and a launch has
+// ceil(M / 32) x cout / 32 workgroups: 273 for b6c96 at eight boards,
+// against 69 for the 128-row tile kernel, whose waves each walk all of K
+// with one step of prefetch.
+constexpr int F32S_WAVES = 8;
+constexpr int F32S_THREADS = 64 * F32S_WAVES;
+constexpr int F32S_DEPTH = 8;             // register ring of weight steps loaded ahead
+constexpr int F32S_LDS_FLOATS = 16384;    // 64 KB of dynamic LDS: window rows x (cinPad + 4)
+
+__host__ __device__ constexpr int f32sWindowRows(int W) { return 32 + 2 * (W + 1); }
+
+template<int KS>
+__global__ __launch_bounds__(F32S_THREADS) void convF32SplitKernel(const float* __restrict__ x, int cinStride, int cinPad,
+                                                                   int cout, const float* __restrict__ w, BoardGeom g,
+                                                                   ConvEpilogue<float> epi) {
+  extern __shared__ __attribute__((aligned(16))) float f32sLds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int HW = g.H * g.W;
+  const int M = g.batch * HW;
+  const int m0 = blockIdx.x * 32;
+  const int n0 = blockIdx.y * 32;
+  const int r = lane & 31;
+  const int h = lane >> 5;
+  const int ld = cinPad + 4;
+  const int halo = g.W + 1;
+  const int winRows = 32 + 2 * halo;
+
+  // Window row i holds input row m0 - halo + i (zero outside 0..M-1). A
+  // thread issues up to eight loads before its first LDS write, so the
+  // window costs one memory latency (the previous kernel's outputs come from
+  // other XCDs' write-backs, not from this L2).
+  {
+    constexpr int U = 8;
+    const int vecs = cinPad / 4;
+    const int total = winRows * vecs;
+    for(int base = 0; base < total; base += U * F32S_THREADS) {
+      float4 val[U];
+#pragma unroll
+      for(int u = 0; u < U; u++) {
+        const int v = base + u * F32S_THREADS + threadIdx.x;
+        const int i = v / vecs;
+        const int src = m0 - halo + i;
+        val[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if(v < total && src >= 0 && src < M) val[u] = *(const float4*)(x + (size_t)src * cinStride + (v - i * vecs) * 4);
+      }
+#pragma unroll
+      for(int u = 0; u < U; u++) {
+        const int v = base + u * F32S_THREADS + threadIdx.x;
+        const int i = v / vecs;
+        if(v < total) *(float4*)&f32sLds[i * ld + (v - i * vecs) * 4] = val[u];
+      }
+    }
+  }
+
+  // This lane's A row (clamped past M: its outputs are never stored).
+  const int m = min(m0 + r, M - 1);
+  const int sp = m % HW;
+  const int y = sp / g.W;
+  const int xc = sp - y * g.W;
+  // w is the split layout (prepareF32SplitWeightsKernel): this block's 2 KB
+  // per (tap, chunk), lane l's vectors at l * 4 and 256 + l * 4.
+  const int chunks = cinPad / 16;
+  const float* wBlk = w + (size_t)blockIdx.y * 512 + lane * 4;
+  const int kIters = KS * KS * chunks;
+  const int steps = kIters > wave ? (kIters - wave + F32S_WAVES - 1) / F32S_WAVES : 0;
+
+  // Epilogue operands of the two result registers this wave stores.
+  constexpr int QW = 16 / F32S_WAVES;
+  const int col = n0 + r;
+  float eRes[QW], eMask[QW], eNc[QW];
+  int eRow[QW];
+#pragma unroll
+  for(int qq = 0; qq < QW; qq++) {
+    const int q = wave * QW + qq;
+    // Result register q of lane l: C[(q / 4) * 8 + (l / 32) * 4 + q % 4][l % 32].
+    eRow[qq] = m0 + (q >> 2) * 8 + h * 4 + (q & 3);
+    const int rowc = min(eRow[qq], M - 1);
+    eMask[qq] = epi.mask != nullptr ? epi.mask[rowc] : 1.0f;
+    eRes[qq] = epi.residual != nullptr ? epi.residual[(size_t)rowc * epi.ldRes + col] : 0.0f;
+    eNc[qq] = epi.ncBias != nullptr ? epi.ncBias[(size_t)(rowc / HW) * epi.ldNC + col] : 0.0f;
+  }
+  const bool actCol = epi.outAct != nullptr && col >= epi.actBegin;
+  const float eScale = actCol ? epi.actScale[col - epi.actBegin] : 1.0f;
+  const float eBias = actCol ? epi.actBias[col - epi.actBegin] : 0.0f;
+
+  float4 rb[F32S_DEPTH][2];
+  auto loadW = [&](int i, float4 (&b)[2]) {
+    const int k = wave + F32S_WAVES * min(i, steps - 1);
+    const int chunk = k / (KS * KS);
+    const int tap = k - chunk * (KS * KS);
+    const float* bp = wBlk + ((size_t)tap * chunks + chunk) * (cout / 32) * 512;
+    b[0] = *(const float4*)bp;
+    b[1] = *(const float4*)(bp + 256);
+  };
+  if(steps > 0) {
+#pragma unroll
+    for(int d = 0; d < F32S_DEPTH; d++) loadW(d, rb[d]);
+  }
+  __syncthreads();
+
+  floatx16 acc;
+#pragma unroll
+  for(int q = 0; q < 16; q++) acc[q] = 0.0f;
+  auto step = [&](int i, const float4 (&b)[2]) {
+    const int k = wave + F32S_WAVES * i;
+    const int chunk = k / (KS * KS);
+    const int tap = k - chunk * (KS * KS);
+    const int dy = tap / KS - KS / 2;
+    const int dx = tap % KS - KS / 2;
+    const int yy = y + dy;
+    const int xx = xc + dx;
+    const bool ok = yy >= 0 && yy < g.H && xx >= 0 && xx < g.W;
+    const float* ap = &f32sLds[(r + halo + dy * g.W + dx) * ld + chunk * 16 + 8 * h];
+    float4 a[2];
+    a[0] = *(const float4*)ap;
+    a[1] = *(const float4*)(ap + 4);
+    const float* af = (const float*)a;
+    const float* bf = (const float*)b;
+#pragma unroll
+    for(int j = 0; j < 8; j++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ok ? af[j] : 0.0f, bf[j], acc, 0, 0, 0);
+  };
+  if(steps > 0) {
+    for(int i = 0; i < steps; i += F32S_DEPTH) {
+#pragma unroll
+      for(int d = 0; d < F32S_DEPTH; d++) {
+        if(i + d < steps) step(i + d, rb[d]);
+        // The slot just used takes the step a ring ahead; the loads are
+        // issued (clamped to the last step) whenever any remain, so the
+        // waits before each step count the same loads on every path.
+        if(i + F32S_DEPTH < steps) loadW(i + d + F32S_DEPTH, rb[d]);
+      }
+    }
+  }
+  __syncthreads();
+  float* part = f32sLds;  // [wave][16][64], the window is no longer read
+#pragma unroll
+  for(int q = 0; q < 16; q++) part[(wave * 16 + q) * 64 + lane] = acc[q];
+  __syncthreads();
+#pragma unroll
+  for(int qq = 0; qq < QW; qq++) {
+    const int q = wave * QW + qq;
+    float v = part[q * 64 + lane];
+#pragma unroll
+    for(int ww = 1; ww < F32S_WAVES; ww++) v += part[(ww * 16 + q) * 64 + lane];
+    const int row = eRow[qq];
+    if(row >= M) continue;
+    v += eNc[qq];
+    if(epi.residual != nullptr) v = epi.maskResidualAdd ? eRes[qq] + v * eMask[qq] : eRes[qq] + v;
+    if(col < epi.rawEnd) epi.outRaw[(size_t)row * epi.ldRaw + col] = v;
+    if(actCol) epi.outAct[(size_t)row * epi.ldAct + col - epi.actBegin] = kgh_activate(v * eScale + eBias, epi.actKind) * eMask[qq];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 3x3 fp16 convolution for large batches: input window staged once per
 // channel chunk, weights streamed per tap, both by direct global->LDS DMA.
 //
@@ -1751,6 +1923,31 @@ __global__ void convDirectGluKernel(const T* __restrict__ x, int cinStride, int 
   epi.outAct[(size_t)m * epi.ldAct + o] = kgh_from_float<T>(kgh_activate(accV, epi.actKind) * accG);
 }
 
+// The fp32 3x3 kernel's weight layout: for each (tap, 16-channel chunk,
+// 32-column block) 512 floats, float4 (q, h, n) at ((q * 2 + h) * 32 + n) * 4
+// holding column n's channels 8 h + 4 q .. + 3 of the chunk, so lane
+// l = 32 h + n of a wave reads its two fragment vectors at l * 4 and
+// 256 + l * 4: one contiguous 1 KB run per load instruction.
+__global__ void prepareF32SplitWeightsKernel(const float* __restrict__ src, float* __restrict__ dst, int cout, int cin, int cinPad) {
+  const long total = 9L * cout * cinPad;
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if(idx >= total) return;
+  const int e = (int)(idx & 3);
+  const int n = (int)((idx >> 2) & 31);
+  const int h = (int)((idx >> 7) & 1);
+  const int q = (int)((idx >> 8) & 1);
+  const long blk = idx >> 9;
+  const int nblocks = cout / 32;
+  const int nb = (int)(blk % nblocks);
+  const long rest = blk / nblocks;
+  const int chunks = cinPad / 16;
+  const int chunk = (int)(rest % chunks);
+  const int tap = (int)(rest / chunks);
+  const int oc = nb * 32 + n;
+  const int ic = chunk * 16 + 8 * h + 4 * q + e;
+  dst[idx] = ic < cin ? src[(((size_t)oc * cin + ic) * 3 + tap / 3) * 3 + tap % 3] : 0.0f;
+}
+
 template<typename T>
 __global__ void prepareConvWeightsKernel(const float* __restrict__ src, T* __restrict__ dst, int cout, int cin, int cinPad,
                                          int ky, int kx) {
@@ -1787,6 +1984,25 @@ void launchMfma(const T* x, int cinStride, int cinPad, int cout, const T* w, Boa
   int M = g.batch * g.H * g.W;
   dim3 grid((M + CONV_BM - 1) / CONV_BM, cout / BN);
   hipLaunchKernelGGL((convMfmaKernel<T, KS, BN, WM>), grid, dim3(CONV_THREADS), 0, stream, x, cinStride, cinPad, cout, w, g, epi);
+  KGH_CHECK_LAUNCH();
+}
+
+// The fp32 split kernel takes every fp32 3x3 conv whose epilogue is the
+// plain contract (no folded RMSNorm, rotary embedding or gated outputs).
+bool f32SplitFits(int ky, int kx, int cinStride, int cinPad, int cout, BoardGeom g, const ConvEpilogue<float>& epi) {
+  return ky == 3 && kx == 3 && cinPad % 16 == 0 && cinStride % 4 == 0 && cout % 32 == 0 && epi.sumSqOut == nullptr &&
+         epi.rowNormIn == nullptr && epi.ropeEnd == 0 && !epi.glu && f32sWindowRows(g.W) * (cinPad + 4) <= F32S_LDS_FLOATS;
+}
+
+void launchF32Split(const float* x, int cinStride, int cinPad, int cout, const float* w, BoardGeom g, const ConvEpilogue<float>& epi,
+                    hipStream_t stream) {
+  const int M = g.batch * g.H * g.W;
+  dim3 grid((M + 31) / 32, cout / 32);
+  // The window, or the eight waves' partial sums (32 KB), whichever is larger.
+  const size_t lds = std::max<size_t>((size_t)f32sWindowRows(g.W) * (cinPad + 4), F32S_WAVES * 16 * 64) * sizeof(float);
+  kgh::g_lastConvKernel = "convF32SplitKernel<3x3 fp32, 32 x 32 blocks, K over 8 waves, LDS window>";
+  hipLaunchKernelGGL((convF32SplitKernel<3>), grid, dim3(F32S_THREADS), lds, stream, x, cinStride, cinPad, cout,
+                     w + (size_t)9 * cout * cinPad, g, epi);
   KGH_CHECK_LAUNCH();
 }
 
@@ -2125,6 +2341,9 @@ template<typename T>
 bool convVariantApplies(int variant, const T* x, int cinStride, int cinPad, int cout, int ky, int kx, const void* wPrepared,
                         BoardGeom g, const ConvEpilogue<T>& epi) {
   (void)x;
+  if constexpr(std::is_same<T, float>::value) {
+    if(wPrepared != nullptr && f32SplitFits(ky, kx, cinStride, cinPad, cout, g, epi)) return false;
+  }
   return variant > CONV_AUTO && variant < CONV_VARIANT_COUNT && mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
          variantFits<T>(variant, ky, cinStride, cinPad, cout, g, epi);
 }
@@ -2150,6 +2369,14 @@ void launchConv(const T* x, int cinStride, int cin, int cinPad, int cout, int ky
   if(epi.ropeEnd > 0 && !convRopeOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi))
     throw KghError(5, "conv: a rotary embedding in the epilogue needs the matrix-core kernels and head dims multiples of 16");
   bool done = false;
+  if constexpr(std::is_same<T, float>::value) {
+    if(wPrepared != nullptr && mfmaPathOk<T>(cinStride, cinPad, cout, ky, kx, wPrepared, epi) &&
+       f32SplitFits(ky, kx, cinStride, cinPad, cout, g, epi)) {
+      launchF32Split(x, cinStride, cinPad, cout, (const float*)wPrepared, g, epi, stream);
+      if(usedMfma != nullptr) *usedMfma = true;
+      return;
+    }
+  }
   if(variant != CONV_AUTO && convVariantApplies<T>(variant, x, cinStride, cinPad, cout, ky, kx, wPrepared, g, epi)) {
     launchVariant<T>(variant, ky, x, cinStride, cinPad, cout, (const T*)wPrepared, g, epi, stream);
     done = true;
@@ -2218,12 +2445,26 @@ void launchConvSplitK(const half_t* x, int cinStride, int cinPad, int cout, cons
   KGH_CHECK_LAUNCH();
 }
 
+bool f32SplitWeights(int ky, int kx, int cinPad, int cout) { return ky == 3 && kx == 3 && cinPad % 16 == 0 && cout % 32 == 0; }
+
+size_t preparedConvWeightElems(bool fp16, int ky, int kx, int cout, int cinPad) {
+  const size_t n = (size_t)ky * kx * cout * cinPad;
+  return !fp16 && f32SplitWeights(ky, kx, cinPad, cout) ? 2 * n : n;
+}
+
 template<typename T>
 void prepareConvWeights(const float* dW, T* dOut, int cout, int cin, int cinPad, int ky, int kx, hipStream_t stream) {
   long total = (long)ky * kx * cout * cinPad;
   hipLaunchKernelGGL(prepareConvWeightsKernel<T>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, dW, dOut, cout,
                      cin, cinPad, ky, kx);
   KGH_CHECK_LAUNCH();
+  if constexpr(std::is_same<T, float>::value) {
+    if(f32SplitWeights(ky, kx, cinPad, cout)) {
+      hipLaunchKernelGGL(prepareF32SplitWeightsKernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, dW,
+                         (float*)dOut + total, cout, cin, cinPad);
+      KGH_CHECK_LAUNCH();
+    }
+  }
 }
 
 template<typename T>

@@ -487,3 +487,22 @@ def test_profile_records_name_the_kernels_that_ran(model_dir):
         assert abs(sum(r[3] for r in mine) - fl) <= 1e-12 * fl
     assert any(r[4].startswith("conv") and "3x3" in r[4] for r in rows if r[0] == 0), rows
     assert any("1x1" in r[4] for r in rows if r[0] == 1), rows
+
+
+@pytest.mark.parametrize("cfg_index", [0, 1], ids=["b6c96", "b10c128"])
+def test_fp32_rows_do_not_depend_on_batch_size(model_dir, cfg_index):
+    """fp32 contexts: every 3x3 conv runs the fp32 split kernel (32 x 32
+    output blocks, K dealt over eight waves, partial sums added in wave order)
+    at every batch size, so a board's row is bitwise the same in every batch
+    that holds it, also across the 32-row block boundaries a batch moves."""
+    cfg = modelgen.configs()[cfg_index]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    n_max = 64
+    h = nn.ComputeHandle(nn.ComputeContext(lm, 19, 19, use_fp16=False), max_batch=n_max)
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, n_max, board_sizes=(19, 9, 13))
+    sym = np.arange(n_max) % 8
+    full = h.get_output(sp, gl, symmetry=sym)
+    for n in (1, 2, 3, 8, 13, 31, 33, 64):
+        out = h.get_output(sp[:n], gl[:n], symmetry=sym[:n])
+        for k in full:
+            assert np.array_equal(out[k], full[k][:n]), f"batch {n} vs {n_max}, {k}: max-abs {np.abs(out[k] - full[k][:n]).max()}"
