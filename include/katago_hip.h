@@ -272,6 +272,21 @@ int kgh_handle_set_low_latency(kgh_handle* handle, int32_t enabled);
  * launches' algorithmic FLOPs (2*M*Cin*Cout*ky*kx each). */
 int kgh_handle_set_profiling(kgh_handle* handle, int32_t enabled);
 int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32_t* launches, double* flops);
+/* Per-block trunk dump, the runtime counterpart of the reference's
+ * DEBUG_INTERMEDIATE_VALUES prints (debugprint.h:14-49, used at
+ * eigenbackend.cpp:1773-1785): while enabled, forwards run without graph
+ * replay and record one line per tensor in DebugPrint::print3DSummary's
+ * format ("DEBUG <name> [NSC NxSxC] valid= min= max= mean= rms= first8= ..."):
+ * the trunk before each top-level block ("HIP Blockstack block <i>"), after
+ * the last block ("HIP Trunk after blocks") and after the tip norm and
+ * activation ("HIP Trunk tip"), statistics over on-board positions. Values
+ * are multiplied by value_scale first: pass the model's
+ * outputScaleMultiplier to undo the load-time scale-by-8 and compare with an
+ * unscaled (Eigen-style) run. kgh_handle_layer_dump copies the last forward's
+ * lines (KGH_ERR_INVALID_ARGUMENT if buf is too small). */
+int kgh_handle_set_layer_dump(kgh_handle* handle, int32_t enabled, float value_scale);
+int kgh_handle_layer_dump(kgh_handle* handle, char* buf, int32_t len);
+
 /* The same records per kernel: one text line per (kind, kernel) in order of
  * first launch, "kind<TAB>launches<TAB>total_ms<TAB>flops<TAB>kernel", the
  * kernel named with the template arguments that select it. No counterpart

@@ -549,6 +549,12 @@ struct kgh_handle {
   std::vector<ProfRec> prof;
   size_t profUsed = 0;
 
+  // Per-block trunk dump (kgh_handle_set_layer_dump): summary lines of the
+  // last forward, values times dumpScale.
+  bool layerDump = false;
+  float dumpScale = 1.0f;
+  std::string dumpText;
+
   // Captured forwards, keyed by batch size and the five row buffers.
   struct GraphEntry {
     int n = 0;
@@ -613,6 +619,37 @@ namespace {
 
 // ---------------------------------------------------------------------------
 // Forward execution.
+
+// One summary line of an [N][S][C] tensor, as DebugPrint::print3DSummary
+// prints it (debugprint.cpp:14-76,78-132): element count, minimum, maximum,
+// mean and root mean square over the positions whose mask is nonzero, then
+// the first eight values of the buffer.
+std::string summaryLine(const std::string& name, const float* data, int N, int S, int C, const float* mask) {
+  int valid = 0;
+  float mn = 1e30f, mx = -1e30f;
+  double sum = 0.0, sq = 0.0;
+  for(int p = 0; p < N * S; p++) {
+    if(mask[p] == 0.0f) continue;
+    for(int c = 0; c < C; c++) {
+      const float v = data[(size_t)p * C + c];
+      valid++;
+      mn = std::min(mn, v);
+      mx = std::max(mx, v);
+      sum += v;
+      sq += (double)v * v;
+    }
+  }
+  if(valid == 0) mn = mx = 0.0f;
+  char line[512];
+  int len = std::snprintf(line, sizeof(line), "DEBUG %s [NSC %dx%dx%d] valid=%d min=%.6g max=%.6g mean=%.6g rms=%.6g first8=", name.c_str(),
+                          N, S, C, valid, mn, mx, valid ? sum / valid : 0.0, valid ? std::sqrt(sq / valid) : 0.0);
+  std::string out(line, (size_t)std::max(0, std::min(len, (int)sizeof(line) - 1)));
+  for(int i = 0; i < 8 && i < N * S * C; i++) {
+    std::snprintf(line, sizeof(line), " %.6g", data[i]);
+    out += line;
+  }
+  return out + "\n";
+}
 
 template<typename T>
 struct Runner {
@@ -704,6 +741,21 @@ struct Runner {
     KGH_HIP_CHECK(hipEventRecord(rec->stop, s));
   }
 
+  // Appends the summary line of a [M][C] activation (row stride C) to the
+  // handle's dump when dumping: the statistics of DebugPrint::print3DSummary
+  // (debugprint.cpp:78-132) over the positions the mask keeps.
+  void dumpTensor(const std::string& name, const T* buf, int C) {
+    if(h == nullptr || !h->layerDump) return;
+    std::vector<T> v((size_t)M * C);
+    std::vector<float> mk(M);
+    KGH_HIP_CHECK(hipMemcpyAsync(v.data(), buf, v.size() * sizeof(T), hipMemcpyDeviceToHost, s));
+    KGH_HIP_CHECK(hipMemcpyAsync(mk.data(), mask, mk.size() * sizeof(float), hipMemcpyDeviceToHost, s));
+    KGH_HIP_CHECK(hipStreamSynchronize(s));
+    std::vector<float> f(v.size());
+    for(size_t i = 0; i < v.size(); i++) f[i] = (float)v[i] * h->dumpScale;
+    h->dumpText += summaryLine(name, f.data(), g.batch, g.H * g.W, C, mk.data());
+  }
+
   // Starts the profiling record of a conv launch (null when not profiling).
   ProfRec* profStart(const ConvW& c) {
     if(h == nullptr || !h->profiling) return nullptr;
@@ -737,6 +789,7 @@ struct Runner {
   // after it folds its norm.
   void runStack(const std::vector<Block>& blocks, int depth, const BNAct* tail, bool rawLive = true, bool sqIn = false) {
     for(size_t i = 0; i < blocks.size(); i++) {
+      if(depth == 0) dumpTensor("HIP Blockstack block " + std::to_string(i), R[0], net.trunkC);
       const bool last = i + 1 == blocks.size();
       const BNAct* next = !last ? (isConvKind(blocks[i + 1]) ? &blocks[i + 1].preBN : nullptr) : tail;
       sqIn = runBlock(blocks[i], depth, next, !last || rawLive, sqIn, !last && normFolds(blocks[i + 1]));
@@ -1030,7 +1083,11 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
     stemSq = r.recordSq(e, net.initialConv, net.inputCPad, net.trunkC, Runner<T>::normFolds(net.blocks[0]));
     r.conv(net.initialConv, (const T*)h->x0, net.inputCPad, e);
   }
-  r.runStack(net.blocks, 0, net.tipKind == 0 ? &net.tipBN : nullptr, net.tipKind != 0, stemSq);
+  if(h->layerDump) h->dumpText.clear();
+  // The raw trunk after the last block is stored only when something reads
+  // it: the RMSNorm tip, or the dump.
+  r.runStack(net.blocks, 0, net.tipKind == 0 ? &net.tipBN : nullptr, net.tipKind != 0 || h->layerDump, stemSq);
+  r.dumpTensor("HIP Trunk after blocks", r.R[0], net.trunkC);
   if(net.tipKind != 0) {
     // Trunk-tip RMSNorm + activation into A[0], the heads' input.
     if(net.tipSpatial)
@@ -1040,6 +1097,8 @@ void forwardImpl(kgh_handle* h, int n, const float* dSpatial, const float* dGlob
       kgh::launchRmsNorm<T>(r.R[0], net.trunkC, r.A[0], net.trunkC, net.trunkC, net.tipGamma, net.tipBeta, net.tipEps, net.tipAct,
                             h->mask, n * HW, s);
   }
+
+  r.dumpTensor("HIP Trunk tip", r.A[0], net.trunkC);
 
   // Heads: 1x1 convs p1 | g1 | v1 from the activated trunk tip.
   T* p1 = (T*)h->p1;
@@ -1181,7 +1240,7 @@ void runForward(kgh_handle* h, int n, const float* sp, const float* gl, const in
     if(h->model->net.fp16) forwardImpl<half_t>(h, n, sp, gl, sym, opt, out);
     else forwardImpl<float>(h, n, sp, gl, sym, opt, out);
   };
-  if(!h->graphsEnabled || h->profiling) {
+  if(!h->graphsEnabled || h->profiling || h->layerDump) {
     eager();
     return;
   }
@@ -2118,6 +2177,28 @@ int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32
     *total_ms = ms;
     *launches = cnt;
     *flops = fl;
+  });
+}
+
+int kgh_handle_set_layer_dump(kgh_handle* handle, int32_t enabled, float value_scale) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(!(value_scale > 0.0f)) invalid("value_scale must be positive");
+    KGH_HIP_CHECK(hipStreamSynchronize(handle->stream));
+    handle->layerDump = enabled != 0;
+    handle->dumpScale = value_scale;
+    handle->dumpText.clear();
+  });
+}
+
+int kgh_handle_layer_dump(kgh_handle* handle, char* buf, int32_t len) {
+  return guarded([&] {
+    requireHandle(handle);
+    if(!buf || len <= 0) invalid("null output");
+    if((int32_t)handle->dumpText.size() >= len)
+      invalid("kgh_handle_layer_dump: buffer of " + std::to_string(len) + " bytes is too small (" +
+              std::to_string(handle->dumpText.size() + 1) + " needed)");
+    std::memcpy(buf, handle->dumpText.c_str(), handle->dumpText.size() + 1);
   });
 }
 

@@ -13,6 +13,7 @@
 #include <unistd.h>
 
 #include <cctype>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
@@ -21,6 +22,7 @@
 #include <memory>
 #include <mutex>
 #include <sstream>
+#include <vector>
 
 #include "../neuralnet/modelversion.h"
 #include "../neuralnet/nneval.h"
@@ -312,6 +314,10 @@ struct ComputeContext {
   // hipLowLatency: handles of at most KGH_LOW_LATENCY_MAX_BATCH rows run the
   // split-K 3x3 convs (kgh_handle_set_low_latency), for batch-1 searches.
   bool lowLatency = false;
+  // hipDebugIntermediateValues: every batch writes the per-block trunk
+  // summary lines (kgh_handle_set_layer_dump) to stderr, as a build with
+  // DEBUG_INTERMEDIATE_VALUES prints them (eigenbackend.cpp:1773-1785).
+  bool dumpLayers = false;
   std::string tunerFile;  // explicit tuning file, else a per-(gpu, board, batch, dtype, architecture) name
   std::string tunerDir;
   uint64_t archHash = 0;  // of the flattened layer table (shapes, not weights)
@@ -471,6 +477,7 @@ ComputeContext* NeuralNet::createComputeContext(const vector<int>& gpuIdxs, Logg
   if(cfg.contains("hipAutoTune")) c->autoTune = cfg.getBool("hipAutoTune");
   if(cfg.contains("hipTunerFile")) c->tunerFile = cfg.getString("hipTunerFile");
   if(cfg.contains("hipLowLatency")) c->lowLatency = cfg.getBool("hipLowLatency");
+  if(cfg.contains("hipDebugIntermediateValues")) c->dumpLayers = cfg.getBool("hipDebugIntermediateValues");
   string home = homeDataDirOverride;
   if(home.empty()) {
     const char* env = getenv("HOME");
@@ -546,6 +553,10 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
   maybeAutoTune(*h, logger, serverThreadIdx);
   const bool lowLatency = context->lowLatency && maxBatchSize <= KGH_LOW_LATENCY_MAX_BATCH;
   if(lowLatency) checkKgh(kgh_handle_set_low_latency(h->handle, 1), "kgh_handle_set_low_latency");
+  // The dump undoes the load-time scale-by-8, so its values compare with an
+  // unscaled (Eigen) run's.
+  if(context->dumpLayers)
+    checkKgh(kgh_handle_set_layer_dump(h->handle, 1, pp.outputScaleMultiplier), "kgh_handle_set_layer_dump");
 
   if(logger != nullptr) {
     char buf[512] = {0};
@@ -642,6 +653,11 @@ void runGetOutput(ComputeHandle* h, InputBuffers* b, int numBatchEltsFilled, NNR
   }
   else {
     checkKgh(kgh_forward_staged(h->handle, n), "kgh_forward_staged");
+  }
+  if(h->context->dumpLayers) {
+    std::vector<char> text((size_t)1 << 20);
+    checkKgh(kgh_handle_layer_dump(h->handle, text.data(), (int32_t)text.size()), "kgh_handle_layer_dump");
+    std::fputs(text.data(), stderr);
   }
 
   const size_t postFloats = (size_t)kgh_post_row_floats(nnX, nnY);

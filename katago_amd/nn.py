@@ -537,6 +537,20 @@ class DeviceHandle:
         hip_check(hip_library().kgh_handle_profile(self._ptr, kind, ctypes.byref(ms), ctypes.byref(cnt), ctypes.byref(fl)))
         return ms.value, cnt.value, fl.value
 
+    def set_layer_dump(self, on: bool, value_scale: float = 1.0):
+        """kgh_handle_set_layer_dump: per-block trunk summary lines of the
+        following forwards, values times value_scale."""
+        lib = hip_library()
+        lib.kgh_handle_set_layer_dump.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_float]
+        hip_check(lib.kgh_handle_set_layer_dump(self._ptr, int(on), value_scale))
+
+    def layer_dump(self) -> str:
+        lib = hip_library()
+        lib.kgh_handle_layer_dump.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int32]
+        buf = ctypes.create_string_buffer(1 << 20)
+        hip_check(lib.kgh_handle_layer_dump(self._ptr, buf, len(buf)))
+        return buf.value.decode()
+
     def profile_kernels(self):
         """kgh_handle_profile_kernels: [(kind, launches, total_ms, flops,
         kernel)] per kernel that ran, in order of first launch."""

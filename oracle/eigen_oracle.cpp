@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <stdexcept>
@@ -365,6 +366,36 @@ struct BlockIntf {
   virtual void apply(float* trunk, const float* mask, const float* maskSum, Geom g) const = 0;
 };
 
+// DebugPrint::print3DSummary's line (debugprint.cpp:14-76,78-132) for an
+// [N][S][C] tensor: count, min, max, mean and root mean square over the
+// positions whose mask is nonzero, then the buffer's first eight values.
+static std::string summaryLine(const std::string& name, const float* data, int N, int S, int C, const float* mask) {
+  int valid = 0;
+  float mn = 1e30f, mx = -1e30f;
+  double sum = 0.0, sq = 0.0;
+  for(int p = 0; p < N * S; p++) {
+    if(mask[p] == 0.0f) continue;
+    for(int c = 0; c < C; c++) {
+      const float v = data[(size_t)p * C + c];
+      valid++;
+      mn = std::min(mn, v);
+      mx = std::max(mx, v);
+      sum += v;
+      sq += (double)v * v;
+    }
+  }
+  if(valid == 0) mn = mx = 0.0f;
+  char line[512];
+  snprintf(line, sizeof(line), "DEBUG %s [NSC %dx%dx%d] valid=%d min=%.6g max=%.6g mean=%.6g rms=%.6g first8=", name.c_str(), N, S, C,
+           valid, mn, mx, valid ? sum / valid : 0.0, valid ? std::sqrt(sq / valid) : 0.0);
+  std::string out = line;
+  for(int i = 0; i < 8 && i < N * S * C; i++) {
+    snprintf(line, sizeof(line), " %.6g", data[i]);
+    out += line;
+  }
+  return out + "\n";
+}
+
 struct BlockStack {
   vector<std::unique_ptr<BlockIntf>> blocks;
   BlockStack(const vector<std::pair<int, unique_ptr_void>>& descs, int nnX, int nnY);
@@ -655,7 +686,7 @@ struct Model {
   // input [N][H][W][Cin] (already symmetry-transformed), global [N][G].
   // Outputs: policy [N][HW][pc], pass [N][pc], value [N][3], score [N][sc], own [N][HW].
   void apply(const float* input, const float* global, int N, vector<float>& policy, vector<float>& pass, vector<float>& value,
-             vector<float>& score, vector<float>& own) const {
+             vector<float>& score, vector<float>& own, std::string* dump = nullptr) const {
     Geom g{N, nnY, nnX};
     const size_t rows = g.rows();
     const int Cin = desc.numInputChannels;
@@ -670,11 +701,19 @@ struct Model {
     initialConv.apply(input, trunk.data(), g, false);
     initialMatMul.apply(global, gbias.data(), N);
     addNCBias(trunk.data(), gbias.data(), C, g);
-    blocks.apply(trunk.data(), mask.data(), maskSum.data(), g);
+    // With a dump, the trunk before each block as BlockStack::apply prints it
+    // under DEBUG_INTERMEDIATE_VALUES (eigenbackend.cpp:1773-1785), then the
+    // trunk after the blocks and after the tip.
+    for(size_t i = 0; i < blocks.blocks.size(); i++) {
+      if(dump) *dump += summaryLine("ORACLE Blockstack block " + std::to_string(i), trunk.data(), N, g.hw(), C, mask.data());
+      blocks.blocks[i]->apply(trunk.data(), mask.data(), maskSum.data(), g);
+    }
+    if(dump) *dump += summaryLine("ORACLE Trunk after blocks", trunk.data(), N, g.hw(), C, mask.data());
     if(desc.trunk.trunkNormKind == TRUNK_NORM_KIND_STANDARD)
       BNLayer(desc.trunk.trunkTipBN, desc.trunk.trunkTipActivation.activation).apply(trunk.data(), tip.data(), mask.data(), g);
     else
       trunkRMSNorm(desc.trunk.trunkTipRMSNorm, desc.trunk.trunkTipActivation.activation, trunk.data(), tip.data(), mask.data(), g);
+    if(dump) *dump += summaryLine("ORACLE Trunk tip", tip.data(), N, g.hw(), C, mask.data());
 
     // Policy head (eigenbackend.cpp:1980-2024)
     const PolicyHeadDesc& ph = desc.policyHead;
@@ -742,6 +781,8 @@ struct OracleModel {
   ModelDesc desc;
   std::unique_ptr<Model> model;
   int nnX, nnY;
+  bool dump = false;
+  std::string dumpText;
 };
 }  // namespace
 
@@ -771,6 +812,19 @@ void* oracle_load_model_ex(const char* path, int nn_x, int nn_y, int apply_trans
 
 void oracle_free_model(void* m) { delete (OracleModel*)m; }
 
+void oracle_set_layer_dump(void* model, int enabled) {
+  OracleModel* m = (OracleModel*)model;
+  m->dump = enabled != 0;
+  m->dumpText.clear();
+}
+
+int oracle_layer_dump(void* model, char* buf, int len) {
+  const std::string& t = ((OracleModel*)model)->dumpText;
+  if(buf == nullptr || (int)t.size() >= len) return -1;
+  std::memcpy(buf, t.c_str(), t.size() + 1);
+  return 0;
+}
+
 int oracle_forward(void* handle, int n, const float* spatial, const float* global_in, const int* symmetry,
                    const float* policy_optimism, float* policy, float* value, float* score, float* ownership, char* err, int errlen) {
   try {
@@ -784,7 +838,8 @@ int oracle_forward(void* handle, int n, const float* spatial, const float* globa
       SymmetryHelpers::copyInputsWithSymmetry(spatial + (size_t)i * HW * Cin, in.data() + (size_t)i * HW * Cin, 1, nnY, nnX, Cin,
                                               true, symmetry[i]);
     vector<float> pol, pass, val, sc, own;
-    m->model->apply(in.data(), global_in, n, pol, pass, val, sc, own);
+    if(m->dump) m->dumpText.clear();
+    m->model->apply(in.data(), global_in, n, pol, pass, val, sc, own, m->dump ? &m->dumpText : nullptr);
     const int pc = d.numPolicyChannels, nsc = d.numScoreValueChannels;
     const bool mix = pc == 2 || (pc == 4 && d.modelVersion >= 16);
     vector<float> tmp(HW);

@@ -61,6 +61,14 @@ int oracle_forward(void* model, int n, const float* spatial, const float* global
                    const float* policy_optimism, float* policy, float* value, float* score, float* ownership,
                    char* err, int errlen);
 
+/* Per-block trunk dump of the following forwards (the lines of the
+ * reference's DEBUG_INTERMEDIATE_VALUES build, debugprint.h:14-49, named
+ * "ORACLE Blockstack block <i>", "ORACLE Trunk after blocks", "ORACLE Trunk
+ * tip"); oracle_layer_dump copies the last forward's lines, -1 if buf is too
+ * small. */
+void oracle_set_layer_dump(void* model, int enabled);
+int oracle_layer_dump(void* model, char* buf, int len);
+
 /* NeuralNet::testEvaluate* (NHWC, fp32): kind 0 conv, 1 batch norm,
  * 2 residual block, 3 global pooling residual block, 5 batch norm followed
  * by an activation layer. Returns 1, or -1 on error. */

@@ -32,6 +32,8 @@ def lib() -> ctypes.CDLL:
         l.oracle_direct_conv_f64.argtypes = [c.c_int] * 4 + [c.c_void_p, c.c_int, c.c_int, c.c_int, c.c_void_p,
                                                               c.c_void_p]
         l.oracle_copy_with_symmetry.argtypes = [c.c_void_p, c.c_void_p] + [c.c_int] * 7
+        l.oracle_set_layer_dump.argtypes = [c.c_void_p, c.c_int]
+        l.oracle_layer_dump.argtypes = [c.c_void_p, c.c_char_p, c.c_int]
         _LIB = l
     return _LIB
 
@@ -61,6 +63,16 @@ class OracleModel:
         if rc != 0:
             raise RuntimeError(err.value.decode())
         return out
+
+    def set_layer_dump(self, enabled: bool):
+        """Per-block trunk summary lines of the following forwards."""
+        lib().oracle_set_layer_dump(self._ptr, int(enabled))
+
+    def layer_dump(self) -> str:
+        buf = ctypes.create_string_buffer(1 << 20)
+        if lib().oracle_layer_dump(self._ptr, buf, len(buf)) != 0:
+            raise RuntimeError("oracle layer dump does not fit the buffer")
+        return buf.value.decode()
 
     def close(self):
         if getattr(self, "_ptr", None):

@@ -33,7 +33,10 @@ For each net the script
     tensors: 19x19, 19x11, 17x19, 7x15 and 9x9 boards), and stores the raw
     head outputs in the order the C++ backends read them: the policy channels
     the exporter writes (0 and 5, or 0, 5, 6 and 7), the three value logits,
-    the six score channels (misc 0-3 and more-misc 0-1) and the ownership.
+    the six score channels (misc 0-3 and more-misc 0-1) and the ownership;
+    and, from the forward's ExtraOutputs, the trunk after the embedding,
+    after each block and after the tip, summarised as KataGo's debug build
+    prints it (count, min, max, mean, rms over on-board positions).
 
 Outputs: pytorch_golden_<name>.bin.gz (the exported model) and
 pytorch_golden.npz (inputs and outputs, plain arrays, loadable with
@@ -187,16 +190,30 @@ def export_and_forward(name, base, changes, seed, spatial_nhwc, glob, tmp):
     x = torch.tensor(spatial_nhwc.reshape(n, 19, 19, 22).transpose(0, 3, 1, 2).astype(np.float64))
     gl = torch.tensor(glob.astype(np.float64))
 
+    nblocks = len(model.blocks)
+    names = ["trunk_after_embedding"] + [f"trunk_after_block{i}" for i in range(nblocks)] + ["trunkfinal"]
+    on = x[:, 0:1, :, :].numpy() > 0
+
     def heads():
+        eo = mp.ExtraOutputs(names)
         with torch.no_grad():
-            out = model(x, gl)[0]
+            out = model(x, gl, extra_outputs=eo)[0]
         policy, value, misc, moremisc, ownership = (t.numpy() for t in out[:5])
+        # The trunk before each block, after the last and after the tip, as
+        # KataGo's debug build summarises them: element count, min, max, mean
+        # and root mean square over on-board positions, all channels.
+        stats = []
+        for nm in names:
+            t = eo.returned[nm].numpy()
+            v = t[np.broadcast_to(on, t.shape)]
+            stats.append([v.size, v.min(), v.max(), v.mean(), np.sqrt((v * v).mean())])
         chans = [0, 5] if policy.shape[1] == 6 else [0, 5, 6, 7]
         return {
             "policy": policy[:, chans, :],  # [n][channels][361 + pass]
             "value": value,  # [n][3]
             "score": np.concatenate([misc[:, 0:4], moremisc[:, 0:2]], axis=1),
             "ownership": ownership.reshape(n, 361),
+            "trunkstats": np.array(stats, np.float64),
         }
 
     result = heads()
@@ -215,7 +232,7 @@ def main():
     with tempfile.TemporaryDirectory() as tmp:
         for name, base, changes, seed in NETS:
             r = export_and_forward(name, base, changes, seed, spatial, glob, tmp)
-            for k in ("policy", "value", "score", "ownership"):
+            for k in ("policy", "value", "score", "ownership", "trunkstats"):
                 arrays[f"{name}/{k}"] = r[k]
                 if "model_act" in r:
                     arrays[f"{name}/model_act/{k}"] = r["model_act"][k]

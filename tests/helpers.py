@@ -49,3 +49,18 @@ def approx_equal_kat(x, y, fp16: bool):
     else:
         tol = 1e-4 * np.maximum(np.maximum(np.abs(x), np.abs(y)), 1.0)
     return np.abs(x - y) < tol
+
+
+def parse_layer_dump(text):
+    """Lines of a per-block trunk dump ("DEBUG <name> [NSC NxSxC] valid= min=
+    max= mean= rms= first8= ..."): [(name without its backend prefix, valid,
+    min, max, mean, rms, first values)]."""
+    import re
+    out = []
+    pat = re.compile(r"^DEBUG (\S+) (.*?) \[NSC (\d+)x(\d+)x(\d+)\] valid=(\d+) min=(\S+) max=(\S+) mean=(\S+) rms=(\S+) first8=(.*)$")
+    for line in text.splitlines():
+        m = pat.match(line)
+        assert m, line
+        out.append((m.group(2), int(m.group(6)), float(m.group(7)), float(m.group(8)), float(m.group(9)), float(m.group(10)),
+                    [float(v) for v in m.group(11).split()]))
+    return out

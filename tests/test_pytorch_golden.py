@@ -74,3 +74,29 @@ def test_rmsnorm_tip_activation_follows_the_eigen_backend():
     assert max(pg.max_errors(out, pg.expected(name, np.zeros(n))).values()) <= TOL
     model_act = pg.expected(name, np.zeros(n), prefix="model_act/")
     assert pg.max_errors(out, model_act)["value"] > 0.1
+
+
+@pytest.mark.parametrize("name", sorted(DECLARED))
+def test_oracle_layer_dump_matches_reference_trunk(name):
+    """The oracle's per-block trunk dump (the lines of the reference's
+    DEBUG_INTERMEDIATE_VALUES build) against the trunk the reference's
+    PyTorch forward reports through ExtraOutputs: after the embedding, after
+    each block, after the tip. Loaded without transformToReduceActivations,
+    which rescales trunk channels, so both hold the same trunk. Element
+    counts exact; min, max and rms within 1e-5 relative, mean within 1e-5 of
+    the rms."""
+    from helpers import parse_layer_dump
+    sp, gl = pg.inputs()
+    n = sp.shape[0]
+    om = oracle.OracleModel(pg.model_path(name), load_time_transforms=False)
+    om.set_layer_dump(True)
+    om.forward(sp, gl, None, np.zeros(n, np.float32))
+    got = parse_layer_dump(om.layer_dump())
+    exp = pg.data()[f"{name}/trunkstats"]
+    names = [g[0] for g in got]
+    assert names == [f"Blockstack block {i}" for i in range(len(exp) - 2)] + ["Trunk after blocks", "Trunk tip"]
+    for g, e in zip(got, exp):
+        assert g[1] == int(e[0]), (g[0], g[1], e[0])
+        for k, (a, b) in enumerate(zip(g[2:6], e[1:5])):
+            tol = 1e-5 * (e[4] if k == 2 else max(abs(b), 1e-3))
+            assert abs(a - b) <= tol + 2e-6 * abs(b), (name, g[0], ["min", "max", "mean", "rms"][k], a, b)
