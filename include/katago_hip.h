@@ -107,6 +107,9 @@ typedef struct kgh_handle kgh_handle;
  * accumulation; otherwise everything is fp32. The layer program and weights
  * are copied; the caller may free them after return. */
 int kgh_model_create(int32_t device, const kgh_model_desc* desc, int32_t use_fp16, kgh_model** out);
+/* Frees the model. Its handles must not run after this; kgh_handle_free
+ * itself does not read the model, so they may still be freed afterwards
+ * (finalizers of a garbage collector can run in either order). */
 int kgh_model_free(kgh_model* model);
 
 /* One execution context (stream, activation buffers, staging) for batches of
@@ -272,6 +275,26 @@ int kgh_handle_set_low_latency(kgh_handle* handle, int32_t enabled);
  * launches' algorithmic FLOPs (2*M*Cin*Cout*ky*kx each). */
 int kgh_handle_set_profiling(kgh_handle* handle, int32_t enabled);
 int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32_t* launches, double* flops);
+/* Host-side fault injection, for tests of the device error paths. No
+ * counterpart in the reference, whose error surface it exercises: there a
+ * failed CUDA call becomes a StringError naming the call, file and line
+ * (CUDA_ERR, cudaerrorcheck.h:10-12); here a failed HIP call becomes
+ * KGH_ERR_HIP (KGH_ERR_OUT_OF_MEMORY for device allocations) with the same
+ * information in kgh_last_error(), which the backend raises as StringError.
+ * kgh_debug_inject_fault arms one fault, process-wide: the countdown-th
+ * checked HIP call at the site (1 = the next) reports hip_error instead of
+ * running; a kernel launch check reports it after the launch, so the kernel
+ * itself runs normally and the GPU stays healthy. countdown <= 0 disarms.
+ * kgh_debug_fault_pending says whether the armed fault has not fired yet. */
+#define KGH_FAULT_ANY_CALL 0
+#define KGH_FAULT_ALLOCATION 1
+#define KGH_FAULT_KERNEL_LAUNCH 2
+int kgh_debug_inject_fault(int32_t site, int32_t countdown, int32_t hip_error);
+int kgh_debug_fault_pending(int32_t* pending);
+/* The HIP runtime's pending last error of the calling thread, not cleared
+ * (hipPeekAtLastError): 0 when no unchecked call left one behind. */
+int kgh_debug_peek_last_error(int32_t* code);
+
 /* Per-block trunk dump, the runtime counterpart of the reference's
  * DEBUG_INTERMEDIATE_VALUES prints (debugprint.h:14-49, used at
  * eigenbackend.cpp:1773-1785): while enabled, forwards run without graph

@@ -12,6 +12,7 @@
 #include "kgh_kernels.h"
 
 #include <algorithm>
+#include <atomic>
 #include <array>
 #include <cmath>
 #include <map>
@@ -25,6 +26,26 @@
 #include <vector>
 
 #include "../../include/katago_hip.h"
+
+namespace kgh {
+namespace {
+// The armed fault: site (-1: none), calls left before it fires, error.
+std::atomic<int> g_faultSite{-1};
+std::atomic<int> g_faultCountdown{0};
+std::atomic<int> g_faultError{0};
+std::mutex g_faultMutex;
+}  // namespace
+
+hipError_t injectedFault(int site) {
+  const int armed = g_faultSite.load(std::memory_order_relaxed);
+  if(armed < 0 || (armed != 0 && armed != site)) return hipSuccess;
+  std::lock_guard<std::mutex> lock(g_faultMutex);
+  if(g_faultSite.load() != armed) return hipSuccess;
+  if(g_faultCountdown.fetch_sub(1) > 1) return hipSuccess;
+  g_faultSite.store(-1);
+  return (hipError_t)g_faultError.load();
+}
+}  // namespace kgh
 
 namespace {
 
@@ -62,7 +83,8 @@ struct DeviceArena {
   std::vector<void*> ptrs;
   void* alloc(size_t bytes) {
     void* p = nullptr;
-    hipError_t e = hipMalloc(&p, std::max<size_t>(bytes, 256));
+    hipError_t e = kgh::injectedFault(KGH_FAULT_ALLOCATION);
+    if(e == hipSuccess) e = hipMalloc(&p, std::max<size_t>(bytes, 256));
     if(e != hipSuccess) throw KghError(KGH_ERR_OUT_OF_MEMORY, std::string("hipMalloc failed: ") + hipGetErrorString(e));
     ptrs.push_back(p);
     return p;
@@ -494,6 +516,7 @@ struct ProfRec {
 
 struct kgh_handle {
   kgh_model* model = nullptr;
+  int device = 0;  // model->device, kept so that kgh_handle_free never reads the model
   int maxBatch = 0, H = 0, W = 0;
   bool exact = false;
   hipStream_t stream = nullptr;
@@ -1225,6 +1248,10 @@ hipGraphExec_t captureForward(kgh_handle* h, int n, const float* sp, const float
     hipGraph_t partial = nullptr;
     (void)hipStreamEndCapture(h->stream, &partial);
     if(partial) (void)hipGraphDestroy(partial);
+    // Ending an abandoned capture can leave an error in the runtime's
+    // last-error state; the next launch check (hipGetLastError) would report
+    // it against a healthy launch of a later forward.
+    (void)hipGetLastError();
     throw;
   }
   KGH_HIP_CHECK(hipStreamEndCapture(h->stream, &graph));
@@ -1589,6 +1616,7 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     const Net& net = model->net;
     std::unique_ptr<kgh_handle> h(new kgh_handle());
     h->model = model;
+    h->device = model->device;
     h->maxBatch = max_batch;
     h->H = nn_y;
     h->W = nn_x;
@@ -1636,11 +1664,11 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     h->dSym = a.allocN<int>(max_batch);
     h->dOpt = a.allocN<float>(max_batch);
     h->dOut = a.allocN<float>((size_t)max_batch * h->rowFloats);
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hSpatial, M * net.inputC * sizeof(float), hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hGlobal, (size_t)max_batch * net.globalC * sizeof(float), hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hSym, (size_t)max_batch * sizeof(int), hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hOpt, (size_t)max_batch * sizeof(float), hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hOut, (size_t)max_batch * h->rowFloats * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hSpatial, M * net.inputC * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hGlobal, (size_t)max_batch * net.globalC * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hSym, (size_t)max_batch * sizeof(int), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hOpt, (size_t)max_batch * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hOut, (size_t)max_batch * h->rowFloats * sizeof(float), hipHostMallocDefault));
     const size_t policySize = (size_t)nn_x * nn_y + 1;
     const size_t postFloats = (size_t)kgh_post_row_floats(nn_x, nn_y);
     h->dLegal = a.allocN<unsigned char>((size_t)max_batch * policySize);
@@ -1648,11 +1676,11 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
     h->dTemp = a.allocN<float>(max_batch);
     h->dPost = a.allocN<float>((size_t)max_batch * postFloats);
     h->dErr = a.allocN<int>(1);
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hLegal, (size_t)max_batch * policySize, hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hInfo, (size_t)max_batch * sizeof(int), hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hTemp, (size_t)max_batch * sizeof(float), hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hPost, (size_t)max_batch * postFloats * sizeof(float), hipHostMallocDefault));
-    KGH_HIP_CHECK(hipHostMalloc((void**)&h->hErr, sizeof(int), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hLegal, (size_t)max_batch * policySize, hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hInfo, (size_t)max_batch * sizeof(int), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hTemp, (size_t)max_batch * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hPost, (size_t)max_batch * postFloats * sizeof(float), hipHostMallocDefault));
+    KGH_HIP_CHECK_AT(KGH_FAULT_ALLOCATION, hipHostMalloc((void**)&h->hErr, sizeof(int), hipHostMallocDefault));
     *out = h.release();
   });
 }
@@ -1660,7 +1688,7 @@ int kgh_handle_create(kgh_model* model, int32_t max_batch, int32_t nn_x, int32_t
 int kgh_handle_free(kgh_handle* handle) {
   return guarded([&] {
     if(handle == nullptr) return;
-    (void)hipSetDevice(handle->model->device);
+    (void)hipSetDevice(handle->device);
     (void)hipStreamSynchronize(handle->stream);
     delete handle;
   });
@@ -1733,6 +1761,7 @@ int kgh_forward_device_noalloc(kgh_model* model, int32_t n, int32_t nn_x, int32_
     // give the same results as any tuned choice).
     kgh_handle view;
     view.model = model;
+    view.device = model->device;
     view.maxBatch = n;
     view.H = nn_y;
     view.W = nn_x;
@@ -2177,6 +2206,35 @@ int kgh_handle_profile(kgh_handle* handle, int32_t kind, double* total_ms, int32
     *total_ms = ms;
     *launches = cnt;
     *flops = fl;
+  });
+}
+
+int kgh_debug_inject_fault(int32_t site, int32_t countdown, int32_t hip_error) {
+  return guarded([&] {
+    if(site < KGH_FAULT_ANY_CALL || site > KGH_FAULT_KERNEL_LAUNCH) invalid("unknown fault site");
+    std::lock_guard<std::mutex> lock(kgh::g_faultMutex);
+    if(countdown <= 0) {
+      kgh::g_faultSite.store(-1);
+      return;
+    }
+    if(hip_error == 0) invalid("the injected error must be a HIP error code");
+    kgh::g_faultError.store(hip_error);
+    kgh::g_faultCountdown.store(countdown);
+    kgh::g_faultSite.store(site);
+  });
+}
+
+int kgh_debug_peek_last_error(int32_t* code) {
+  return guarded([&] {
+    if(code == nullptr) invalid("null output");
+    *code = (int32_t)hipPeekAtLastError();
+  });
+}
+
+int kgh_debug_fault_pending(int32_t* pending) {
+  return guarded([&] {
+    if(pending == nullptr) invalid("null output");
+    *pending = kgh::g_faultSite.load() >= 0 ? 1 : 0;
   });
 }
 

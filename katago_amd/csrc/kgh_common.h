@@ -30,15 +30,36 @@ struct KghError : public std::runtime_error {
   KghError(int c, const std::string& m) : std::runtime_error(m), code(c) {}
 };
 
-#define KGH_HIP_CHECK(expr)                                                                          \
+namespace kgh {
+// Host-side fault injection (kgh_debug_inject_fault): the HIP error an armed
+// fault reports at this checked call (site 1 = an allocation, 2 = a kernel
+// launch, 0 = any other call), or hipSuccess. One relaxed atomic load when
+// nothing is armed.
+hipError_t injectedFault(int site);
+}  // namespace kgh
+
+// A checked HIP call: an armed fault replaces it (a launch check reports the
+// fault after the launch); a failure becomes KghError(KGH_ERR_HIP) naming the
+// call, file and line, as the reference's CUDA_ERR does
+// (cudaerrorcheck.h:10-12).
+#define KGH_HIP_CHECK_AT(site, expr)                                                                 \
   do {                                                                                               \
-    hipError_t kgh_e_ = (expr);                                                                      \
+    hipError_t kgh_e_ = kgh::injectedFault(site);                                                    \
+    if(kgh_e_ == hipSuccess) kgh_e_ = (expr);                                                        \
     if(kgh_e_ != hipSuccess)                                                                         \
       throw KghError(2, std::string(#expr) + " failed: " + hipGetErrorString(kgh_e_) + " (" +       \
                           __FILE__ + ":" + std::to_string(__LINE__) + ")");                          \
   } while(0)
 
-#define KGH_CHECK_LAUNCH() KGH_HIP_CHECK(hipGetLastError())
+#define KGH_HIP_CHECK(expr) KGH_HIP_CHECK_AT(0, expr)
+#define KGH_CHECK_LAUNCH()                                                                           \
+  do {                                                                                               \
+    hipError_t kgh_e_ = hipGetLastError();                                                           \
+    if(kgh_e_ == hipSuccess) kgh_e_ = kgh::injectedFault(2);                                         \
+    if(kgh_e_ != hipSuccess)                                                                         \
+      throw KghError(2, std::string("kernel launch failed: ") + hipGetErrorString(kgh_e_) + " (" +  \
+                          __FILE__ + ":" + std::to_string(__LINE__) + ")");                          \
+  } while(0)
 
 // ---------------------------------------------------------------------------
 // Activations in fp32, with the reference's formulas:

@@ -300,13 +300,22 @@ struct LoadedModel {
   LoadedModel& operator=(const LoadedModel&) = delete;
 };
 
+// One uploaded copy of the weights per (device, precision), shared by the
+// handles of a context and counted by them. The context and each handle own
+// the table, so handles and their context may be freed in either order.
+struct ModelTable {
+  std::mutex mutex;
+  std::map<std::pair<int, bool>, std::pair<kgh_model*, int>> models;
+  ~ModelTable() {
+    for(auto& kv : models) kgh_model_free(kv.second.first);
+  }
+};
+
 struct ComputeContext {
   int nnXLen;
   int nnYLen;
   enabled_t useFP16Mode;
-  std::mutex mutex;
-  // One uploaded copy of the weights per (device, precision), shared by handles.
-  std::map<std::pair<int, bool>, std::pair<kgh_model*, int>> models;
+  std::shared_ptr<ModelTable> table = std::make_shared<ModelTable>();
 
   // Autotuning (config keys hipAutoTune, hipTunerFile; the OpenCL backend's
   // openCLTunerFile is the model): tables live in <home data dir>/hiptuning.
@@ -323,13 +332,11 @@ struct ComputeContext {
   uint64_t archHash = 0;  // of the flattened layer table (shapes, not weights)
 
   ComputeContext(int x, int y, enabled_t fp16) : nnXLen(x), nnYLen(y), useFP16Mode(fp16) {}
-  ~ComputeContext() {
-    for(auto& kv : models) kgh_model_free(kv.second.first);
-  }
 };
 
 struct ComputeHandle {
   ComputeContext* context = nullptr;
+  std::shared_ptr<ModelTable> table;  // the context's; outlives it if the handle is freed last
   int device = 0;
   bool useFP16 = false;
   bool inputsUseNHWC = true;
@@ -355,12 +362,12 @@ struct ComputeHandle {
   int tuningSource = 0;  // 0 built-in choices, 1 loaded from a tuning file, 2 tuned at creation
   ~ComputeHandle() {
     if(handle != nullptr) kgh_handle_free(handle);
-    if(context != nullptr && model != nullptr) {
-      std::lock_guard<std::mutex> lock(context->mutex);
-      auto it = context->models.find({device, useFP16});
-      if(it != context->models.end() && --it->second.second == 0) {
+    if(table != nullptr && model != nullptr) {
+      std::lock_guard<std::mutex> lock(table->mutex);
+      auto it = table->models.find({device, useFP16});
+      if(it != table->models.end() && --it->second.second == 0) {
         kgh_model_free(it->second.first);
-        context->models.erase(it);
+        table->models.erase(it);
       }
     }
   }
@@ -506,11 +513,13 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
   h->numScore = desc.numScoreValueChannels;
   h->maxBatchSize = maxBatchSize;
 
+  h->table = context->table;
   {
-    std::lock_guard<std::mutex> lock(context->mutex);
+    ModelTable& t = *h->table;
+    std::lock_guard<std::mutex> lock(t.mutex);
     auto key = std::make_pair(h->device, h->useFP16);
-    auto it = context->models.find(key);
-    if(it == context->models.end()) {
+    auto it = t.models.find(key);
+    if(it == t.models.end()) {
       Flattener f;
       f.model(desc);
       kgh_model_desc d = f.describe(desc);
@@ -531,7 +540,7 @@ ComputeHandle* NeuralNet::createComputeHandle(ComputeContext* context, const Loa
       context->archHash = hsh;
       kgh_model* m = nullptr;
       checkKgh(kgh_model_create(h->device, &d, h->useFP16 ? 1 : 0, &m), "kgh_model_create");
-      it = context->models.emplace(key, std::make_pair(m, 0)).first;
+      it = t.models.emplace(key, std::make_pair(m, 0)).first;
     }
     it->second.second++;
     h->model = it->second.first;

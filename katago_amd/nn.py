@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -23,7 +24,12 @@ _hip = None
 
 
 class StringError(RuntimeError):
-    """Error raised by the backend (KataGo's StringError)."""
+    """Error raised by the backend (KataGo's StringError); code is the C
+    library's status (KGH_ERR_*), 0 where there is none."""
+
+    def __init__(self, message: str, code: int = 0):
+        super().__init__(message)
+        self.code = code
 
 
 def _f32p(a):
@@ -170,6 +176,7 @@ class ComputeContext:
         mode = 2 if use_fp16 is None else (1 if use_fp16 else 0)
         self.model = model
         self.nn_x, self.nn_y = nn_x, nn_y
+        self._handles = weakref.WeakSet()
         cfg = []
         if auto_tune is not None:
             cfg.append(f"hipAutoTune = {'true' if auto_tune else 'false'}")
@@ -183,7 +190,13 @@ class ComputeContext:
             _raise(err)
 
     def close(self):
+        """Frees the context; its live handles are closed first, since a
+        handle cannot run without its context. (Handles the garbage collector
+        finalizes after the context are still freed safely: they share the
+        context's model table.)"""
         if getattr(self, "_ptr", None):
+            for h in list(getattr(self, "_handles", ())):
+                h.close()
             host_library().kgn_free_context(self._ptr)
             self._ptr = None
 
@@ -209,6 +222,7 @@ class ComputeHandle:
                                           int(inputs_use_nhwc), gpu_idx, err, len(err))
         if not self._ptr:
             _raise(err)
+        context._handles.add(self)
 
     @property
     def using_fp16(self) -> bool:
@@ -390,9 +404,38 @@ def test_evaluate(kind: int, desc_text: str, batch: int, nn_x: int, nn_y: int, u
     return out[: batch * nn_x * nn_y * out_channels]
 
 
+HIP_ERROR_OUT_OF_MEMORY = 2
+HIP_ERROR_LAUNCH_FAILURE = 719
+FAULT_ANY_CALL, FAULT_ALLOCATION, FAULT_KERNEL_LAUNCH = 0, 1, 2
+
+
+def inject_fault(site: int, countdown: int, hip_error: int = HIP_ERROR_LAUNCH_FAILURE) -> None:
+    """kgh_debug_inject_fault: the countdown-th checked HIP call at the site
+    reports hip_error (one-shot); countdown 0 disarms."""
+    lib = hip_library()
+    lib.kgh_debug_inject_fault.argtypes = [ctypes.c_int32] * 3
+    hip_check(lib.kgh_debug_inject_fault(site, countdown, hip_error))
+
+
+def peek_last_error() -> int:
+    """kgh_debug_peek_last_error: the runtime's pending HIP error code."""
+    v = ctypes.c_int32()
+    hip_check(hip_library().kgh_debug_peek_last_error(ctypes.byref(v)))
+    return v.value
+
+
+def fault_pending() -> bool:
+    v = ctypes.c_int32()
+    hip_check(hip_library().kgh_debug_fault_pending(ctypes.byref(v)))
+    return bool(v.value)
+
+
 def hip_check(status: int) -> None:
     if status != 0:
-        raise StringError(hip_library().kgh_last_error().decode(errors="replace"))
+        # Raised without a local name: a frame holding the exception that
+        # holds the frame would keep every caller's locals alive until the
+        # cycle collector runs.
+        raise StringError(hip_library().kgh_last_error().decode(errors="replace"), status)
 
 
 def device_count() -> int:
@@ -445,6 +488,7 @@ class DeviceModel:
                         info.num_score_value_channels, info.num_ownership_channels, len(self.layers),
                         self.layers.ctypes.data, self.weights.ctypes.data, len(self.weights))
         self.info = info
+        self._handles = weakref.WeakSet()
         self._ptr = ctypes.c_void_p()
         lib.kgh_model_create.argtypes = [ctypes.c_int32, ctypes.POINTER(_ModelDescC), ctypes.c_int32,
                                          ctypes.POINTER(ctypes.c_void_p)]
@@ -460,7 +504,12 @@ class DeviceModel:
         hip_check(lib.kgh_forward_device_noalloc(self._ptr, n, nn_x, nn_y, d_spatial, d_global, d_sym, d_opt, d_out, stream))
 
     def close(self):
+        """Frees the model; its live handles are closed first, since a handle
+        cannot run without the weights. (kgh_handle_free does not read the
+        model, so handles finalized after it are still freed safely.)"""
         if getattr(self, "_ptr", None) and self._ptr.value:
+            for h in list(getattr(self, "_handles", ())):
+                h.close()
             hip_library().kgh_model_free(self._ptr)
             self._ptr = ctypes.c_void_p()
 
@@ -482,6 +531,7 @@ class DeviceHandle:
         lib.kgh_handle_create.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.POINTER(ctypes.c_void_p)]
         hip_check(lib.kgh_handle_create(model._ptr, max_batch, nn_x, nn_y, 0, ctypes.byref(self._ptr)))
+        model._handles.add(self)
         lib.kgh_forward_device.argtypes = [ctypes.c_void_p, ctypes.c_int32] + [ctypes.c_void_p] * 5
         lib.kgh_handle_synchronize.argtypes = [ctypes.c_void_p]
         lib.kgh_handle_set_profiling.argtypes = [ctypes.c_void_p, ctypes.c_int32]
