@@ -75,10 +75,23 @@ typedef struct kgn_position {
 /* Featurizes n positions into nn_x by nn_y tensors exactly as
  * NNInputs::fillRowV7 does: spatial receives n * nn_x * nn_y * 22 floats
  * (NHWC if use_nhwc, else NCHW), global n * 19. num_threads worker threads
- * share the positions (0 = one per available core). Returns 0, or -1 with a
- * message in err on an invalid position. */
+ * take the positions in runs of consecutive ones (0 = one per available
+ * core). Returns 0, or -1 with a message in err on an invalid position. */
 int32_t kgn_featurize(const kgn_position* positions, int32_t n, int32_t nn_x, int32_t nn_y, int32_t use_nhwc,
                       float* spatial, float* global_out, int32_t num_threads, char* err, int32_t errlen);
+
+/* The boards' ladder searches are the featurizer's main cost, and KataGo's
+ * fillRowV7 repeats them for the two previous boards of every position
+ * (nninputs.cpp:2546-2566). Each thread keeps the ladder stones of the last
+ * `entries` boards it searched (8 by default, KGN_FEATURIZE_MAX_CACHE at
+ * most), keyed by everything the search reads (size, ko point, colours,
+ * chain order), so a board that comes again (the board one move back is
+ * usually the current board of the position featurized before; siblings of a
+ * search share their parent) is not searched again. The rows are the same
+ * with or without it. 0 turns it off. Returns the previous setting, or -1 for
+ * an out-of-range value. No counterpart in the reference. */
+#define KGN_FEATURIZE_MAX_CACHE 64
+int32_t kgn_featurize_set_cache(int32_t entries);
 
 #ifdef __cplusplus
 }

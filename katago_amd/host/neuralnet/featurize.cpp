@@ -21,6 +21,10 @@
 // chain linked breadth-first from its first stone in scan order, which can
 // differ from KataGo in such positions (about one in ten thousand of random
 // play's positions).
+//
+// Each thread keeps the ladder stones of the boards it searched last, keyed
+// by the whole board, so the boards one and two moves back, which fillRowV7
+// searches again for every position, are usually found instead.
 #include "../../../include/katago_featurize.h"
 
 #include <algorithm>
@@ -38,20 +42,56 @@ namespace {
 constexpr int MAX_SIDE = 19;
 constexpr int MAX_W = MAX_SIDE + 2;
 constexpr int MAX_AREA = MAX_W * MAX_W;
+// Every board is laid out on the largest board's padded grid, so the four
+// neighbour offsets are constants: up, left, right, down (KataGo's
+// adj_offsets order, board.cpp:36-45).
+constexpr int STRIDE = MAX_W;
+constexpr int ADJ[4] = {-STRIDE, -1, 1, STRIDE};
+constexpr int NONE_KEY = -1;
 constexpr int8_t EMPTY = 0, BLACK = 1, WHITE = 2, WALL = 3;
 constexpr int NONE = -1;
 constexpr int LADDER_NODE_BUDGET = 25000;  // board.cpp:1590
 
 inline int8_t opponent(int8_t p) { return (int8_t)(3 - p); }
 
+struct LadderFrame;
+
+// One stone reported by iterLadders: a stone of a chain in inescapable
+// atari or that can be put into one, and, for the first stone of a chain
+// with two liberties, the attacker's working moves (at most two).
+struct LadderHit {
+  int16_t point;  // a point of the padded grid
+  int8_t numWorking;
+  int16_t working[2];
+};
+
+// A board's ladder stones, kept for boards that come again: the board one
+// move back of a position is usually the current board of the position
+// before it, and the siblings of a search share their parent. The key is
+// everything the search reads: the size, the ko point, the colours and (when
+// the caller gives them) each stone's chain head and successor.
+struct LadderCacheEntry {
+  bool valid = false;
+  int xs = 0, ys = 0, ko = NONE_KEY;
+  bool chains = false;
+  int8_t colors[MAX_SIDE * MAX_SIDE];
+  int16_t head[MAX_SIDE * MAX_SIDE];
+  int16_t next[MAX_SIDE * MAX_SIDE];
+  std::vector<LadderHit> hits;
+};
+
 // Per-thread scratch of the board routines: a stamped mark array for
-// duplicate-free walks.
+// duplicate-free walks, the ladder search's stack, and the ladder cache.
 struct Scratch {
   uint32_t mark[MAX_AREA] = {};
   uint32_t stamp = 0;
-  // The ladder search's move list of each depth, sized before a search so
-  // that no list moves while a shallower level holds it.
-  std::vector<std::vector<int>> movePool;
+  // The move lists of every level of a ladder search, one after another
+  // (a level's list starts where its parent's ends), addressed by index.
+  std::vector<int> moves;
+  std::vector<LadderFrame> frames;
+  std::vector<int> working;
+  std::vector<LadderCacheEntry> cache;
+  size_t cacheNext = 0;  // the entry the next miss replaces
   uint32_t next() {
     if(++stamp == 0) {
       memset(mark, 0, sizeof(mark));
@@ -61,7 +101,7 @@ struct Scratch {
   }
 };
 
-// A board with a wall border: point (x, y) is (y + 1) * stride + x + 1. Each
+// A board with a wall border: point (x, y) is (y + 1) * STRIDE + x + 1. Each
 // chain is a circular list through next[] whose order, and whose head, follow
 // the same rules as KataGo's Board (board.cpp:990-1330): a move merges its
 // neighbours by splicing the smaller chain in after the larger one's head,
@@ -70,8 +110,7 @@ struct Scratch {
 // its early exits looks at the last entry of a move list built in it, so the
 // order is part of the result. libs[] and size[] are valid at heads.
 struct GoBoard {
-  int xs = 0, ys = 0, stride = 0;
-  int adj[4] = {};
+  int xs = 0, ys = 0;
   int16_t ko = NONE;
   int8_t color[MAX_AREA];
   int16_t head[MAX_AREA];
@@ -86,7 +125,7 @@ struct GoBoard {
     uint8_t capDirs;  // bit d: the move captured in direction d; 0x10: suicide
   };
 
-  int at(int x, int y) const { return (y + 1) * stride + x + 1; }
+  static int at(int x, int y) { return (y + 1) * STRIDE + x + 1; }
   int atPoint(int point) const { return at(point % xs, point / xs); }
   int numLibs(int p) const { return libs[head[p]]; }
 
@@ -100,11 +139,6 @@ struct GoBoard {
     if(koPoint < -1 || koPoint >= xSize * ySize) throw std::runtime_error("featurize: ko_point off the board");
     xs = xSize;
     ys = ySize;
-    stride = xs + 2;
-    adj[0] = -stride;  // up, left, right, down: KataGo's adj_offsets order
-    adj[1] = -1;
-    adj[2] = 1;
-    adj[3] = stride;
     for(int i = 0; i < MAX_AREA; i++) {
       color[i] = WALL;
       head[i] = (int16_t)i;
@@ -112,69 +146,87 @@ struct GoBoard {
       libs[i] = 0;
       size[i] = 0;
     }
-    for(int y = 0; y < ys; y++)
-      for(int x = 0; x < xs; x++) {
-        const int8_t c = colors[y * xs + x];
+    const int area = xs * ys;
+    int16_t toGrid[MAX_SIDE * MAX_SIDE];
+    for(int y = 0, i = 0; y < ys; y++)
+      for(int x = 0; x < xs; x++, i++) {
+        const int8_t c = colors[i];
         if(c != EMPTY && c != BLACK && c != WHITE) throw std::runtime_error("featurize: colour outside 0..2");
-        color[at(x, y)] = c;
+        toGrid[i] = (int16_t)at(x, y);
+        color[toGrid[i]] = c;
       }
     if(chainHead != nullptr && chainNext != nullptr) {
-      const int area = xs * ys;
       for(int i = 0; i < area; i++) {
-        const int p = atPoint(i);
+        const int p = toGrid[i];
         if(color[p] == EMPTY) continue;
         const int h = chainHead[i], nx = chainNext[i];
         if(h < 0 || h >= area || nx < 0 || nx >= area) throw std::runtime_error("featurize: chain link off the board");
-        head[p] = (int16_t)atPoint(h);
-        next[p] = (int16_t)atPoint(nx);
+        head[p] = toGrid[h];
+        next[p] = toGrid[nx];
       }
+      // Each chain once from its head: every stone of the circle has the
+      // chain's colour and head, and the circle closes within the board;
+      // size and liberties are counted on the way.
+      int stones = 0, reached = 0;
       for(int i = 0; i < area; i++) {
-        const int p = atPoint(i);
-        if(color[p] == EMPTY || head[p] != p) continue;
-        int n = 0, cur = p;
+        const int p = toGrid[i];
+        if(color[p] == EMPTY) continue;
+        stones++;
+        if(head[p] != p) continue;
+        const uint32_t st = s.next();
+        int n = 0, l = 0, cur = p;
         do {
           if(color[cur] != color[p] || head[cur] != p || ++n > area) throw std::runtime_error("featurize: inconsistent chain links");
+          for(int d = 0; d < 4; d++) {
+            const int a = cur + ADJ[d];
+            if(color[a] == EMPTY && s.mark[a] != st) {
+              s.mark[a] = st;
+              l++;
+            }
+          }
           cur = next[cur];
         } while(cur != p);
         size[p] = (int16_t)n;
+        libs[p] = (int16_t)l;
+        reached += n;
       }
+      // Every stone lies on its head's circle (the circles are disjoint).
+      if(reached != stones) throw std::runtime_error("featurize: inconsistent chain links");
     }
     else {
       const uint32_t st = s.next();
       int16_t queue[MAX_AREA];
-      for(int y = 0; y < ys; y++)
-        for(int x = 0; x < xs; x++) {
-          const int p = at(x, y);
-          if(color[p] == EMPTY || s.mark[p] == st) continue;
-          const int8_t c = color[p];
-          int qh = 0, qt = 0;
-          queue[qt++] = (int16_t)p;
-          s.mark[p] = st;
-          int prev = p, n = 0;
-          while(qh < qt) {
-            const int q = queue[qh++];
-            head[q] = (int16_t)p;
-            next[prev] = (int16_t)q;
-            prev = q;
-            n++;
-            for(int d = 0; d < 4; d++) {
-              const int a = q + adj[d];
-              if(color[a] == c && s.mark[a] != st) {
-                s.mark[a] = st;
-                queue[qt++] = (int16_t)a;
-              }
+      for(int i = 0; i < area; i++) {
+        const int p = toGrid[i];
+        if(color[p] == EMPTY || s.mark[p] == st) continue;
+        const int8_t c = color[p];
+        int qh = 0, qt = 0;
+        queue[qt++] = (int16_t)p;
+        s.mark[p] = st;
+        int prev = p, n = 0;
+        while(qh < qt) {
+          const int q = queue[qh++];
+          head[q] = (int16_t)p;
+          next[prev] = (int16_t)q;
+          prev = q;
+          n++;
+          for(int d = 0; d < 4; d++) {
+            const int a = q + ADJ[d];
+            if(color[a] == c && s.mark[a] != st) {
+              s.mark[a] = st;
+              queue[qt++] = (int16_t)a;
             }
           }
-          next[prev] = (int16_t)p;
-          size[p] = (int16_t)n;
         }
-    }
-    for(int y = 0; y < ys; y++)
-      for(int x = 0; x < xs; x++) {
-        const int p = at(x, y);
+        next[prev] = (int16_t)p;
+        size[p] = (int16_t)n;
+      }
+      for(int i = 0; i < area; i++) {
+        const int p = toGrid[i];
         if(color[p] != EMPTY && head[p] == p) libs[p] = (int16_t)countLibs(p, s);
       }
-    ko = (int16_t)(koPoint < 0 ? NONE : atPoint(koPoint));
+    }
+    ko = (int16_t)(koPoint < 0 ? NONE : toGrid[koPoint]);
   }
 
   int countLibs(int h, Scratch& s) const {
@@ -183,7 +235,7 @@ struct GoBoard {
     int cur = h;
     do {
       for(int d = 0; d < 4; d++) {
-        const int a = cur + adj[d];
+        const int a = cur + ADJ[d];
         if(color[a] == EMPTY && s.mark[a] != st) {
           s.mark[a] = st;
           n++;
@@ -204,7 +256,7 @@ struct GoBoard {
     int last = h2;
     while(true) {
       for(int d = 0; d < 4; d++) {
-        const int q = last + adj[d];
+        const int q = last + ADJ[d];
         if(color[q] == EMPTY && !isLibertyOf(q, h1)) newLibs++;
       }
       head[last] = (int16_t)h1;
@@ -219,7 +271,7 @@ struct GoBoard {
   bool isSuicide(int p, int8_t pla) const {
     const int8_t opp = opponent(pla);
     for(int d = 0; d < 4; d++) {
-      const int a = p + adj[d];
+      const int a = p + ADJ[d];
       if(color[a] == EMPTY) return false;
       if(color[a] == pla && numLibs(a) > 1) return false;
       if(color[a] == opp && numLibs(a) == 1) return false;
@@ -230,7 +282,7 @@ struct GoBoard {
   // Whether point q is next to a stone of the chain headed by h.
   bool isLibertyOf(int q, int h) const {
     for(int d = 0; d < 4; d++) {
-      const int a = q + adj[d];
+      const int a = q + ADJ[d];
       if(color[a] == color[h] && head[a] == h) return true;
     }
     return false;
@@ -241,7 +293,7 @@ struct GoBoard {
     int seen[4];
     int n = 0;
     for(int d = 0; d < 4; d++) {
-      const int a = q + adj[d];
+      const int a = q + ADJ[d];
       if(color[a] != c) continue;
       const int h = head[a];
       bool dup = false;
@@ -282,7 +334,7 @@ struct GoBoard {
     int oppSeen[4];
     int numOppSeen = 0;
     for(int d = 0; d < 4; d++) {
-      const int a = p + adj[d];
+      const int a = p + ADJ[d];
       if(color[a] == pla) {
         if(head[a] == head[p]) continue;
         libs[head[a]]--;
@@ -315,7 +367,7 @@ struct GoBoard {
     r.capDirs = 0;
     const int8_t opp = opponent(pla);
     for(int d = 0; d < 4; d++) {
-      const int a = p + adj[d];
+      const int a = p + ADJ[d];
       if(color[a] == opp && numLibs(a) == 1) r.capDirs |= (uint8_t)(1 << d);
     }
     if(r.capDirs == 0 && isSuicide(p, pla)) r.capDirs = 0x10;
@@ -333,7 +385,7 @@ struct GoBoard {
     changeSurroundingLiberties(p, opponent(pla), -1);
     int nextTail = p;
     for(int d = 0; d < 4; d++)
-      if(color[p + adj[d]] == EMPTY) nextTail = addChainWalk(h, nextTail, p + adj[d], pla);
+      if(color[p + ADJ[d]] == EMPTY) nextTail = addChainWalk(h, nextTail, p + ADJ[d], pla);
     return nextTail;
   }
   // A chain refilled by an undo starts with no liberties; the undone move's
@@ -347,7 +399,7 @@ struct GoBoard {
   int rebuildWalk(int h, int tail, int p, int8_t pla) {
     int add = 0;
     for(int d = 0; d < 4; d++) {
-      const int q = p + adj[d];
+      const int q = p + ADJ[d];
       if(color[q] == EMPTY && !isLibertyOf(q, h)) add++;
     }
     libs[h] = (int16_t)(libs[h] + add);
@@ -356,7 +408,7 @@ struct GoBoard {
     next[p] = (int16_t)tail;
     int nextTail = p;
     for(int d = 0; d < 4; d++) {
-      const int a = p + adj[d];
+      const int a = p + ADJ[d];
       if(color[a] == pla && head[a] != h) nextTail = rebuildWalk(h, nextTail, a, pla);
     }
     return nextTail;
@@ -374,7 +426,7 @@ struct GoBoard {
     const int p = r.loc;
     const int8_t opp = opponent(r.pla);
     for(int d = 0; d < 4; d++) {
-      const int a = p + adj[d];
+      const int a = p + ADJ[d];
       if((r.capDirs & (1 << d)) && color[a] == EMPTY) addChain(a, opp);
     }
     if(r.capDirs == 0x10) addChain(p, r.pla);
@@ -383,7 +435,7 @@ struct GoBoard {
     const int h = head[p];
     if(size[h] > 1) {
       int neighbours = 0;
-      for(int d = 0; d < 4; d++) neighbours += color[p + adj[d]] == r.pla;
+      for(int d = 0; d < 4; d++) neighbours += color[p + ADJ[d]] == r.pla;
       if(neighbours <= 1) {
         int hh = h;
         if(hh == p) {
@@ -402,7 +454,7 @@ struct GoBoard {
         next[cur] = next[p];
         int delta = 1;
         for(int d = 0; d < 4; d++) {
-          const int q = p + adj[d];
+          const int q = p + ADJ[d];
           if(color[q] == EMPTY && !isLibertyOf(q, hh)) delta--;
         }
         libs[hh] = (int16_t)(libs[hh] + delta);
@@ -415,7 +467,7 @@ struct GoBoard {
           cur = next[cur];
         } while(cur != p);
         for(int d = 0; d < 4; d++) {
-          const int a = p + adj[d];
+          const int a = p + ADJ[d];
           if(color[a] == r.pla && head[a] == UNLINKED) rebuildChain(a, r.pla);
         }
       }
@@ -430,19 +482,19 @@ struct GoBoard {
 
   int immediateLibs(int p) const {
     int n = 0;
-    for(int d = 0; d < 4; d++) n += color[p + adj[d]] == EMPTY;
+    for(int d = 0; d < 4; d++) n += color[p + ADJ[d]] == EMPTY;
     return n;
   }
 
   bool isAdjacentTo(int p, int8_t pla) const {
     for(int d = 0; d < 4; d++)
-      if(color[p + adj[d]] == pla) return true;
+      if(color[p + ADJ[d]] == pla) return true;
     return false;
   }
 
   bool isAdjacentToHead(int8_t pla, int p, int h) const {
     for(int d = 0; d < 4; d++) {
-      const int a = p + adj[d];
+      const int a = p + ADJ[d];
       if(color[a] == pla && head[a] == h) return true;
     }
     return false;
@@ -452,41 +504,45 @@ struct GoBoard {
 // ---------------------------------------------------------------------------
 // Ladders (board.cpp:1428-1790).
 
+// One level of a ladder search: its move list (a range of Scratch::moves),
+// the next move to try, and the record of the move being searched below it.
+struct LadderFrame {
+  int start, len, cur;
+  bool defender;
+  GoBoard::Record rec;
+};
+
 struct Ladder {
   Scratch& s;
   explicit Ladder(Scratch& sc) : s(sc) {}
 
   // Board::findLiberties: the liberties of the chain at p not already in
-  // out, appended in chain order starting from the stone p itself.
-  static void findLiberties(const GoBoard& b, int p, std::vector<int>& out) {
+  // list[0..len), appended in chain order starting from the stone p itself.
+  static void findLiberties(const GoBoard& b, int p, int* list, int& len) {
     int cur = p;
     do {
       for(int d = 0; d < 4; d++) {
-        const int a = cur + b.adj[d];
-        if(b.color[a] == EMPTY && std::find(out.begin(), out.end(), a) == out.end()) out.push_back(a);
+        const int a = cur + ADJ[d];
+        if(b.color[a] == EMPTY && std::find(list, list + len, a) == list + len) list[len++] = a;
       }
       cur = b.next[cur];
     } while(cur != p);
   }
 
   // Board::findLibertyGainingCaptures: liberties of the opponent chains in
-  // atari next to the chain at p, without repeats.
-  void libertyGainingCaptures(const GoBoard& b, int p, std::vector<int>& out) {
+  // atari next to the chain at p, without repeats, appended to the list.
+  void libertyGainingCaptures(const GoBoard& b, int p, int* list, int& len) {
     const int8_t opp = opponent(b.color[p]);
-    int checked[MAX_AREA];
-    int numChecked = 0;
+    const uint32_t st = s.next();  // marks the opponent heads already looked at
     int cur = p;
     do {
       for(int d = 0; d < 4; d++) {
-        const int a = cur + b.adj[d];
+        const int a = cur + ADJ[d];
         if(b.color[a] != opp) continue;
         const int ah = b.head[a];
-        if(b.libs[ah] != 1) continue;
-        bool seen = false;
-        for(int j = 0; j < numChecked; j++) seen = seen || checked[j] == ah;
-        if(seen) continue;
-        checked[numChecked++] = ah;
-        findLiberties(b, a, out);
+        if(b.libs[ah] != 1 || s.mark[ah] == st) continue;
+        s.mark[ah] = st;
+        findLiberties(b, a, list, len);
       }
       cur = b.next[cur];
     } while(cur != p);
@@ -497,7 +553,7 @@ struct Ladder {
     int cur = p;
     do {
       for(int d = 0; d < 4; d++) {
-        const int a = cur + b.adj[d];
+        const int a = cur + ADJ[d];
         if(b.color[a] == opp && b.numLibs(a) == 1) return true;
       }
       cur = b.next[cur];
@@ -510,7 +566,7 @@ struct Ladder {
     const int8_t opp = opponent(pla);
     int immediate = 0, caps = 0, capStones = 0, connSum = 0, connMax = 0;
     for(int d = 0; d < 4; d++) {
-      const int a = p + b.adj[d];
+      const int a = p + ADJ[d];
       if(b.color[a] == EMPTY) {
         immediate++;
       }
@@ -530,15 +586,16 @@ struct Ladder {
     upper = immediate + capStones + connSum;
   }
 
-  // Board::getNumLibertiesAfterPlay (board.cpp:344-429), capped at max.
-  int libsAfterPlay(const GoBoard& b, int p, int8_t pla, int max) {
+  // Board::getNumLibertiesAfterPlay (board.cpp:344-429), capped at max
+  // (at most 3 here: the list below holds fewer than max points).
+  static int libsAfterPlay(const GoBoard& b, int p, int8_t pla, int max) {
     const int8_t opp = opponent(pla);
-    int found[MAX_AREA];
+    int found[4];
     int n = 0;
     int capHeads[4];
     int numCap = 0;
     for(int d = 0; d < 4; d++) {
-      const int a = p + b.adj[d];
+      const int a = p + ADJ[d];
       if(b.color[a] == EMPTY) {
         found[n++] = a;
         if(n >= max) return max;
@@ -562,7 +619,7 @@ struct Ladder {
     int connHeads[4];
     int numConn = 0;
     for(int d = 0; d < 4; d++) {
-      const int a = p + b.adj[d];
+      const int a = p + ADJ[d];
       if(b.color[a] != pla) continue;
       const int h = b.head[a];
       bool seen = false;
@@ -572,7 +629,7 @@ struct Ladder {
       int cur = a;
       do {
         for(int k = 0; k < 4; k++) {
-          const int q = cur + b.adj[k];
+          const int q = cur + ADJ[k];
           if(q == p || !wouldBeEmpty(q)) continue;
           bool counted = false;
           for(int l = 0; l < n; l++) counted = counted || found[l] == q;
@@ -593,7 +650,7 @@ struct Ladder {
     const int8_t opp = opponent(pla);
     int capturable = NONE;
     for(int d = 0; d < 4; d++) {
-      const int a = p + b.adj[d];
+      const int a = p + ADJ[d];
       if(b.color[a] != WALL && b.color[a] != opp) return false;
       if(b.color[a] == opp && b.numLibs(a) == 1) {
         if(capturable != NONE) return false;
@@ -607,7 +664,7 @@ struct Ladder {
   static int connectionLibsX2(const GoBoard& b, int p, int8_t pla) {
     int n = 0;
     for(int d = 0; d < 4; d++) {
-      const int a = p + b.adj[d];
+      const int a = p + ADJ[d];
       if(b.color[a] == pla) {
         const int l = b.numLibs(a);
         if(l > 1) n += l * 2 - 3;
@@ -618,121 +675,161 @@ struct Ladder {
 
   static bool areAdjacent(const GoBoard& b, int p, int q) {
     const int d = p > q ? p - q : q - p;
-    return d == 1 || d == b.stride;
+    return d == 1 || d == STRIDE;
   }
 
-  struct Budget {};  // thrown when the node budget is spent
+  // At most this many moves in one level's list: the defender's liberty and
+  // one per opponent chain in atari around it.
+  static constexpr int MAX_LIST = MAX_SIDE * MAX_SIDE + 1;
 
-  GoBoard* board = nullptr;
-  int target = 0;          // a stone of the defending chain
-  int8_t defender = 0, attacker = 0;
-  bool defenderFirst = true;
-  int stackSize = 0;
-  int nodes = 0;
-
-  // One level of Board::searchIsLadderCaptured's explicit stack: whether the
-  // defending chain is captured with best play from here.
-  bool level(int depth) {
-    if(depth >= stackSize - 1) return true;
-    if(nodes >= LADDER_NODE_BUDGET) throw Budget();
-    GoBoard& b = *board;
-    const bool isDefender = defenderFirst ? (depth % 2 == 0) : (depth % 2 == 1);
+  // Entering a level of the search (board.cpp:1630-1720): either the level's
+  // verdict (1 captured, 0 escapes) or -1 with its move list in
+  // s.moves[start .. start + len).
+  int enter(GoBoard& b, int target, int8_t defender, bool isDefender, size_t start, int& len) {
+    const int8_t attacker = opponent(defender);
     const int libs = b.numLibs(target);
-    if(!isDefender && libs <= 1) return true;
-    if(!isDefender && libs >= 3) return false;
-    if(isDefender && libs >= 2) return false;
-    if(isDefender && b.ko != NONE) return false;
-    std::vector<int>& moves = s.movePool[depth];
-    moves.clear();
+    if(!isDefender && libs <= 1) return 1;
+    if(!isDefender && libs >= 3) return 0;
+    if(isDefender && libs >= 2) return 0;
+    if(isDefender && b.ko != NONE) return 0;
+    if(s.moves.size() < start + MAX_LIST) s.moves.resize(start + MAX_LIST + 4096);
+    int* m = s.moves.data() + start;
+    len = 0;
     if(isDefender) {
       // Captures first, then the chain's liberty unless it is one of them;
       // the bound below is taken at the list's last entry.
-      libertyGainingCaptures(b, target, moves);
-      findLiberties(b, target, moves);
+      libertyGainingCaptures(b, target, m, len);
+      findLiberties(b, target, m, len);
       int lower, upper;
-      boundLibsAfterPlay(b, moves.back(), defender, lower, upper);
-      if(lower >= 3) return false;
-      if(moves.size() == 1 && upper <= 1) return true;
+      boundLibsAfterPlay(b, m[len - 1], defender, lower, upper);
+      if(lower >= 3) return 0;
+      if(len == 1 && upper <= 1) return 1;
     }
     else {
-      findLiberties(b, target, moves);
-      int libs0 = b.immediateLibs(moves[0]);
-      int libs1 = b.immediateLibs(moves[1]);
-      if(libs0 == 0 && libs1 == 0 && wouldBeKoCapture(b, moves[0], attacker) && wouldBeKoCapture(b, moves[1], attacker)) {
-        if(libsAfterPlay(b, moves[0], defender, 3) <= 2 && libsAfterPlay(b, moves[1], defender, 3) <= 2) {
-          if(!hasLibertyGainingCaptures(b, target)) return true;
+      findLiberties(b, target, m, len);
+      int libs0 = b.immediateLibs(m[0]);
+      int libs1 = b.immediateLibs(m[1]);
+      if(libs0 == 0 && libs1 == 0 && wouldBeKoCapture(b, m[0], attacker) && wouldBeKoCapture(b, m[1], attacker)) {
+        if(libsAfterPlay(b, m[0], defender, 3) <= 2 && libsAfterPlay(b, m[1], defender, 3) <= 2) {
+          if(!hasLibertyGainingCaptures(b, target)) return 1;
         }
       }
-      if(!areAdjacent(b, moves[0], moves[1])) {
-        if(libs0 >= 3 && libs1 >= 3) return false;
-        else if(libs0 >= 3) moves.resize(1);
+      if(!areAdjacent(b, m[0], m[1])) {
+        if(libs0 >= 3 && libs1 >= 3) return 0;
+        else if(libs0 >= 3) len = 1;
         else if(libs1 >= 3) {
-          moves[0] = moves[1];
-          moves.resize(1);
+          m[0] = m[1];
+          len = 1;
         }
       }
-      if(moves.size() > 1) {
-        libs0 = libs0 * 2 + connectionLibsX2(b, moves[0], defender);
-        libs1 = libs1 * 2 + connectionLibsX2(b, moves[1], defender);
-        if(libs1 > libs0) std::swap(moves[0], moves[1]);
+      if(len > 1) {
+        libs0 = libs0 * 2 + connectionLibsX2(b, m[0], defender);
+        libs1 = libs1 * 2 + connectionLibsX2(b, m[1], defender);
+        if(libs1 > libs0) std::swap(m[0], m[1]);
       }
     }
-    const int8_t mover = isDefender ? defender : attacker;
-    for(size_t i = 0; i < moves.size(); i++) {
-      if(i > 0 && nodes >= LADDER_NODE_BUDGET) throw Budget();
-      if(!b.isLegalNoSuicide(moves[i], mover)) continue;
-      const GoBoard::Record rec = b.playRecorded(moves[i], mover, s);
-      nodes++;
-      bool captured;
-      try {
-        captured = level(depth + 1);
-      }
-      catch(const Budget&) {
-        b.undo(rec, s);
-        throw;
-      }
-      b.undo(rec, s);
-      if(nodes >= LADDER_NODE_BUDGET) throw Budget();
-      if(isDefender && !captured) return false;
-      if(!isDefender && captured) return true;
-    }
-    return isDefender;
+    return -1;
   }
 
-  // Board::searchIsLadderCaptured (board.cpp:1567-1790).
+  // Board::searchIsLadderCaptured (board.cpp:1567-1790): whether the chain
+  // at p is captured with best play, searched depth first over an explicit
+  // stack. The defender moves at even depths when defFirst. The search
+  // gives up (the chain escapes) after LADDER_NODE_BUDGET moves, undoing
+  // every move but leaving the root's ko point cleared, as the reference's
+  // budget exit does.
   bool captured(GoBoard& b, int p, bool defFirst) {
     if(b.color[p] != BLACK && b.color[p] != WHITE) return false;
-    const int libs = b.numLibs(p);
-    if(libs > 2 || (defFirst && libs > 1)) return false;
-    board = &b;
-    target = p;
-    defender = b.color[p];
-    attacker = opponent(defender);
-    defenderFirst = defFirst;
-    stackSize = b.xs * b.ys * 3 / 2 + 1;
-    if((int)s.movePool.size() < stackSize) s.movePool.resize(stackSize);
-    nodes = 0;
+    const int libs0 = b.numLibs(p);
+    if(libs0 > 2 || (defFirst && libs0 > 1)) return false;
+    const int8_t defender = b.color[p];
+    const int stackSize = b.xs * b.ys * 3 / 2 + 1;
+    if((int)s.frames.size() < stackSize) s.frames.resize(stackSize);
+    LadderFrame* f = s.frames.data();
     const int16_t savedKo = b.ko;
     if(defFirst) b.ko = NONE;
-    try {
-      const bool r = level(0);
-      b.ko = savedKo;
-      return r;
-    }
-    catch(const Budget&) {
-      // As the reference's budget exit: every move is undone, and the ko
-      // point cleared at the root stays cleared.
+    int nodes = 0;
+    int depth = 0;
+    bool r = false;
+    // Undoes the moves of levels 0..depth-1: the budget exit.
+    auto giveUp = [&]() {
+      for(int d = depth - 1; d >= 0; d--) b.undo(f[d].rec, s);
       return false;
+    };
+    while(true) {
+      // Enter level `depth`.
+      bool decided = true;
+      if(depth >= stackSize - 1) {
+        r = true;
+      }
+      else {
+        if(nodes >= LADDER_NODE_BUDGET) return giveUp();
+        LadderFrame& fr = f[depth];
+        fr.defender = defFirst ? (depth % 2 == 0) : (depth % 2 == 1);
+        fr.start = depth == 0 ? 0 : f[depth - 1].start + f[depth - 1].len;
+        int len = 0;
+        const int v = enter(b, p, defender, fr.defender, (size_t)fr.start, len);
+        if(v >= 0) {
+          r = v == 1;
+        }
+        else {
+          fr.len = len;
+          fr.cur = 0;
+          decided = false;
+        }
+      }
+      // Unwind decided levels and pick the next move to search.
+      while(true) {
+        if(decided) {
+          if(depth == 0) {
+            b.ko = savedKo;
+            return r;
+          }
+          depth--;
+          LadderFrame& fr = f[depth];
+          b.undo(fr.rec, s);
+          if(nodes >= LADDER_NODE_BUDGET) return giveUp();
+          if(fr.defender != r) {  // the defender escaped, or the attacker captured
+            continue;
+          }
+        }
+        LadderFrame& fr = f[depth];
+        const int8_t mover = fr.defender ? defender : opponent(defender);
+        bool played = false;
+        while(fr.cur < fr.len) {
+          const int i = fr.cur++;
+          if(i > 0 && nodes >= LADDER_NODE_BUDGET) return giveUp();
+          const int mv = s.moves[(size_t)fr.start + i];
+          if(!b.isLegalNoSuicide(mv, mover)) continue;
+          fr.rec = b.playRecorded(mv, mover, s);
+          nodes++;
+          played = true;
+          break;
+        }
+        if(played) break;
+        r = fr.defender;  // every move tried: the defender escaped none / the attacker captured with none
+        decided = true;
+      }
+      depth++;
     }
   }
 
   // Board::searchIsLadderCapturedAttackerFirst2Libs (board.cpp:1520-1565).
   bool capturedAttackerFirst2Libs(GoBoard& b, int p, std::vector<int>& working) {
+    working.clear();
     if(b.color[p] != BLACK && b.color[p] != WHITE) return false;
     if(b.numLibs(p) != 2) return false;
     const int8_t opp = opponent(b.color[p]);
-    std::vector<int> libs;
-    findLiberties(b, p, libs);
+    int libs[2];
+    int n = 0;
+    int cur = p;
+    do {
+      for(int d = 0; d < 4 && n < 2; d++) {
+        const int a = cur + ADJ[d];
+        if(b.color[a] == EMPTY && (n == 0 || libs[0] != a)) libs[n++] = a;
+      }
+      cur = b.next[cur];
+    } while(cur != p && n < 2);
+    if(n < 2) return false;
     bool works[2] = {false, false};
     for(int i = 0; i < 2; i++) {
       if(!b.isLegalNoSuicide(libs[i], opp)) continue;
@@ -740,7 +837,6 @@ struct Ladder {
       works[i] = captured(b, p, true);
       b.undo(rec, s);
     }
-    working.clear();
     if(works[0]) working.push_back(libs[0]);
     if(works[1]) working.push_back(libs[1]);
     return works[0] || works[1];
@@ -756,7 +852,7 @@ void iterLadders(const GoBoard& board, Scratch& s, F&& f) {
   int numSolved = 0;
   GoBoard copy = board;
   Ladder ladder(s);
-  std::vector<int> working;
+  std::vector<int>& working = s.working;
   for(int y = 0; y < board.ys; y++)
     for(int x = 0; x < board.xs; x++) {
       const int p = board.at(x, y);
@@ -790,6 +886,81 @@ void iterLadders(const GoBoard& board, Scratch& s, F&& f) {
       numSolved++;
       if(laddered) f(p, working);
     }
+}
+
+// The stones iterLadders reports on a board, with the working moves of the
+// first stone of each chain that has two liberties.
+void ladderHits(const GoBoard& board, Scratch& s, std::vector<LadderHit>& out) {
+  out.clear();
+  iterLadders(board, s, [&](int p, const std::vector<int>& working) {
+    LadderHit h;
+    h.point = (int16_t)p;
+    h.numWorking = 0;
+    h.working[0] = h.working[1] = 0;
+    if(board.numLibs(p) == 2)
+      for(size_t k = 0; k < working.size() && k < 2; k++) h.working[h.numWorking++] = (int16_t)working[k];
+    out.push_back(h);
+  });
+}
+
+std::atomic<int> g_ladderCacheEntries{8};
+
+// The ladder stones of board k of a position: from this thread's cache when
+// the same board (size, ko point, colours, chain order) was analysed before,
+// else computed (on `ready` when the caller has built the board) and cached.
+// The result is valid until the next call on this thread.
+const std::vector<LadderHit>& boardLadders(const kgn_position& pos, int k, const GoBoard* ready, Scratch& s) {
+  const int xs = pos.x_size, ys = pos.y_size, area = xs * ys;
+  const int8_t* colors = pos.colors[k];
+  const int16_t* ch = pos.chain_head[k];
+  const int16_t* cn = pos.chain_next[k];
+  const bool chains = ch != nullptr && cn != nullptr;
+  const int ko = pos.ko_point[k];
+  auto compute = [&](std::vector<LadderHit>& out) {
+    if(ready != nullptr) {
+      ladderHits(*ready, s, out);
+    }
+    else {
+      GoBoard b;
+      b.init(xs, ys, colors, ko, ch, cn, s);
+      ladderHits(b, s, out);
+    }
+  };
+  const int cap = g_ladderCacheEntries.load(std::memory_order_relaxed);
+  if(cap <= 0) {
+    s.cache.clear();
+    static thread_local std::vector<LadderHit> uncached;
+    compute(uncached);
+    return uncached;
+  }
+  if((int)s.cache.size() != cap) {
+    s.cache.assign((size_t)cap, LadderCacheEntry());
+    s.cacheNext = 0;
+  }
+  for(LadderCacheEntry& e : s.cache) {
+    if(!e.valid || e.xs != xs || e.ys != ys || e.ko != ko || e.chains != chains) continue;
+    if(memcmp(e.colors, colors, (size_t)area) != 0) continue;
+    bool same = true;
+    if(chains)
+      for(int i = 0; i < area && same; i++) same = colors[i] == EMPTY || (e.head[i] == ch[i] && e.next[i] == cn[i]);
+    if(same) return e.hits;
+  }
+  LadderCacheEntry& e = s.cache[s.cacheNext];
+  s.cacheNext = (s.cacheNext + 1) % (size_t)cap;
+  e.valid = false;  // until the board has been checked and searched
+  compute(e.hits);
+  e.xs = xs;
+  e.ys = ys;
+  e.ko = ko;
+  e.chains = chains;
+  memcpy(e.colors, colors, (size_t)area);
+  for(int i = 0; i < area; i++) {
+    const bool stone = chains && colors[i] != EMPTY;
+    e.head[i] = stone ? ch[i] : 0;
+    e.next[i] = stone ? cn[i] : 0;
+  }
+  e.valid = true;
+  return e.hits;
 }
 
 // ---------------------------------------------------------------------------
@@ -836,7 +1007,7 @@ void areaForPla(const GoBoard& b, int8_t pla, bool safeBig, bool unsafeBig, bool
       nextInRegion[p] = (int16_t)tail;
       tail = p;
       for(int d = 0; d < 4; d++) {
-        const int a = p + b.adj[d];
+        const int a = p + ADJ[d];
         if((b.color[a] == EMPTY || b.color[a] == opp) && regionOf[a] == -1) {
           queue[qt++] = a;
           regionOf[a] = (int16_t)r;
@@ -862,7 +1033,7 @@ void areaForPla(const GoBoard& b, int8_t pla, bool safeBig, bool unsafeBig, bool
       internal[r] = 0;
       containsOpp[r] = false;
       for(int d = 0; d < 4; d++) {
-        const int a = p + b.adj[d];
+        const int a = p + ADJ[d];
         if(b.color[a] != pla) continue;
         const int h = b.head[a];
         bool present = false;
@@ -897,7 +1068,7 @@ void areaForPla(const GoBoard& b, int8_t pla, bool safeBig, bool unsafeBig, bool
       int cur = h;
       do {
         for(int d = 0; d < 4; d++) {
-          const int a = cur + b.adj[d];
+          const int a = cur + ADJ[d];
           const int r = regionOf[a];
           if(r >= 0 && !bordersDeadByHead[regionHead[r]] && (b.color[a] == EMPTY || b.color[a] == opp)) {
             bordersDeadByHead[regionHead[r]] = true;
@@ -977,7 +1148,7 @@ void calculateIndependentLifeArea(const GoBoard& b, int8_t* result, int& whiteMi
       if(basic[p] == EMPTY || seki[p]) continue;
       bool touchesDame = false;
       for(int d = 0; d < 4; d++) {
-        const int a = p + b.adj[d];
+        const int a = p + ADJ[d];
         touchesDame = touchesDame || (b.color[a] == EMPTY && basic[a] == EMPTY);
       }
       if(!((b.color[p] == basic[p] && b.numLibs(p) == 1) || touchesDame)) continue;
@@ -988,7 +1159,7 @@ void calculateIndependentLifeArea(const GoBoard& b, int8_t* result, int& whiteMi
       while(qh != qt) {
         const int q = queue[qh++];
         for(int d = 0; d < 4; d++) {
-          const int a = q + b.adj[d];
+          const int a = q + ADJ[d];
           if(basic[a] == pla && !seki[a]) {
             seki[a] = true;
             queue[qt++] = a;
@@ -1008,7 +1179,7 @@ void calculateIndependentLifeArea(const GoBoard& b, int8_t* result, int& whiteMi
       while(qh != qt) {
         const int q = queue[qh++];
         for(int d = 0; d < 4; d++) {
-          const int a = q + b.adj[d];
+          const int a = q + ADJ[d];
           if(basic[a] == pla && result[a] != basic[a]) {
             result[a] = basic[a];
             queue[qt++] = a;
@@ -1189,29 +1360,20 @@ void featurizeOne(const kgn_position& pos, int nnX, int nnY, bool nhwc, float* r
     }
   }
 
-  // Features 14-17: ladders on this board and the two before it.
-  iterLadders(board, s, [&](int p, const std::vector<int>& working) {
-    const int x = p % board.stride - 1, y = p / board.stride - 1;
-    set(x, y, 14);
-    if(board.color[p] == opp && board.numLibs(p) > 1)
-      for(int w : working) set(w % board.stride - 1, w / board.stride - 1, 17);
-  });
-  GoBoard prev;
-  const GoBoard* prevBoard = &board;
-  if(included >= 1) {
-    if(pos.colors[1] != nullptr) prev.init(xs, ys, pos.colors[1], pos.ko_point[1], pos.chain_head[1], pos.chain_next[1], s);
-    else prev = board;
-    prevBoard = &prev;
+  // Features 14-17: ladders on this board and the two before it. A board
+  // one or two moves back that is absent (a null colour array), or that the
+  // history does not reach, is the board after it, whose stones are reused.
+  auto setGrid = [&](int p, int f) { set(p % STRIDE - 1, p / STRIDE - 1, f); };
+  const std::vector<LadderHit>* hits = &boardLadders(pos, 0, &board, s);
+  for(const LadderHit& h : *hits) {
+    setGrid(h.point, 14);
+    if(board.color[h.point] == opp)
+      for(int k = 0; k < h.numWorking; k++) setGrid(h.working[k], 17);
   }
-  iterLadders(*prevBoard, s, [&](int p, const std::vector<int>&) { set(p % board.stride - 1, p / board.stride - 1, 15); });
-  GoBoard prevPrev;
-  const GoBoard* prevPrevBoard = prevBoard;
-  if(included >= 2) {
-    if(pos.colors[2] != nullptr) prevPrev.init(xs, ys, pos.colors[2], pos.ko_point[2], pos.chain_head[2], pos.chain_next[2], s);
-    else prevPrev = *prevBoard;
-    prevPrevBoard = &prevPrev;
-  }
-  iterLadders(*prevPrevBoard, s, [&](int p, const std::vector<int>&) { set(p % board.stride - 1, p / board.stride - 1, 16); });
+  if(included >= 1 && pos.colors[1] != nullptr) hits = &boardLadders(pos, 1, nullptr, s);
+  for(const LadderHit& h : *hits) setGrid(h.point, 15);
+  if(included >= 2 && pos.colors[2] != nullptr) hits = &boardLadders(pos, 2, nullptr, s);
+  for(const LadderHit& h : *hits) setGrid(h.point, 16);
 
   // Features 20, 21: stones at the start of the second encore.
   if(pos.encore_phase >= 2)
@@ -1283,6 +1445,11 @@ void setErr(char* err, int32_t errlen, const std::string& msg) {
 
 }  // namespace
 
+extern "C" int32_t kgn_featurize_set_cache(int32_t entries) {
+  if(entries < 0 || entries > KGN_FEATURIZE_MAX_CACHE) return -1;
+  return g_ladderCacheEntries.exchange(entries);
+}
+
 extern "C" int32_t kgn_featurize(const kgn_position* positions, int32_t n, int32_t nn_x, int32_t nn_y, int32_t use_nhwc,
                                  float* spatial, float* global_out, int32_t num_threads, char* err, int32_t errlen) {
   if(n < 0 || (n > 0 && (positions == nullptr || spatial == nullptr || global_out == nullptr)) || nn_x < 1 || nn_y < 1 ||
@@ -1292,22 +1459,28 @@ extern "C" int32_t kgn_featurize(const kgn_position* positions, int32_t n, int32
   }
   const size_t rowElts = (size_t)KGN_FEATURES_SPATIAL_V7 * nn_x * nn_y;
   int threads = num_threads > 0 ? num_threads : (int)std::max(1u, std::thread::hardware_concurrency());
-  threads = std::max(1, std::min(threads, n));
+  // Each worker takes runs of consecutive positions, whose boards often
+  // recur one or two moves later (the ladder cache's hits).
+  constexpr int RUN = 8;
+  threads = std::max(1, std::min(threads, (n + RUN - 1) / RUN));
   std::atomic<int> nextRow(0);
   std::atomic<int> failedRow(-1);
   std::string failure;
   auto work = [&]() {
-    Scratch s;
+    static thread_local Scratch s;
     while(true) {
-      const int i = nextRow.fetch_add(1);
-      if(i >= n || failedRow.load() >= 0) return;
-      try {
-        featurizeOne(positions[i], nn_x, nn_y, use_nhwc != 0, spatial + rowElts * i, global_out + (size_t)KGN_FEATURES_GLOBAL_V7 * i, s);
-      }
-      catch(const std::exception& e) {
-        int expected = -1;
-        if(failedRow.compare_exchange_strong(expected, i)) failure = e.what();
-        return;
+      const int first = nextRow.fetch_add(RUN);
+      if(first >= n || failedRow.load() >= 0) return;
+      for(int i = first; i < std::min(n, first + RUN); i++) {
+        try {
+          featurizeOne(positions[i], nn_x, nn_y, use_nhwc != 0, spatial + rowElts * i,
+                       global_out + (size_t)KGN_FEATURES_GLOBAL_V7 * i, s);
+        }
+        catch(const std::exception& e) {
+          int expected = -1;
+          if(failedRow.compare_exchange_strong(expected, i)) failure = e.what();
+          return;
+        }
       }
     }
   };

@@ -738,6 +738,21 @@ class Positions:
         return a.ctypes.data
 
 
+KGN_FEATURIZE_MAX_CACHE = 64  # include/katago_featurize.h
+
+
+def featurize_set_cache(entries: int) -> int:
+    """kgn_featurize_set_cache: ladder results kept per thread for boards
+    that come again (0 turns it off); returns the previous setting."""
+    lib = host_library()
+    lib.kgn_featurize_set_cache.restype = ctypes.c_int32
+    lib.kgn_featurize_set_cache.argtypes = [ctypes.c_int32]
+    prev = lib.kgn_featurize_set_cache(entries)
+    if prev < 0:
+        raise StringError(f"kgn_featurize_set_cache: {entries} entries is out of range")
+    return prev
+
+
 def featurize(positions: Positions, nn_x: int = 19, nn_y: int = 19, use_nhwc: bool = True, num_threads: int = 0):
     """kgn_featurize: returns spatial [n, nn_y*nn_x*22] (NHWC or NCHW per
     row) and global [n, 19] float32 arrays."""

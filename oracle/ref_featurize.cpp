@@ -17,8 +17,15 @@
 // KataGo's own fillRowV7 on every position of a random game:
 //   compare <name> <seed> <xSize> <ySize> <nnXLen> <nnYLen> <numMoves> <rules> <fixtureEvery>
 // which prints a summary line and, every fixtureEvery positions, the
-// position with KataGo's rows as a fixture line.
+// position with KataGo's rows as a fixture line; and, to time both
+// featurizers on the same positions (each on one thread):
+//   time <name> <seed> <xSize> <ySize> <nnXLen> <nnYLen> <numMoves> <rules> <reps>
+// which plays one random game, keeps every position, and prints the
+// microseconds per position of KataGo's fillRowV7, of kgn_featurize over the
+// prebuilt positions in one single-threaded call with its ladder cache off
+// and on, and of positionFromHistory + kgn_featurize one position per call.
 // Output on stdout: one JSON object per position and line.
+#include <chrono>
 #include <cstdio>
 #include <iostream>
 #include <sstream>
@@ -219,6 +226,97 @@ int compareOne(const string& name, const Board& board, const BoardHistory& hist,
   return diffs;
 }
 
+// Random play as the compare command plays it: mostly legal moves, passes
+// now and then, two forced passes at half, seven tenths and nine tenths.
+Loc randomMove(const Board& board, const BoardHistory& hist, Player pla, Rand& rand, int m, int moves) {
+  vector<Loc> cands;
+  for(int y = 0; y < board.y_size; y++)
+    for(int x = 0; x < board.x_size; x++) {
+      Loc loc = Location::getLoc(x, y, board.x_size);
+      if(hist.isLegal(board, loc, pla)) cands.push_back(loc);
+    }
+  const bool forcedPass = m == moves / 2 || m == moves / 2 + 1 || m == moves * 7 / 10 || m == moves * 7 / 10 + 1 ||
+                          m == moves * 9 / 10 || m == moves * 9 / 10 + 1;
+  return forcedPass || cands.empty() || rand.nextUInt(30) == 0 ? Board::PASS_LOC : cands[rand.nextUInt((uint32_t)cands.size())];
+}
+
+double secondsSince(std::chrono::steady_clock::time_point t0) {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+
+void timeGame(const string& name, uint64_t seed, int xs, int ys, int nnX, int nnY, int moves, const string& rulesS, int reps) {
+  Board board(xs, ys);
+  Player pla = P_BLACK;
+  BoardHistory hist(board, pla, rulesNamed(rulesS), 0);
+  Rand rand(seed);
+  vector<Board> boards;
+  vector<BoardHistory> hists;
+  vector<Player> plas;
+  for(int m = 0; m <= moves; m++) {
+    boards.push_back(board);
+    hists.push_back(hist);
+    plas.push_back(pla);
+    if(m == moves || hist.isGameFinished) break;
+    hist.makeBoardMoveAssumeLegal(board, randomMove(board, hist, pla, rand, m, moves), pla, nullptr);
+    pla = getOpp(pla);
+  }
+  const int n = (int)boards.size();
+  MiscNNInputParams params;
+  const int C = NNInputs::NUM_FEATURES_SPATIAL_V7, G = NNInputs::NUM_FEATURES_GLOBAL_V7;
+  const size_t rowS = (size_t)C * nnX * nnY;
+  vector<float> spatial(rowS * n), global((size_t)G * n), sink(rowS), gsink(G);
+  char err[512];
+
+  auto t0 = std::chrono::steady_clock::now();
+  for(int r = 0; r < reps; r++)
+    for(int i = 0; i < n; i++)
+      NNInputs::fillRowV7(boards[i], hists[i], plas[i], params, nnX, nnY, true, sink.data(), gsink.data());
+  const double ref = secondsSince(t0) / ((double)reps * n);
+
+  vector<kgn_position> pos(n);
+  vector<HipBackend::PositionStorage> storage(n);
+  for(int i = 0; i < n; i++) HipBackend::positionFromHistory(boards[i], hists[i], plas[i], params, pos[i], storage[i]);
+  // kgn_featurize over the whole game in one single-threaded call, with the
+  // ladder cache off and then on (emptied first: a cache size change clears
+  // it, so no board of an earlier pass is found).
+  double batch[2];
+  for(int cached = 0; cached < 2; cached++) {
+    kgn_featurize_set_cache(0);
+    if(kgn_featurize(pos.data(), 1, nnX, nnY, 1, spatial.data(), global.data(), 1, err, sizeof(err)) != 0)
+      throw StringError(string("kgn_featurize failed: ") + err);
+    kgn_featurize_set_cache(cached ? 8 : 0);
+    t0 = std::chrono::steady_clock::now();
+    for(int r = 0; r < reps; r++) {
+      if(r > 0 && cached) {
+        kgn_featurize_set_cache(0);
+        if(kgn_featurize(pos.data(), 1, nnX, nnY, 1, spatial.data(), global.data(), 1, err, sizeof(err)) != 0)
+          throw StringError(string("kgn_featurize failed: ") + err);
+        kgn_featurize_set_cache(8);
+      }
+      if(kgn_featurize(pos.data(), n, nnX, nnY, 1, spatial.data(), global.data(), 1, err, sizeof(err)) != 0)
+        throw StringError(string("kgn_featurize failed: ") + err);
+    }
+    batch[cached] = secondsSince(t0) / ((double)reps * n);
+  }
+  // One position per call, converting each from KataGo's objects, as
+  // NNEvaluator::evaluate would call it (cache on, emptied first).
+  kgn_featurize_set_cache(0);
+  kgn_featurize_set_cache(8);
+  t0 = std::chrono::steady_clock::now();
+  for(int i = 0; i < n; i++) {
+    HipBackend::positionFromHistory(boards[i], hists[i], plas[i], params, pos[i], storage[i]);
+    if(kgn_featurize(&pos[i], 1, nnX, nnY, 1, sink.data(), gsink.data(), 1, err, sizeof(err)) != 0)
+      throw StringError(string("kgn_featurize failed: ") + err);
+  }
+  const double perCall = secondsSince(t0) / n;
+  char line[512];
+  snprintf(line, sizeof(line),
+           "{\"timing\":\"%s\",\"positions\":%d,\"reps\":%d,\"fillRowV7_us\":%.3f,\"featurize_uncached_us\":%.3f,"
+           "\"featurize_cached_us\":%.3f,\"adapter_plus_featurize_cached_us\":%.3f}",
+           name.c_str(), n, reps, ref * 1e6, batch[0] * 1e6, batch[1] * 1e6, perCall * 1e6);
+  std::cout << line << std::endl;
+}
+
 }  // namespace
 
 int main() {
@@ -297,6 +395,13 @@ int main() {
       }
       std::cout << "{\"summary\":\"" << name << "\",\"positions\":" << positions << ",\"mismatched\":" << mismatched
                 << ",\"first_diff\":\"" << firstDiff << "\"}" << std::endl;
+    }
+    else if(word == "time") {
+      string name, rulesS;
+      uint64_t seed;
+      int xs, ys, nnX, nnY, moves, reps;
+      std::cin >> name >> seed >> xs >> ys >> nnX >> nnY >> moves >> rulesS >> reps;
+      timeGame(name, seed, xs, ys, nnX, nnY, moves, rulesS, reps);
     }
     else {
       std::cerr << "unknown record " << word << std::endl;

@@ -79,6 +79,28 @@ def test_featurizer_threads_give_the_same_rows():
     assert np.array_equal(one[0], many[0]) and np.array_equal(one[1], many[1])
 
 
+def test_featurizer_ladder_cache_gives_the_same_rows():
+    """The per-thread ladder cache (kgn_featurize_set_cache) keys a board by
+    its size, ko point, colours and chain order: rows computed with boards
+    found in it equal rows computed without it, also when the same colours
+    come with and without chain links, and across threads."""
+    group = [fx for fx in FIXTURES if fx["nnx"] == 19 and fx["nny"] == 19][:20]
+    with_links, without_links = nn.Positions(group), nn.Positions(group, with_chain_order=False)
+    prev = nn.featurize_set_cache(0)
+    try:
+        ref_links = nn.featurize(with_links, 19, 19, num_threads=1)
+        ref_plain = nn.featurize(without_links, 19, 19, num_threads=1)
+        nn.featurize_set_cache(nn.KGN_FEATURIZE_MAX_CACHE)
+        for threads in (1, 1, 3):  # the second pass finds every board of the first
+            for pos, ref in ((with_links, ref_links), (without_links, ref_plain), (with_links, ref_links)):
+                got = nn.featurize(pos, 19, 19, num_threads=threads)
+                assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])
+        with pytest.raises(nn.StringError):
+            nn.featurize_set_cache(nn.KGN_FEATURIZE_MAX_CACHE + 1)
+    finally:
+        nn.featurize_set_cache(prev)
+
+
 def test_featurizer_without_chain_order_differs_only_in_rare_ladder_cases():
     """Without KataGo's chain links each chain is linked breadth-first from
     its first stone: the ladder search's early exit that reads a move list's
