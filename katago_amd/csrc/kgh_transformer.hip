@@ -199,11 +199,13 @@ __global__ void ropeKernel(T* __restrict__ qkv, int ld, int H, int KV, int dq, c
 }
 
 // ---------------------------------------------------------------------------
-// Attention with matrix cores (fp16). One workgroup of 12 wave64s per
-// (board, query head); K (row-major, rows padded by 16 bytes) and V
-// (transposed, [dim][key], rows padded by 8 bytes) of the board's kv head are
-// staged in LDS once, so each wave then streams the keys from LDS with no
-// further barrier. Wave w owns queries 32w .. 32w+31 and, per block of 32
+// Attention with matrix cores (fp16). A workgroup of 12 wave64s takes the
+// (board, query head) items blockIdx.x, blockIdx.x + gridDim.x, ... in turn
+// (one workgroup per CU: the LDS holds one item); K (row-major, rows padded
+// by 16 bytes) and V (transposed, [dim][key], rows padded by 8 bytes) of the
+// item's kv head are staged in LDS once, so each wave then streams the keys
+// from LDS with no further barrier, while the next item's K and V rows load
+// into registers. Wave w owns queries 32w .. 32w+31 and, per block of 32
 // keys, computes S^T = K Q^T (lane = query, 16 keys per lane), an online
 // softmax per lane, and O^T += V^T P^T with P taken straight from the
 // accumulator registers: the key order inside the second product's k slots
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
                                                                      int KV, const float* __restrict__ mask, int HW,
                                                                      half_t* __restrict__ out, int ldOut, float scale,
                                                                      const float* __restrict__ cosT, const float* __restrict__ sinT,
-                                                                     int learnable) {
+                                                                     int learnable, int items) {
   static_assert(DQ % 16 == 0 && DV % 16 == 0 && DQ <= 64 && DV <= 64, "head dims (LDS holds all keys)");
   constexpr int DVP = (DV + 31) / 32 * 32;
   constexpr int KLD = DQ + 8;             // halves per K row (16-byte pad)
@@ -253,7 +255,8 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
   uint4 kRows[K_ITERS];
   uint4 vRows[V_ITERS];
   float keyMask = 0.0f;
-  auto fetch = [&](int item) {
+  // The item's K rows and key mask, then its V rows, into registers.
+  auto fetchK = [&](int item) {
     const int n = item / H;
     const int kvh = (item - n * H) / (H / KV);
     const size_t rowBase = (size_t)n * HW;
@@ -264,6 +267,12 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
       const int g = i - key * (DQ / 8);
       kRows[it] = key < HW ? *(const uint4*)(qkv + (rowBase + key) * ld + kOff + kvh * DQ + g * 8) : make_uint4(0, 0, 0, 0);
     }
+    keyMask = tid < HW ? mask[rowBase + tid] : 0.0f;
+  };
+  auto fetchV = [&](int item) {
+    const int n = item / H;
+    const int kvh = (item - n * H) / (H / KV);
+    const size_t rowBase = (size_t)n * HW;
 #pragma unroll
     for(int it = 0; it < V_ITERS; it++) {
       const int i = tid + it * FA_THREADS;
@@ -271,7 +280,6 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
       const int g = i - key * (DVP / 8);
       vRows[it] = key < HW && g * 8 < DV ? *(const uint4*)(qkv + (rowBase + key) * ld + vOff + kvh * DV + g * 8) : make_uint4(0, 0, 0, 0);
     }
-    keyMask = tid < HW ? mask[rowBase + tid] : 0.0f;
   };
   // Writes the loaded K rows (rotated when cosT is set), V^T and key mask
   // into LDS.
@@ -313,9 +321,9 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
     if(tid < FA_MAX_KEYS) keyBias[tid] = (tid < HW && keyMask != 0.0f) ? 0.0f : -INFINITY;
   };
 
+  // Computes item from the staged LDS (every wave reaches the end: the
+  // barriers around it are uniform).
   auto attend = [&](int item) {
-    stage(item);
-    __syncthreads();
     const int n = item / H;
     const int h = item - n * H;
     const size_t rowBase = (size_t)n * HW;
@@ -439,8 +447,22 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
       }
     }
   };
-  fetch(blockIdx.x);
-  attend(blockIdx.x);
+  // The next item's K rows load during this item's attention (registers
+  // allow one of the two), its V rows right after.
+  int item = blockIdx.x;
+  fetchK(item);
+  fetchV(item);
+  while(true) {
+    stage(item);
+    __syncthreads();
+    const int nextItem = item + (int)gridDim.x;
+    if(nextItem < items) fetchK(nextItem);
+    attend(item);
+    if(nextItem >= items) break;
+    fetchV(nextItem);
+    __syncthreads();  // every wave is done with the LDS before it is restaged
+    item = nextItem;
+  }
 }
 
 // Attention without matrix cores, for fp32 contexts and head shapes the
@@ -487,11 +509,31 @@ __global__ void attentionSimpleKernel(const T* __restrict__ qkv, int ld, int kOf
   for(int e = 0; e < dv; e++) dst[e] = kgh_from_float<T>(acc[e] * inv);
 }
 
+// The current device's compute units (one attention workgroup fits each).
+int deviceComputeUnits() {
+  static thread_local int cachedDevice = -1, cachedCUs = 0;
+  int dev = 0;
+  KGH_HIP_CHECK(hipGetDevice(&dev));
+  if(dev != cachedDevice) {
+    int cus = 0;
+    KGH_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    cachedCUs = cus > 0 ? cus : 1;
+    cachedDevice = dev;
+  }
+  return cachedCUs;
+}
+
 template<int DQ, int DV>
 bool launchFlash(const half_t* qkv, int ld, int kOff, int vOff, int H, int KV, const float* mask, int HW, int batch, half_t* out,
                  int ldOut, float scale, const float* cosT, const float* sinT, bool learnable, hipStream_t stream) {
-  hipLaunchKernelGGL((flashAttentionKernel<DQ, DV>), dim3(batch * H), dim3(FA_THREADS), 0, stream, qkv, ld, kOff, vOff, H, KV, mask, HW,
-                     out, ldOut, scale, cosT, sinT, learnable ? 1 : 0);
+  // As many workgroups as the CUs hold at once (the LDS of one item each).
+  constexpr int DVP = (DV + 31) / 32 * 32;
+  constexpr int ldsBytes = FA_MAX_KEYS * (DQ + 8) * 2 + DVP * (FA_MAX_KEYS + 4) * 2 + FA_MAX_KEYS * 4;
+  constexpr int perCU = std::max(1, 163840 / ldsBytes);
+  const int items = batch * H;
+  const int grid = std::min(items, perCU * deviceComputeUnits());
+  hipLaunchKernelGGL((flashAttentionKernel<DQ, DV>), dim3(grid), dim3(FA_THREADS), 0, stream, qkv, ld, kOff, vOff, H, KV, mask, HW,
+                     out, ldOut, scale, cosT, sinT, learnable ? 1 : 0, items);
   KGH_CHECK_LAUNCH();
   return true;
 }
