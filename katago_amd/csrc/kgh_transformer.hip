@@ -233,6 +233,7 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
   __shared__ __attribute__((aligned(16))) half_t Ks[FA_MAX_KEYS * KLD];
   __shared__ __attribute__((aligned(16))) half_t Vt[DVP * VLD];
   __shared__ float keyBias[FA_MAX_KEYS];  // 0 for a valid key, -inf for a masked one or one past HW
+  __shared__ int tileFull[FA_MAX_KEYS / 32];  // 1: every key of the 32-key tile is valid (its bias is 0)
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -318,7 +319,15 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
 #pragma unroll
       for(int j = 0; j < 8; j++) Vt[(g * 8 + j) * VLD + key] = v[j];
     }
-    if(tid < FA_MAX_KEYS) keyBias[tid] = (tid < HW && keyMask != 0.0f) ? 0.0f : -INFINITY;
+    const bool validKey = tid < HW && keyMask != 0.0f;
+    if(tid < FA_MAX_KEYS) keyBias[tid] = validKey ? 0.0f : -INFINITY;
+    // Waves 0 .. FA_MAX_KEYS/64 - 1 cover the keys: a wave's two 32-key
+    // tiles from the two halves of its ballot.
+    const unsigned long long valid = __ballot(validKey);
+    if(tid < FA_MAX_KEYS && lane == 0) {
+      tileFull[2 * wave] = (unsigned)valid == 0xffffffffu;
+      tileFull[2 * wave + 1] = (unsigned)(valid >> 32) == 0xffffffffu;
+    }
   };
 
   // Computes item from the staged LDS (every wave reaches the end: the
@@ -357,9 +366,14 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
 #pragma unroll
         for(int r = 0; r < 16; r++) o[db][r] = 0.0f;
       // Scores stay unscaled (scale > 0 keeps their order); the exponent
-      // scales them by c = scale * log2(e): p = 2^(s c - m c).
+      // scales them by c = scale * log2(e): p = 2^(s c - r), with r a
+      // reference point that only moves when a tile's maximum passes it by
+      // more than 8 (p stays at most 256, exact enough in fp16 and summed in
+      // fp32), so the output accumulators are rescaled about once per query
+      // instead of whenever the running maximum grows. The normalization by
+      // the sum of the same p makes the choice of r cancel.
       const float c = scale * 1.44269504088896341f;
-      float mRun = -INFINITY, lRun = 0.0f;
+      float rRef = -INFINITY, lRun = 0.0f;
 
       // S^T of the 32-key block at kb.
       auto scores = [&](int kb, floatx16& sc) {
@@ -371,38 +385,46 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
           sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], sc, 0, 0, 0);
         }
       };
-      const int keyTiles = (HW + 31) / 32;
-      floatx16 sNext;
-      scores(0, sNext);
-      for(int kt = 0; kt < keyTiles; kt++) {
+      // One 32-key tile: the softmax of its scores s (computed earlier) and
+      // O^T += V^T P^T; the next tile's scores go into sNext first, so the
+      // matrix cores run them meanwhile. Called with the two score buffers
+      // alternating, so no registers are copied between tiles.
+      auto tile = [&](int kt, floatx16& s, floatx16& sNext, int keyTiles) {
         const int kb = kt * 32;
-        floatx16 s = sNext;
         if(kt + 1 < keyTiles) scores(kb + 32, sNext);
+        // A tile of valid keys adds a zero bias: skipped (wave-uniform).
+        if(!tileFull[kt]) {
+#pragma unroll
+          for(int r = 0; r < 16; r++) s[r] += keyBias[kb + (r >> 2) * 8 + kq * 4 + (r & 3)];
+        }
         float mTile = -INFINITY;
 #pragma unroll
-        for(int r = 0; r < 16; r++) {
-          s[r] += keyBias[kb + (r >> 2) * 8 + kq * 4 + (r & 3)];
-          mTile = fmaxf(mTile, s[r]);
-        }
+        for(int r = 0; r < 16; r++) mTile = fmaxf(mTile, s[r]);
         mTile = fmaxf(mTile, __shfl_xor(mTile, 32));
         // Every lane runs every matrix instruction (no divergence around
-        // them): while a query has seen no valid key, mNew is -inf and the
-        // reference point 0 makes corr and every p exactly 0.
-        const float mNew = fmaxf(mRun, mTile);
-        const float mRef = mNew == -INFINITY ? 0.0f : mNew;
-        const float corr = __builtin_amdgcn_exp2f((mRun - mRef) * c);
-        const float negM = -mRef * c;
-        float psum = 0.0f;
+        // them): while a query has seen no valid key, rRef is -inf, the
+        // exponent's offset 0 makes every p exactly 0 (masked scores are
+        // -inf), and the first finite maximum moves rRef with corr = 0 on
+        // accumulators that are still 0.
+        const float tileRef = mTile * c;
+        float corr = 1.0f;
+        if(tileRef > rRef + 8.0f) {
+          corr = __builtin_amdgcn_exp2f(rRef - tileRef);
+          rRef = tileRef;
+        }
+        const float negM = rRef == -INFINITY ? 0.0f : -rRef;
+        // Four partial sums (a shallow dependency chain), then their sum.
+        float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for(int r = 0; r < 16; r++) {
           const float p = __builtin_amdgcn_exp2f(fmaf(s[r], c, negM));
           s[r] = p;
-          psum += p;
+          part[r & 3] += p;
         }
+        float psum = (part[0] + part[1]) + (part[2] + part[3]);
         psum += __shfl_xor(psum, 32);
         lRun = lRun * corr + psum;
-        mRun = mNew;
-        // corr is exactly 1 for a query whose running maximum did not move,
+        // corr is exactly 1 for a query whose reference point did not move,
         // and the rescale is skipped when that holds for the whole wave.
         if(__any(corr != 1.0f)) {
 #pragma unroll
@@ -425,6 +447,13 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, o[db], 0, 0, 0);
           }
         }
+      };
+      const int keyTiles = (HW + 31) / 32;
+      floatx16 sA, sB;
+      scores(0, sA);
+      for(int kt = 0; kt < keyTiles; kt += 2) {
+        tile(kt, sA, sB, keyTiles);
+        if(kt + 1 < keyTiles) tile(kt + 1, sB, sA, keyTiles);
       }
 
       if(qi < HW) {
