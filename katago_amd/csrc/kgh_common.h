@@ -175,26 +175,36 @@ struct ConvEpilogue {
   int ropeLearnable;
 };
 
-// One rotated pair, as the rotary-embedding kernels compute it.
+// One rotated pair, as every kernel that rotates computes it. The fused
+// multiply-adds are explicit: left to the compiler's contraction, which
+// product it fuses depends on the code around the inlined call, and the
+// kernels (and their variants) must round the same way bit for bit.
 __device__ __forceinline__ void kgh_rope_pair(float x0, float x1, float c, float s, float& y0, float& y1) {
-  y0 = x0 * c - x1 * s;
-  y1 = x0 * s + x1 * c;
+  y0 = fmaf(x0, c, -(x1 * s));
+  y1 = fmaf(x0, s, x1 * c);
 }
 
 // The rotary embedding of one lane's 16 stored channels c0.. of a row at
 // board position xy (see ConvEpilogue): c0 is a multiple of 16, so the 8
 // pairs lie in one head and their table entries are contiguous.
+// The table entries of those 8 pairs (cosines, then sines), loaded ahead of
+// their use by kgh_rope_apply.
 template<typename T>
-__device__ __forceinline__ void kgh_rope_stored(const ConvEpilogue<T>& e, int xy, int HW, int c0, T (&o)[16]) {
+__device__ __forceinline__ void kgh_rope_load(const ConvEpilogue<T>& e, int xy, int HW, int c0, float4 (&cs)[2], float4 (&sn)[2]) {
   const int head = c0 >> e.ropeDqShift;
   const int pairs = e.ropeDq >> 1;
   const int table = !e.ropeLearnable ? 0 : c0 < e.ropeQC ? head / e.ropeGroup : head - (e.ropeQC >> e.ropeDqShift);
   const size_t ti = ((size_t)table * HW + xy) * pairs + ((c0 & (e.ropeDq - 1)) >> 1);
-  float cs[8], sn[8];
-  *(float4*)&cs[0] = *(const float4*)(e.ropeCos + ti);
-  *(float4*)&cs[4] = *(const float4*)(e.ropeCos + ti + 4);
-  *(float4*)&sn[0] = *(const float4*)(e.ropeSin + ti);
-  *(float4*)&sn[4] = *(const float4*)(e.ropeSin + ti + 4);
+  cs[0] = *(const float4*)(e.ropeCos + ti);
+  cs[1] = *(const float4*)(e.ropeCos + ti + 4);
+  sn[0] = *(const float4*)(e.ropeSin + ti);
+  sn[1] = *(const float4*)(e.ropeSin + ti + 4);
+}
+
+template<typename T>
+__device__ __forceinline__ void kgh_rope_apply(const float4 (&cs4)[2], const float4 (&sn4)[2], T (&o)[16]) {
+  const float* cs = (const float*)cs4;
+  const float* sn = (const float*)sn4;
 #pragma unroll
   for(int q = 0; q < 8; q++) {
     float y0, y1;
@@ -202,6 +212,13 @@ __device__ __forceinline__ void kgh_rope_stored(const ConvEpilogue<T>& e, int xy
     o[2 * q] = kgh_from_float<T>(y0);
     o[2 * q + 1] = kgh_from_float<T>(y1);
   }
+}
+
+template<typename T>
+__device__ __forceinline__ void kgh_rope_stored(const ConvEpilogue<T>& e, int xy, int HW, int c0, T (&o)[16]) {
+  float4 cs[2], sn[2];
+  kgh_rope_load(e, xy, HW, c0, cs, sn);
+  kgh_rope_apply(cs, sn, o);
 }
 
 // The consumer row scale of a folded RMSNorm (see ConvEpilogue): the block
