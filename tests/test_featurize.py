@@ -83,16 +83,30 @@ def test_featurizer_ladder_cache_gives_the_same_rows():
     """The per-thread ladder cache (kgn_featurize_set_cache) keys a board by
     its size, ko point, colours and chain order: rows computed with boards
     found in it equal rows computed without it, also when the same colours
-    come with and without chain links, and across threads."""
+    come with and without chain links or with another ko point, and across
+    threads."""
     group = [fx for fx in FIXTURES if fx["nnx"] == 19 and fx["nny"] == 19][:20]
+    # The same boards with another ko point on each (an empty point of the
+    # current and the previous board): cached results must not be reused.
+    moved = []
+    for fx in group:
+        c = dict(fx)
+        c["ko_point"] = list(fx["ko_point"])
+        for k in (0, 1):
+            empties = [i for i, v in enumerate(fx["colors"][k]) if v == 0 and i != fx["ko_point"][k]]
+            if empties:
+                c["ko_point"][k] = empties[len(empties) // 2]
+        moved.append(c)
     with_links, without_links = nn.Positions(group), nn.Positions(group, with_chain_order=False)
+    ko_moved = nn.Positions(moved)
     prev = nn.featurize_set_cache(0)
     try:
         ref_links = nn.featurize(with_links, 19, 19, num_threads=1)
         ref_plain = nn.featurize(without_links, 19, 19, num_threads=1)
+        ref_moved = nn.featurize(ko_moved, 19, 19, num_threads=1)
         nn.featurize_set_cache(nn.KGN_FEATURIZE_MAX_CACHE)
         for threads in (1, 1, 3):  # the second pass finds every board of the first
-            for pos, ref in ((with_links, ref_links), (without_links, ref_plain), (with_links, ref_links)):
+            for pos, ref in ((with_links, ref_links), (without_links, ref_plain), (ko_moved, ref_moved), (with_links, ref_links)):
                 got = nn.featurize(pos, 19, 19, num_threads=threads)
                 assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])
         with pytest.raises(nn.StringError):
