@@ -379,6 +379,26 @@ def test_rows_do_not_depend_on_batch_size(model_dir, cfg_index):
             assert same, f"batch {n} vs {n_max}, {k}: max-abs {np.abs(out[k] - full[k][:n]).max()}"
 
 
+def test_attention_items_per_workgroup_do_not_change_rows():
+    """The fp16 attention kernel launches as many workgroups as the CUs hold
+    and each takes (board, head) items in turn, the next item's K rows
+    loading during the current one. A net with 6 query heads of 32 dims
+    (values 16 wide: the 32/16 kernel, two workgroups per CU) at 100 boards
+    gives 600 items, more than the 512 workgroups, so some take two: every
+    board's row equals the row of a batch with one item per workgroup."""
+    import pytorch_golden as pg
+    lm = nn.LoadedModel(pg.model_path("b2c96h6kv3qk32v16tflrs-silu-rsnh"))
+    n = 100
+    h = nn.ComputeHandle(nn.ComputeContext(lm, 19, 19, use_fp16=True), max_batch=n)
+    sp, gl = modelgen.synthetic_inputs(11, n, board_sizes=(19, 13))
+    full = h.get_output(sp, gl)
+    for lo, hi in ((0, 3), (40, 47), (97, 100)):
+        part = h.get_output(sp[lo:hi], gl[lo:hi])
+        for k in full:
+            assert np.isfinite(part[k]).all(), k
+            assert np.array_equal(part[k], full[k][lo:hi]), (lo, hi, k)
+
+
 def test_nchw_rows_match_oracle(model_dir):
     """getOutput with inputsUseNHWC = false (rows in NCHW order, as the
     OpenCL/TensorRT/Metal backends take them, setup.cpp:145)."""
