@@ -332,7 +332,7 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
 
   // Computes item from the staged LDS (every wave reaches the end: the
   // barriers around it are uniform).
-  auto attend = [&](int item) {
+  auto attend = [&](int item, int nextItem) {
     const int n = item / H;
     const int h = item - n * H;
     const size_t rowBase = (size_t)n * HW;
@@ -358,6 +358,10 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
         }
       }
     }
+    // The next item's K rows load during this item's key loop, issued after
+    // the query fragments: a wave's memory operations are waited on in issue
+    // order, so loads issued before them would delay their first use.
+    if(nextItem < items) fetchK(nextItem);
 
     if(q0 < HW) {
       floatx16 o[DVP / 32];
@@ -485,8 +489,7 @@ __global__ __launch_bounds__(FA_THREADS, 1) void flashAttentionKernel(const half
     stage(item);
     __syncthreads();
     const int nextItem = item + (int)gridDim.x;
-    if(nextItem < items) fetchK(nextItem);
-    attend(item);
+    attend(item, nextItem);
     if(nextItem >= items) break;
     fetchV(nextItem);
     __syncthreads();  // every wave is done with the LDS before it is restaged
