@@ -379,6 +379,21 @@ def test_rows_do_not_depend_on_batch_size(model_dir, cfg_index):
             assert same, f"batch {n} vs {n_max}, {k}: max-abs {np.abs(out[k] - full[k][:n]).max()}"
 
 
+@pytest.mark.parametrize("cfg_index,n,fp16", [(3, 1024, True), (4, 512, True), (1, 2048, True), (0, 1024, False)],
+                         ids=["b18c384nbt-mixed-1024", "t12d384h6-512", "b10c128-2048", "b6c96-fp32-1024"])
+def test_large_batches_rows_match_small_batch(model_dir, cfg_index, n, fp16):
+    """Batches well past the benchmark sizes: four boards per CU in the
+    one-board 3x3 kernel, thousands of 1x1 tiles, twelve attention items per
+    workgroup, the fp32 3x3 kernel's 34,656 workgroups. The first, middle
+    and last rows of mixed board sizes are bitwise equal to the same rows run
+    as a small batch."""
+    cfg = modelgen.configs()[cfg_index]
+    lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
+    h = nn.ComputeHandle(nn.ComputeContext(lm, 19, 19, use_fp16=fp16), max_batch=n)
+    sp, gl = modelgen.synthetic_inputs(cfg.input_seed, n, board_sizes=(9, 13, 19))
+    _rows_match_small_batch(h, sp, gl, [0, 1, n // 2, n - 2, n - 1], label=f"config {cfg_index} batch {n}")
+
+
 def test_attention_items_per_workgroup_do_not_change_rows():
     """The fp16 attention kernel launches as many workgroups as the CUs hold
     and each takes (board, head) items in turn, the next item's K rows
