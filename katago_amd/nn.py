@@ -111,6 +111,13 @@ def host_library() -> ctypes.CDLL:
     return _host
 
 
+def _as_rows(a, n: int):
+    """a as a contiguous float32 [n, row] array; an empty batch stays empty
+    (reshape cannot infer a row length from zero rows)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a.reshape(n, a.size // n if n else 0)
+
+
 def _errbuf():
     return ctypes.create_string_buffer(4096)
 
@@ -248,8 +255,8 @@ class ComputeHandle:
         lib = host_library()
         n = int(np.asarray(global_in).shape[0])
         hw = self.context.nn_x * self.context.nn_y
-        spatial = np.ascontiguousarray(spatial, dtype=np.float32).reshape(n, -1)
-        global_in = np.ascontiguousarray(global_in, dtype=np.float32).reshape(n, -1)
+        spatial = _as_rows(spatial, n)
+        global_in = _as_rows(global_in, n)
         sym = np.ascontiguousarray(np.zeros(n) if symmetry is None else symmetry, dtype=np.int32)
         opt = np.ascontiguousarray(np.zeros(n) if policy_optimism is None else policy_optimism, dtype=np.float32)
         policy = np.zeros((n, hw + 1), np.float32)
@@ -271,8 +278,8 @@ class ComputeHandle:
         lib = host_library()
         n = int(np.asarray(global_in).shape[0])
         hw = self.context.nn_x * self.context.nn_y
-        spatial = np.ascontiguousarray(spatial, dtype=np.float32).reshape(n, -1)
-        global_in = np.ascontiguousarray(global_in, dtype=np.float32).reshape(n, -1)
+        spatial = _as_rows(spatial, n)
+        global_in = _as_rows(global_in, n)
         legal = np.ascontiguousarray(legal, dtype=np.uint8).reshape(n, hw + 1)
         info = np.ascontiguousarray(row_info, dtype=np.int32)
         temp = np.ascontiguousarray(np.ones(n) if temperature is None else temperature, dtype=np.float32)

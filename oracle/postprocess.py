@@ -9,7 +9,9 @@ Parity pins (tests/test_postprocess.py): closed forms (uniform policy, the
 95% pass cap, temperature as a power of the probabilities, softmax sums,
 perspective flips, the softplus-based score stdev, the short-term error
 formulas of each model-version branch), hand-computed known answers, and the
-reference's own invariants (illegal moves -1, off-board ownership 0).
+reference's own invariants (illegal moves -1, off-board ownership 0), and
+its two errors for non-finite results (a NaN logit of a legal move, a NaN
+value or score field).
 """
 from __future__ import annotations
 
@@ -140,6 +142,9 @@ def postprocess_row(policy, value, score, ownership, legal, *, nn_x: int, nn_y: 
     else:
         st_wl = soft_plus(stw * osm)
         st_sc = soft_plus(sts * osm) * 10.0
+    # nneval.cpp:1167-1184.
+    if not all(math.isfinite(v) for v in (prob_sum, score_mean, score_mean_sq, lead_v, var_time_left, st_wl, st_sc)):
+        raise ValueError("Got nonfinite for nneval value")
     if white_to_move:
         vals = [win, loss, no_result, score_mean, score_mean_sq, lead_v]
     else:

@@ -490,6 +490,8 @@ def test_errors_are_raised_not_crashed(model_dir):
     sp, gl = modelgen.synthetic_inputs(1, 3)
     with pytest.raises(nn.StringError, match="numBatchEltsFilled"):
         h.get_output(sp, gl)
+    with pytest.raises(nn.StringError, match="numBatchEltsFilled"):
+        h.get_output(sp[:0], gl[:0])
     with pytest.raises(nn.StringError, match="symmetry"):
         h.get_output(sp[:1], gl[:1], symmetry=[9])
 

@@ -139,6 +139,32 @@ def test_no_legal_move_is_an_error():
         _row(np.zeros(HW + 1), legal=np.zeros(HW + 1, bool))
 
 
+def test_nonfinite_results_are_errors():
+    """nneval.cpp:1012-1016 and 1167-1184: a NaN or infinite logit of a
+    legal move makes the policy sum non-finite; a NaN value or score field
+    makes the value results non-finite. Both are errors. A NaN on an illegal
+    move is never read."""
+    with np.errstate(invalid="ignore"):
+        for bad in (np.nan, np.inf):
+            pol = np.zeros(HW + 1, np.float32)
+            pol[40] = bad
+            with pytest.raises(ValueError, match="nonfinite for policy sum"):
+                _row(pol)
+        legal = np.ones(HW + 1, bool)
+        legal[40] = False
+        pol = np.zeros(HW + 1, np.float32)
+        pol[40] = np.nan
+        probs, _, _ = _row(pol, legal=legal)
+        assert probs[40] == -1.0 and np.isclose(probs[legal].sum(), 1.0)
+        with pytest.raises(ValueError, match="nonfinite for nneval value"):
+            _row(np.zeros(HW + 1), value=(np.nan, 0.0, 0.0))
+        for field in range(6):
+            score = [0.0] * 6
+            score[field] = np.nan
+            with pytest.raises(ValueError, match="nonfinite for nneval value"):
+                _row(np.zeros(HW + 1), score=tuple(score))
+
+
 # ---------------------------------------------------------------------------
 # GPU
 
@@ -203,6 +229,43 @@ def test_device_postprocess_matches_restatement(which, model_dir):
     d_bad = nn.DeviceBuffer.from_array(bad)
     with pytest.raises(nn.StringError, match="no legal move"):
         h.postprocess_device(n, d_raw.ptr, d_bad.ptr, d_info.ptr, d_temp.ptr, cp, d_post.ptr)
+
+
+@pytest.mark.gpu
+def test_device_postprocess_nonfinite_results_are_errors():
+    """The device kernel raises the reference's two errors for non-finite
+    results (nneval.cpp:1012-1016, 1167-1184) where the restatement does: a
+    NaN logit of a legal move, a NaN value logit. The same handle then
+    post-processes clean rows as before."""
+    lm = nn.LoadedModel(G170_MODEL)
+    dm = nn.DeviceModel(lm, use_fp16=False)
+    n = 4
+    h = nn.DeviceHandle(dm, n)
+    score_c = lm.info.num_score_value_channels
+    raw, legal, info, temp, flags = _random_rows(np.random.default_rng(11), n, score_c)
+    params = pp.PostProcessParams()
+    cp = nn.PostParams(params.output_scale_multiplier, params.score_mean_multiplier, params.score_stdev_multiplier,
+                       params.lead_multiplier, params.variance_time_multiplier, params.shortterm_value_error_multiplier,
+                       params.shortterm_score_error_multiplier)
+    d_legal = nn.DeviceBuffer.from_array(legal.astype(np.uint8))
+    d_info = nn.DeviceBuffer.from_array(info)
+    d_temp = nn.DeviceBuffer.from_array(temp)
+    d_post = nn.DeviceBuffer(n * (2 * HW + 10) * 4)
+
+    def run(rows):
+        d_raw = nn.DeviceBuffer.from_array(rows)
+        h.postprocess_device(n, d_raw.ptr, d_legal.ptr, d_info.ptr, d_temp.ptr, cp, d_post.ptr)
+        return d_post.to_array(np.float32, (n, 2 * HW + 10))
+
+    bad = raw.copy()
+    bad[2, np.flatnonzero(legal[2])[0]] = np.nan
+    with pytest.raises(nn.StringError, match="nonfinite for policy sum"):
+        run(bad)
+    bad = raw.copy()
+    bad[1, HW + 1] = np.nan
+    with pytest.raises(nn.StringError, match="nonfinite for nneval value"):
+        run(bad)
+    _check_rows(run(raw), raw, legal, temp, flags, score_c, lm.info.model_version, params)
 
 
 @pytest.mark.gpu
