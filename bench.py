@@ -244,40 +244,60 @@ def featurize_rate(batch, seconds=2.0):
     return out
 
 
-def featurize_serve_rate(lm, cfg, batch, rounds=30):
-    """Positions in, network outputs out: one thread featurizes the next batch
-    (kgn_featurize on BOX_CPU_SHARE - 1 threads) while another runs the
-    current one through getOutput (pinned staging, H2D, forward, D2H)."""
+def featurize_serve_rate(lm, cfg, batch, rounds=30, servers=2):
+    """Positions in, network outputs out: one thread featurizes batches
+    (kgn_featurize on BOX_CPU_SHARE - servers threads) into a queue, and
+    `servers` threads, each with its own handle on the device (as KataGo's
+    server threads per GPU), run them through getOutput (pinned staging, H2D,
+    forward, D2H), so one batch's host packing and copies overlap another's
+    forward."""
     import queue
     from katago_amd import nn
     pos = nn.Positions(_fixture_positions(batch))
     ctx = nn.ComputeContext(lm, 19, 19, use_fp16=cfg.fp16, auto_tune=False)
-    h = nn.ComputeHandle(ctx, max_batch=batch)
-    q = queue.Queue(maxsize=2)
-    h.get_output(*nn.featurize(pos, 19, 19))  # warm up (graph capture)
+    handles = [nn.ComputeHandle(ctx, max_batch=batch) for _ in range(servers)]
+    q = queue.Queue(maxsize=servers + 1)
+    first = nn.featurize(pos, 19, 19)
+    for h in handles:
+        h.get_output(*first)  # warm up (graph capture)
 
     def produce():
         for _ in range(rounds):
-            q.put(nn.featurize(pos, 19, 19, num_threads=max(1, BOX_CPU_SHARE - 1)))
-        q.put(None)
+            q.put(nn.featurize(pos, 19, 19, num_threads=max(1, BOX_CPU_SHARE - servers)))
+        for _ in range(servers):
+            q.put(None)
 
-    t = threading.Thread(target=produce)
+    done = [0] * servers
+    errors = []
+
+    def serve(i):
+        try:
+            while True:
+                item = q.get()
+                if item is None:
+                    break
+                handles[i].get_output(*item)
+                done[i] += batch
+        except Exception as e:  # re-raised below, after every thread ended
+            errors.append(e)
+            while q.get() is not None:  # let the producer finish
+                pass
+
+    threads = [threading.Thread(target=produce)] + [threading.Thread(target=serve, args=(i,)) for i in range(servers)]
     t0 = time.perf_counter()
-    t.start()
-    rows = 0
-    while True:
-        item = q.get()
-        if item is None:
-            break
-        h.get_output(*item)
-        rows += batch
-    t.join()
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
     secs = time.perf_counter() - t0
-    h.close()
+    for h in handles:
+        h.close()
     ctx.close()
-    return {"value": round(rows / secs, 1), "unit": "evals/s", "batches": rounds,
+    if errors:
+        raise errors[0]
+    return {"value": round(sum(done) / secs, 1), "unit": "evals/s", "batches": rounds, "server_threads": servers,
             "path": "positions -> kgn_featurize (host) -> getOutput (pinned staging, H2D, forward, D2H) -> rows, "
-                    "featurizing overlapped with the device"}
+                    "featurizing overlapped with the device, two server threads with a handle each"}
 
 
 def serve_rate(lm, cfg, batch, server_threads=2, rounds=40):
