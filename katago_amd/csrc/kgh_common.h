@@ -314,6 +314,7 @@ enum ConvVariant {
   CONV_ALLK1_32,
   CONV_DMA1_256_GLU,  // 1x1 fp16 DMA kernel, 384 x 256 tiles, gated (SwiGLU) epilogue only
   CONV_BOARD_HALF_64_T32,  // the half-board kernel with 32-row wave tiles (12 waves per workgroup)
+  CONV_BOARD_HALF_192,  // the half-board kernel with 192 output channels per tile (one workgroup per CU)
   CONV_VARIANT_COUNT
 };
 

@@ -2214,6 +2214,7 @@ bool variantFits(int v, int ky, int cinStride, int cinPad, int cout, BoardGeom g
       if(v == CONV_BOARD_128) return boardWindowFits(cinStride, cinPad, cout, 128, g, epi);
       if(v == CONV_BOARD_64 || v == CONV_BOARD_HALF_64 || v == CONV_BOARD_HALF_64_T32)
         return boardWindowFits(cinStride, cinPad, cout, 64, g, epi);
+      if(v == CONV_BOARD_HALF_192) return boardWindowFits(cinStride, cinPad, cout, 192, g, epi);
     }
     else {
       if(v == CONV_DMA1_192) return dma1x1Fits(cinStride, cinPad, cout, 192, g);
@@ -2264,6 +2265,7 @@ void launchVariant(int v, int ky, const T* x, int cinStride, int cinPad, int cou
       case CONV_BOARD_64: launchBoardWindow<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_HALF_64: launchBoardWindow<64, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_BOARD_HALF_64_T32: launchBoardWindow<64, 2, 32>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
+      case CONV_BOARD_HALF_192: launchBoardWindow<192, 2>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_ALLK1_64: launch1x1AllK<64>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_ALLK1_32: launch1x1AllK<32>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
       case CONV_DMA1_192: launch1x1Dma<192>(x, cinStride, cinPad, cout, w, g, epi, stream); return;
@@ -2317,7 +2319,8 @@ const char* convVariantName(int variant) {
   static const char* names[] = {"auto", "tw192", "tw128", "tw64", "tw8w192", "dma1x1_192", "dma1x1_128", "dma1x1_64",
                                 "tile192", "tile128", "tile96", "tile64", "tile32", "board192", "board128", "board64",
                                 "dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "boardhalf64", "allk1x1_64", "allk1x1_32",
-                                "dma1x1_256glu", "boardhalf64t32"};
+                                "dma1x1_256glu", "boardhalf64t32", "boardhalf192"};
+  static_assert(sizeof(names) / sizeof(names[0]) == CONV_VARIANT_COUNT, "a name per variant");
   return variant >= 0 && variant < CONV_VARIANT_COUNT ? names[variant] : "?";
 }
 

@@ -100,12 +100,16 @@ def test_every_kernel_variant_gives_identical_bits(model_dir, fp16):
             assert np.array_equal(out[k], ref[k]), (v, k)
 
 
-@pytest.mark.parametrize("variant", [16, 17, 18, 20, 21], ids=["dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "allk1x1_64", "allk1x1_32"])
-def test_half_height_1x1_variants_give_identical_bits_on_nbt(model_dir, variant):
-    """The 192-row 1x1 kernels and the whole-K small-batch 1x1 kernels on
-    C2's nested-bottleneck shapes, including the post 1x1 conv whose residual
-    is loaded into the accumulators (through the stage that shares the A
-    buffers in the 192-row kernel): bitwise the built-in outputs."""
+@pytest.mark.parametrize("variant", [16, 17, 18, 20, 21, 13, 15, 19, 23, 24],
+                         ids=["dma1x1h_192", "dma1x1h_128", "dma1x1h_64", "allk1x1_64", "allk1x1_32", "board192", "board64",
+                              "boardhalf64", "boardhalf64t32", "boardhalf192"])
+def test_variants_give_identical_bits_on_nbt(model_dir, variant):
+    """On C2's nested-bottleneck shapes (192-channel 3x3 convs, which the
+    b10c128 test above cannot pin to the 192-column board kernels): the
+    192-row and whole-K 1x1 kernels, including the post 1x1 conv whose
+    residual is loaded into the accumulators (through the stage that shares
+    the A buffers in the 192-row kernel), and the one-board 3x3 kernels on
+    whole and half boards: bitwise the built-in outputs."""
     cfg = modelgen.configs()[2]
     lm = nn.LoadedModel(modelgen.ensure_model(model_dir, cfg))
     n = 12  # batches of 8 boards or fewer are not tuned
