@@ -29,7 +29,8 @@ __device__ __forceinline__ float waveSum(float v) {
 // Sixteen lanes per row group, four groups per wave, RPG consecutive rows per
 // group: lane l of a row holds 16-byte channel groups l, l + 16, ... (NG of
 // them) in registers across both passes, with gamma/beta loaded before the
-// reduction and the activation fixed at compile time.
+// reduction and the activation fixed at compile time (the conv epilogues'
+// fast forms).
 template<typename T, int NG, int ACT, int RPG>
 __global__ __launch_bounds__(256) void rmsNormRowKernel(const T* __restrict__ x, int ldX, T* __restrict__ y, int ldY, int C,
                                                        const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
@@ -56,9 +57,11 @@ __global__ __launch_bounds__(256) void rmsNormRowKernel(const T* __restrict__ x,
     }
   }
   T v[RPG][NG][VEC];
+  float rowMask[RPG];  // loaded with the rows: no second round trip after the reduction
 #pragma unroll
   for(int rr = 0; rr < RPG; rr++) {
     const int r = min(row0 + rr, M - 1);  // rows past M are loaded, never stored
+    rowMask[rr] = mask[r];
     const T* xr = x + (size_t)r * ldX;
 #pragma unroll
     for(int i = 0; i < NG; i++) {
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(256) void rmsNormRowKernel(const T* __restrict__ x,
     for(int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
     const float inv = 1.0f / sqrtf(ss / (float)C + eps);
     if(!live) continue;
-    const bool on = mask[r] != 0.0f;
+    const bool on = rowMask[rr] != 0.0f;
     T* yr = y + (size_t)r * ldY;
 #pragma unroll
     for(int i = 0; i < NG; i++) {
@@ -95,7 +98,7 @@ __global__ __launch_bounds__(256) void rmsNormRowKernel(const T* __restrict__ x,
         for(int j = 0; j < VEC; j++) {
           const float g = PRELOAD ? gm[PRELOAD ? i : 0][j] : gamma[c + j];
           const float b = PRELOAD ? bt[PRELOAD ? i : 0][j] : (beta != nullptr ? beta[c + j] : 0.0f);
-          const float f = kgh_activate(kgh_to_float(v[rr][i][j]) * inv * g + b, ACT);
+          const float f = kgh_activate_fast(kgh_to_float(v[rr][i][j]) * inv * g + b, ACT);
           o[j] = kgh_from_float<T>(on ? f : 0.0f);
         }
         *(uint4*)(yr + c) = *(const uint4*)o;
@@ -166,7 +169,7 @@ __global__ void rmsNormApplyKernel(const T* __restrict__ x, int ldX, T* __restri
   *(uint4*)v = *(const uint4*)(x + (size_t)row * ldX + c);
 #pragma unroll
   for(int j = 0; j < VEC; j++) {
-    float f = kgh_activate(kgh_to_float(v[j]) * s * gamma[c + j] + beta[c + j], act);
+    float f = kgh_activate_fast(kgh_to_float(v[j]) * s * gamma[c + j] + beta[c + j], act);
     o[j] = kgh_from_float<T>(on ? f : 0.0f);
   }
   *(uint4*)(y + (size_t)row * ldY + c) = *(const uint4*)o;
