@@ -24,6 +24,13 @@
 // microseconds per position of KataGo's fillRowV7, of kgn_featurize over the
 // prebuilt positions in one single-threaded call with its ladder cache off
 // and on, and of positionFromHistory + kgn_featurize one position per call.
+// and, for a position reached by a given move sequence (the canary
+// positions of testnnevalcanary.cpp):
+//   moves <name> <xSize> <ySize> <nnXLen> <nnYLen> <rules> <komi> <numMoves> {<b|w> <x> <y>}
+// (x = y = -1 for a pass) which plays the moves with KataGo's BoardHistory,
+// sets the komi (as BoardHistory::setKomi after the setup), checks this
+// repository's featurizer against fillRowV7 on the position (a "compare"
+// line) and emits the position as a "case" would.
 // Output on stdout: one JSON object per position and line.
 #include <chrono>
 #include <cstdio>
@@ -395,6 +402,31 @@ int main() {
       }
       std::cout << "{\"summary\":\"" << name << "\",\"positions\":" << positions << ",\"mismatched\":" << mismatched
                 << ",\"first_diff\":\"" << firstDiff << "\"}" << std::endl;
+    }
+    else if(word == "moves") {
+      string name, rulesS;
+      int xs, ys, nnX, nnY, n;
+      float komi;
+      std::cin >> name >> xs >> ys >> nnX >> nnY >> rulesS >> komi >> n;
+      Board board(xs, ys);
+      Player pla = P_BLACK;
+      BoardHistory hist(board, pla, rulesNamed(rulesS), 0);
+      for(int m = 0; m < n; m++) {
+        string c;
+        int x, y;
+        std::cin >> c >> x >> y;
+        const Player mover = c == "w" ? P_WHITE : P_BLACK;
+        const Loc loc = x < 0 ? Board::PASS_LOC : Location::getLoc(x, y, xs);
+        if(!hist.isLegal(board, loc, mover)) throw StringError(name + ": illegal move " + std::to_string(m));
+        hist.makeBoardMoveAssumeLegal(board, loc, mover, nullptr);
+        pla = getOpp(mover);
+      }
+      hist.setKomi(komi);
+      string firstDiff;
+      const int d = compareOne(name, board, hist, pla, nnX, nnY, false, firstDiff, 1);
+      std::cout << "{\"compare\":\"" << name << "\",\"differing\":" << d << ",\"first_diff\":\"" << firstDiff << "\"}"
+                << std::endl;
+      emit(name, board, hist, pla, nnX, nnY, 7);
     }
     else if(word == "time") {
       string name, rulesS;
