@@ -261,14 +261,18 @@ def featurize_serve_rate(lm, cfg, batch, rounds=30, servers=2):
     for h in handles:
         h.get_output(*first)  # warm up (graph capture)
 
-    def produce():
-        for _ in range(rounds):
-            q.put(nn.featurize(pos, 19, 19, num_threads=max(1, BOX_CPU_SHARE - servers)))
-        for _ in range(servers):
-            q.put(None)
-
     done = [0] * servers
     errors = []
+
+    def produce():
+        try:
+            for _ in range(rounds):
+                q.put(nn.featurize(pos, 19, 19, num_threads=max(1, BOX_CPU_SHARE - servers)))
+        except Exception as e:  # re-raised below; the servers still get their end marks
+            errors.append(e)
+        finally:
+            for _ in range(servers):
+                q.put(None)
 
     def serve(i):
         try:
