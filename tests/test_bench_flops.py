@@ -48,3 +48,13 @@ def test_c4_transformer_flops(model_dir):
     projections = 12 * 2 * HW * (384 * 3 * 384 + 384 * 384 + 384 * 2 * 1024 + 1024 * 384)
     attention = 12 * 6 * 2 * HW * HW * (64 + 64)
     assert projections + attention <= f1 + other <= (projections + attention) * 1.01
+
+
+def test_roofline_traffic_comes_from_the_committed_counter_profile():
+    """bench.py's roofline.traffic is the FETCH_SIZE + WRITE_SIZE mean per 3x3
+    launch from profiles/: within 1.0-1.3x of the ~106 MB of algorithmic
+    bytes a C2 trunk conv moves on average (input, residual where there is
+    one, one or two outputs)."""
+    traffic = _bench().measured_traffic()
+    algorithmic = (36 * (4 * 35.5e6) + 36 * (2 * 35.5e6)) / 72
+    assert traffic is not None and 1.0 * algorithmic <= traffic <= 1.3 * algorithmic
