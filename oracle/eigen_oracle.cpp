@@ -20,6 +20,8 @@
 // How each part is pinned is listed in eigen_oracle.h.
 #include "eigen_oracle.h"
 
+#include <immintrin.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -39,16 +41,52 @@ using std::vector;
 namespace OracleEigen {
 
 // ---------------------------------------------------------------------------
-// Dense row-major GEMM: C[M,N] (+)= A[M,K] * B[K,N]. Four A rows at a time so
-// that the inner loop over N is a contiguous fused multiply-add the compiler
-// vectorizes.
+// Dense row-major GEMM: C[M,N] (+)= A[M,K] * B[K,N]. Every output is a chain
+// c = fma(a[k], b[k][j], c) over k in order, whichever path computes it: a
+// register-blocked AVX2 kernel (six rows x sixteen columns of C held in
+// registers across a block of k) for the bulk, four A rows at a time with a
+// contiguous inner loop over N for the edges.
 static void sgemm(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C, int ldc, bool accumulate) {
   if(!accumulate)
     for(int i = 0; i < M; i++) std::fill(C + (size_t)i * ldc, C + (size_t)i * ldc + N, 0.0f);
   const int KB = 256;
+  const int N16 = N / 16 * 16;
+  const int M6 = M / 6 * 6;
   for(int k0 = 0; k0 < K; k0 += KB) {
     int k1 = std::min(K, k0 + KB);
-    int i = 0;
+    for(int i = 0; i < M6; i += 6) {
+      for(int j = 0; j < N16; j += 16) {
+        __m256 c[6][2];
+        for(int r = 0; r < 6; r++) {
+          c[r][0] = _mm256_loadu_ps(C + (size_t)(i + r) * ldc + j);
+          c[r][1] = _mm256_loadu_ps(C + (size_t)(i + r) * ldc + j + 8);
+        }
+        for(int k = k0; k < k1; k++) {
+          const float* b = B + (size_t)k * ldb + j;
+          const __m256 b0 = _mm256_loadu_ps(b), b1 = _mm256_loadu_ps(b + 8);
+          for(int r = 0; r < 6; r++) {
+            const __m256 a = _mm256_broadcast_ss(A + (size_t)(i + r) * lda + k);
+            c[r][0] = _mm256_fmadd_ps(a, b0, c[r][0]);
+            c[r][1] = _mm256_fmadd_ps(a, b1, c[r][1]);
+          }
+        }
+        for(int r = 0; r < 6; r++) {
+          _mm256_storeu_ps(C + (size_t)(i + r) * ldc + j, c[r][0]);
+          _mm256_storeu_ps(C + (size_t)(i + r) * ldc + j + 8, c[r][1]);
+        }
+      }
+      // Columns past the last block of sixteen.
+      for(int r = 0; r < 6; r++) {
+        float* cr = C + (size_t)(i + r) * ldc;
+        const float* ar = A + (size_t)(i + r) * lda;
+        for(int k = k0; k < k1; k++) {
+          const float* b = B + (size_t)k * ldb;
+          const float x = ar[k];
+          for(int j = N16; j < N; j++) cr[j] = std::fma(x, b[j], cr[j]);
+        }
+      }
+    }
+    int i = M6;
     for(; i + 4 <= M; i += 4) {
       float* c0 = C + (size_t)i * ldc;
       float* c1 = c0 + ldc;
@@ -63,10 +101,10 @@ static void sgemm(int M, int N, int K, const float* A, int lda, const float* B, 
         float x0 = a0[k], x1 = a1[k], x2 = a2[k], x3 = a3[k];
         for(int j = 0; j < N; j++) {
           float bj = b[j];
-          c0[j] += x0 * bj;
-          c1[j] += x1 * bj;
-          c2[j] += x2 * bj;
-          c3[j] += x3 * bj;
+          c0[j] = std::fma(x0, bj, c0[j]);
+          c1[j] = std::fma(x1, bj, c1[j]);
+          c2[j] = std::fma(x2, bj, c2[j]);
+          c3[j] = std::fma(x3, bj, c3[j]);
         }
       }
     }
@@ -76,7 +114,7 @@ static void sgemm(int M, int N, int K, const float* A, int lda, const float* B, 
       for(int k = k0; k < k1; k++) {
         const float* b = B + (size_t)k * ldb;
         float x0 = a0[k];
-        for(int j = 0; j < N; j++) c0[j] += x0 * b[j];
+        for(int j = 0; j < N; j++) c0[j] = std::fma(x0, b[j], c0[j]);
       }
     }
   }
