@@ -142,3 +142,21 @@ def test_device_passes_canaries(net, fp16):
         fails += [f"symmetry {sym[r]}: {f}"
                   for f in failed_checks(CANARIES[i], out["policy"][r], out["values"][r], net in POLICY_ONLY)]
     assert not fails, "\n".join(fails)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("net", ["b4c256h4nbttflrs", "g170-b6c96"])
+def test_low_latency_mode_passes_canaries(net):
+    """The handle's low-latency mode (split-K 3x3 convs, handles of at most 16
+    rows), one position per call as a single-threaded search evaluates:
+    every canary assertion holds under every symmetry."""
+    lm = nn.LoadedModel(os.path.join(GOLDEN, NETS[net]))
+    h = nn.ComputeHandle(nn.ComputeContext(lm, NNX, NNY, use_fp16=True, auto_tune=False, low_latency=True), max_batch=1)
+    sp, gl = rows()
+    legal, info = post_inputs()
+    fails = []
+    for i, c in enumerate(CANARIES):
+        for s in range(8):
+            out = h.get_output_post(sp[i:i + 1], gl[i:i + 1], legal[i:i + 1], info[i:i + 1], symmetry=np.array([s], np.int32))
+            fails += [f"symmetry {s}: {f}" for f in failed_checks(c, out["policy"][0], out["values"][0], net in POLICY_ONLY)]
+    assert not fails, "\n".join(fails)
