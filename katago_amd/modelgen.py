@@ -126,6 +126,10 @@ class Arch:
     residual_gain: float = 1.0
     num_input: int = 22
     num_global: int = 19
+    # SGF metadata encoder (version >= 15; 1 = the 192 metadata channels of
+    # sgfmetadata.cpp): written with random weights for the tests of its
+    # rejection, not evaluated.
+    meta_encoder_version: int = 0
 
 
 def _he(rng: SplitMix64, shape, fan_in: int, gain: float = 1.0) -> np.ndarray:
@@ -281,7 +285,8 @@ class _Builder:
         for v in (20.0, 20.0, 20.0, 20.0, 40.0, 0.25, 30.0):  # post-process multipliers (v >= 13)
             w.line(v)
         if a.version >= 15:
-            for _ in range(8):  # metaEncoderVersion 0 and seven reserved zeros
+            w.line(a.meta_encoder_version)
+            for _ in range(7):  # seven reserved zeros
                 w.line(0)
         # trunk
         w.line("trunk")
@@ -297,6 +302,18 @@ class _Builder:
                 w.line(0)
         self.conv("model.conv_spatial", 3, 3, a.num_input, a.trunk_c)
         self.matmul("model.linear_global", a.num_global, a.trunk_c)
+        if a.meta_encoder_version > 0:
+            # SGFMetadataEncoderDesc (desc.cpp): name, input channels, then
+            # mul, bias, act, mul, bias, act, mul to the trunk width.
+            w.line("model.metadata_encoder")
+            w.line(192)
+            self.matmul("model.metadata_encoder.mul1", 192, 32)
+            self.matbias("model.metadata_encoder.bias1", 32)
+            self.act("model.metadata_encoder.act1")
+            self.matmul("model.metadata_encoder.mul2", 32, 32)
+            self.matbias("model.metadata_encoder.bias2", 32)
+            self.act("model.metadata_encoder.act2")
+            self.matmul("model.metadata_encoder.mul3", 32, a.trunk_c)
         for i, kind in enumerate(a.blocks):
             name = f"model.blocks.{i}"
             if kind == "regular":

@@ -191,3 +191,18 @@ def test_context_config_text_rejects_a_line_without_equals(model_dir):
     ptr = lib.kgn_create_context_cfg(lm._ptr, 19, 19, 1, b"", b"# tuning\n\nhipAutoTune = false\nhipLowLatency\n", err, len(err))
     assert not ptr
     assert "without '='" in err.value.decode() and "hipLowLatency" in err.value.decode()
+
+
+def test_metadata_encoder_models_parse_and_are_rejected_at_handle_creation(tmp_path):
+    """A version-15 net with an SGF metadata encoder (metaEncoderVersion 1,
+    the 192 metadata channels; SGFMetadataEncoderDesc, desc.cpp) parses, and
+    createComputeHandle rejects it with the documented StringError, on the
+    host before any device work (the reference's CUDA backend evaluates such
+    nets; none is among the benchmark configs)."""
+    import dataclasses
+    arch = dataclasses.replace(modelgen.b6c96(), version=15, meta_encoder_version=1, name="b6c96-meta")
+    lm = nn.LoadedModel(modelgen.write_model(arch, 3, str(tmp_path / "meta.bin.gz")))
+    assert lm.info.num_input_meta_channels == 192 and lm.info.model_version == 15
+    ctx = nn.ComputeContext(lm, 19, 19, use_fp16=True)
+    with pytest.raises(nn.StringError, match="SGF metadata encoder"):
+        nn.ComputeHandle(ctx, max_batch=2)
