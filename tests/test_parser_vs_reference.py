@@ -119,3 +119,14 @@ def test_parser_matches_reference_on_generated_models(dumper, model_dir, cfg_ind
     transformer) as this repository's writer produces them: the reference
     parser reads them to the same weights."""
     assert _compare(dumper, modelgen.ensure_model(model_dir, modelgen.configs()[cfg_index])) > 10
+
+
+def test_reference_parser_reads_the_generated_metadata_encoder_net(dumper, tmp_path):
+    """The writer's SGF metadata encoder (the net the host rejects at handle
+    creation, test_host.py) is in the reference's grammar: KataGo's own
+    desc.cpp loads the file, with its 192 metadata input channels."""
+    import dataclasses
+    arch = dataclasses.replace(modelgen.b6c96(), version=15, meta_encoder_version=1, name="b6c96-meta")
+    path = modelgen.write_model(arch, 3, str(tmp_path / "meta.bin.gz"))
+    out = subprocess.run([dumper, path], capture_output=True, text=True, check=True).stdout
+    assert out.splitlines()[0].startswith("model 15 22 19 ")
