@@ -124,7 +124,8 @@ def test_parser_matches_reference_on_generated_models(dumper, model_dir, cfg_ind
 def test_reference_parser_reads_the_generated_metadata_encoder_net(dumper, tmp_path):
     """The writer's SGF metadata encoder (the net the host rejects at handle
     creation, test_host.py) is in the reference's grammar: KataGo's own
-    desc.cpp loads the file, with its 192 metadata input channels."""
+    desc.cpp loads the file (its encoder's input width is checked there
+    against the 192 metadata channels)."""
     import dataclasses
     arch = dataclasses.replace(modelgen.b6c96(), version=15, meta_encoder_version=1, name="b6c96-meta")
     path = modelgen.write_model(arch, 3, str(tmp_path / "meta.bin.gz"))
